@@ -1,0 +1,191 @@
+"""Benchmark of the MI355X quantized preshuffle GEMM (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--workload C2] [--secondary T] [--no-cpu]
+
+A step is one GEMM launch over the workload's operands, already resident in HBM.  The
+headline workload is C2 (FP8 decode 16x28672x8192, HBM-bound): ``value`` is achieved GB/s
+of algorithmic traffic (A + B + C + scales).  The FP8 8192^3 workload (MFMA-bound) is
+measured in the same run and reported under ``secondary`` in TFLOP/s.  Kernel time comes
+from HIP events recorded on the launch stream around the K timed launches; B (and A) are
+rotated over several copies whose total exceeds the 256 MB last-level cache, so every
+launch streams its operands from HBM.  The CPU baseline times the oracle's
+dequantize-then-matmul restatement on the host cores for a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+from flydsl_amd import _lib, workloads
+from flydsl_amd.kernels.blockscale_preshuffle_gemm import compile_blockscale_preshuffle_gemm
+from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
+
+METRIC = "FP8 GEMM TFLOP/s + % MFMA peak (large M); achieved HBM GB/s (small M)"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"fp8": 5000.0, "fp8_block": 5000.0, "int8": 5000.0, "int4": 5000.0}
+LLC_BYTES = 256 << 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Runner:
+    """Device operands (rotated copies) and a launch closure for one workload."""
+
+    def __init__(self, w: workloads.Workload, dev, min_rotation_bytes=3 * LLC_BYTES):
+        self.w = w
+        ops = workloads.make_operands(w)
+        per_call = ops["a"].numel() + ops["b_dev"].numel()
+        copies = max(1, min(8, -(-min_rotation_bytes // per_call)))
+        self.copies = copies
+        self.a = [ops["a"].to(dev).view(torch.int8).view(-1) for _ in range(copies)]
+        self.b = [ops["b_dev"].to(dev).view(torch.int8).view(-1) for _ in range(copies)]
+        sa = ops["sa_t"] if w.kind == "fp8_block" else ops["sa"]
+        self.sa = sa.to(dev).contiguous().view(-1)
+        self.sb = ops["sb"].to(dev).contiguous().view(-1)
+        self.c = torch.empty(w.M, w.N, dtype=torch.bfloat16, device=dev)
+        if w.kind == "fp8_block":
+            self.fn = compile_blockscale_preshuffle_gemm(M=w.M, N=w.N, K=w.K, tile_m=64, tile_n=128, tile_k=128,
+                                                         out_dtype="bf16")
+        else:
+            self.fn = compile_preshuffle_gemm_a8(M=w.M, N=w.N, K=w.K, tile_m=128, tile_n=128, tile_k=128,
+                                                 in_dtype=w.kind, out_dtype="bf16")
+        self.variant = _lib.variants()[_lib.load().flygemm_select_variant(
+            w.M, w.N, w.K, _lib.FLYGEMM_IN.get(w.kind, 0), int(w.kind == "fp8_block"))]
+        del ops
+
+    def launch(self, i, stream):
+        j = i % self.copies
+        self.fn(self.c.view(-1), self.a[j], self.b[j], self.sa, self.sb, self.w.M, self.w.N, stream)
+
+    def time(self, steps, warmup):
+        stream = torch.cuda.current_stream()
+        for i in range(warmup):
+            self.launch(i, stream)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        for i in range(steps):
+            self.launch(i, stream)
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = start.elapsed_time(end)
+        return ms / steps, wall
+
+
+def roofline(w: workloads.Workload, ms_per_launch: float, bound: str, traffic=None):
+    if bound == "hbm":
+        achieved = w.bytes / (ms_per_launch * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    achieved = w.flops / (ms_per_launch * 1e-3) / 1e12
+    peak = MFMA_PEAK_TFLOPS[w.kind]
+    return {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def cpu_baseline(w: workloads.Workload, budget_s: float = 12.0):
+    """Time the oracle's dequantize-then-matmul (numpy, float32, all host cores) on rows of
+    the workload; report GB/s over the same algorithmic bytes per full call."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import gemm as og
+
+    cores = len(os.sched_getaffinity(0))
+    ops = workloads.make_operands(w)
+    a = ops["a"].view(torch.uint8).numpy() if ops["a"].dtype != torch.int8 else ops["a"].numpy()
+    b = ops["b"].view(torch.uint8).numpy() if ops["b"].dtype != torch.int8 else ops["b"].numpy()
+    sa, sb = ops["sa"].numpy().reshape(-1), ops["sb"].numpy().reshape(-1)
+    kind = "fp8" if w.kind in ("fp8", "fp8_block") else "int8"
+    with threadpool_limits(limits=cores):
+        og.run_torch(a, b[:256], sa, sb[:256], kind)  # warm-up
+        times = []
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < budget_s and len(times) < 5:
+            t0 = time.perf_counter()
+            og.run_torch(a, b, sa, sb, kind)
+            times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    return {"value": round(w.bytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full {w.name} call ({w.M}x{w.N}x{w.K}), median of {len(times)}, "
+                      f"oracle.gemm.run_torch float32 numpy/BLAS; {w.flops / t / 1e12:.4f} TFLOP/s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="C2")
+    ap.add_argument("--secondary", default="T", help="extra MFMA-bound workload ('' to skip)")
+    ap.add_argument("--all", action="store_true", help="also time every configuration")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
+              "multi-GPU path: run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    _lib.load()
+
+    w = workloads.WORKLOADS[args.workload]
+    log(f"[bench] preparing {w.name} {w.kind} {w.M}x{w.N}x{w.K}")
+    r = Runner(w, dev)
+    log(f"[bench] timing {w.name} variant={r.variant} copies={r.copies}")
+    ms, wall = r.time(args.steps, args.warmup)
+    bound = "hbm" if w.name in ("C1", "C2") else "mfma"
+    gbs = w.bytes * args.steps / (ms * args.steps * 1e-3) / 1e9
+    result = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8" if "fp8" in w.kind else ("int8" if w.kind == "int8" else "int4xint8"),
+        "data": "synthetic (seeded N(0,1), quantized per BASELINE)",
+        "config": {"workload": f"{w.name}: {w.note} {w.M}x{w.N}x{w.K} seed {w.seed}", "M": w.M, "N": w.N,
+                   "K": w.K, "kernel": r.variant, "wall_s": round(wall, 4)},
+        "roofline": roofline(w, ms, "hbm"),
+    }
+    if bound == "mfma":
+        result["roofline_mfma"] = roofline(w, ms, "mfma")
+    del r
+    torch.cuda.empty_cache()
+
+    extra = []
+    if args.secondary:
+        extra.append(args.secondary)
+    if args.all:
+        extra += [n for n in workloads.WORKLOADS if n not in extra and n != args.workload]
+    sec = {}
+    for name in extra:
+        w2 = workloads.WORKLOADS[name]
+        log(f"[bench] preparing {name} {w2.kind} {w2.M}x{w2.N}x{w2.K}")
+        r2 = Runner(w2, dev)
+        log(f"[bench] timing {name} variant={r2.variant}")
+        ms2, _ = r2.time(max(5, args.steps // 2), max(2, args.warmup // 2))
+        b2 = "hbm" if name in ("C1", "C2") else "mfma"
+        sec[name] = {"ms": round(ms2, 5), "TFLOP/s": round(w2.flops / ms2 / 1e9, 1),
+                     "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
+                     "roofline": roofline(w2, ms2, b2)}
+        del r2
+        torch.cuda.empty_cache()
+    if sec:
+        result["secondary"] = sec
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,52 @@
+"""Build the gfx950 HIP library in-tree: ``flydsl_amd/_flygemm.so``.
+
+``python -m flydsl_amd.build`` (or ``__graft_entry__.build()``) always recompiles.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(PKG_DIR, "csrc", "flygemm.hip")
+OUT = os.path.join(PKG_DIR, "_flygemm.so")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # no packed-fp32 VALU instructions (v_pk_*_f32) in device code: some of their forms
+    # have produced silently wrong results on MI355X
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the epilogue rounds (acc * sa) * sb to fp32 before the output cast, as the
+    # reference does; contraction would fuse the multiply into the cast (one rounding)
+    "-ffp-contract=off",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found: the ROCm toolchain is required to build flydsl_amd")
+    return path
+
+
+def build(verbose: bool = False) -> str:
+    tmp = OUT + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, SRC]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,195 @@
+// C-ABI of the gfx950 quantized preshuffle GEMM library (declarations: include/flygemm.h).
+//
+// Every entry point validates its arguments on the host, picks a kernel variant (or uses
+// the one the caller names), launches asynchronously on the caller's stream and returns 0
+// or a nonzero error code; the message of the last failure on the calling thread is
+// returned by flygemm_last_error().  Nothing here allocates device memory or synchronizes.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/flygemm.h"
+#include "gemm_decode.h"
+#include "gemm_main.h"
+
+using namespace flygemm;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+typedef void (*KernelFn)(GemmArgs);
+
+// ---- variant table -------------------------------------------------------------------
+enum Family { FAM_MAIN = 0, FAM_DECODE = 1 };
+
+struct Shape {
+  const char* name;
+  int family;
+  int bm, bn, threads;  // main: workgroup tile; decode: bm = 16*MR rows, bn = 16*NBW cols
+};
+
+#define MAIN_SHAPES(X)        \
+  X(256, 256, 2, 4)           \
+  X(128, 256, 2, 4)           \
+  X(128, 128, 2, 2)           \
+  X(64, 128, 1, 4)
+
+#define DECODE_SHAPES(X) \
+  X(1, 1, 4, 4)          \
+  X(2, 1, 4, 2)          \
+  X(4, 1, 4, 2)
+
+const Shape kShapes[] = {
+#define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64},
+    MAIN_SHAPES(MS)
+#undef MS
+#define DS(MR, NBW, NW, U) {"decode_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64},
+        DECODE_SHAPES(DS)
+#undef DS
+};
+constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+
+// One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
+template <int KIND, int EPI, bool BF16>
+struct KernelRow {
+  static const KernelFn* get() {
+    static const KernelFn fns[] = {
+#define MS(BM, BN, WM, WN) gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16>,
+        MAIN_SHAPES(MS)
+#undef MS
+#define DS(MR, NBW, NW, U) gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI, BF16>,
+            DECODE_SHAPES(DS)
+#undef DS
+    };
+    static_assert(sizeof(fns) / sizeof(fns[0]) == kNumShapes, "variant table mismatch");
+    return fns;
+  }
+};
+
+const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
+  const bool bf16 = out_dtype == FLYGEMM_OUT_BF16;
+  if (epi == EPI_ROWCOL) {
+    if (kind == KIND_FP8) return bf16 ? KernelRow<KIND_FP8, EPI_ROWCOL, true>::get() : KernelRow<KIND_FP8, EPI_ROWCOL, false>::get();
+    if (kind == KIND_INT8) return bf16 ? KernelRow<KIND_INT8, EPI_ROWCOL, true>::get() : KernelRow<KIND_INT8, EPI_ROWCOL, false>::get();
+    if (kind == KIND_INT4) return bf16 ? KernelRow<KIND_INT4, EPI_ROWCOL, true>::get() : KernelRow<KIND_INT4, EPI_ROWCOL, false>::get();
+  } else if (epi == EPI_BLOCK) {
+    if (kind == KIND_FP8) return bf16 ? KernelRow<KIND_FP8, EPI_BLOCK, true>::get() : KernelRow<KIND_FP8, EPI_BLOCK, false>::get();
+  } else if (epi == EPI_RAW) {
+    if (kind == KIND_FP8) return KernelRow<KIND_FP8, EPI_RAW, true>::get();
+    if (kind == KIND_INT8) return KernelRow<KIND_INT8, EPI_RAW, true>::get();
+    if (kind == KIND_INT4) return KernelRow<KIND_INT4, EPI_RAW, true>::get();
+  }
+  return nullptr;
+}
+
+int select_variant(int M, int N, int K, int kind, int epi) {
+  (void)K;
+  (void)kind;
+  (void)epi;
+  if (M <= 16) return 4;
+  if (M <= 32) return 5;
+  if (M <= 64) return 6;
+  // main family: largest tile that still gives every CU work
+  for (int v = 0; v < 4; ++v) {
+    const long wg = (long)((M + kShapes[v].bm - 1) / kShapes[v].bm) * ((N + kShapes[v].bn - 1) / kShapes[v].bn);
+    if (wg >= 240) return v;
+  }
+  return 3;
+}
+
+int check_common(const void* c, const void* a, const void* b, int M, int N, int K, int variant) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(hipErrorInvalidValue, "invalid sizes M=%d N=%d K=%d", M, N, K);
+  if (N % 16 != 0) return fail(hipErrorInvalidValue, "N=%d must be a multiple of 16 (preshuffle block)", N);
+  if (K % 128 != 0) return fail(hipErrorInvalidValue, "K=%d must be a multiple of 128 (K tile)", K);
+  if ((long)M * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N >= (1L << 31))
+    return fail(hipErrorInvalidValue, "operand too large for 32-bit element offsets (M=%d N=%d K=%d)", M, N, K);
+  if (M > 0 && (!c || !a || !b)) return fail(hipErrorInvalidValue, "null tensor pointer");
+  if (variant < -1 || variant >= kNumShapes) return fail(hipErrorInvalidValue, "unknown variant %d", variant);
+  return 0;
+}
+
+int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, hipStream_t stream) {
+  if (args.M == 0) return 0;
+  const int v = variant >= 0 ? variant : select_variant(args.M, args.N, args.K, kind, epi);
+  const Shape& s = kShapes[v];
+  if (s.family == FAM_DECODE && args.M > s.bm)
+    return fail(hipErrorInvalidValue, "variant %s handles M <= %d, got M=%d", s.name, s.bm, args.M);
+  const KernelFn* row = kernel_row(kind, epi, out_dtype);
+  if (!row) return fail(hipErrorInvalidValue, "unsupported combination kind=%d epilogue=%d", kind, epi);
+  dim3 grid;
+  if (s.family == FAM_MAIN) {
+    grid = dim3(((args.M + s.bm - 1) / s.bm) * ((args.N + s.bn - 1) / s.bn));
+  } else {
+    grid = dim3((args.N + s.bn - 1) / s.bn);
+  }
+  hipLaunchKernelGGL(row[v], grid, dim3(s.threads), 0, stream, args);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(e, "launch of %s failed: %s", s.name, hipGetErrorString(e));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int flygemm_preshuffle(void* c, const void* a, const void* b, const float* scale_a, const float* scale_b,
+                       int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t out_dtype,
+                       int32_t variant, void* stream) {
+  int rc = check_common(c, a, b, M, N, K, variant);
+  if (rc) return rc;
+  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_INT4)
+    return fail(hipErrorInvalidValue, "in_dtype %d not supported", in_dtype);
+  if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16)
+    return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
+  if (M > 0 && (!scale_a || !scale_b)) return fail(hipErrorInvalidValue, "null scale pointer");
+  GemmArgs args{c, (const uint8_t*)a, (const uint8_t*)b, scale_a, scale_b, M, N, K};
+  return launch(in_dtype, EPI_ROWCOL, out_dtype, variant, args, (hipStream_t)stream);
+}
+
+int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_scale_t, const float* w_scale,
+                       int32_t M, int32_t N, int32_t K, int32_t scale_block_k, int32_t out_dtype,
+                       int32_t variant, void* stream) {
+  int rc = check_common(c, a, b, M, N, K, variant);
+  if (rc) return rc;
+  if (scale_block_k != 128) return fail(hipErrorInvalidValue, "scale_block_k=%d: only 128 is supported", scale_block_k);
+  if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16)
+    return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
+  if (M > 0 && (!x_scale_t || !w_scale)) return fail(hipErrorInvalidValue, "null scale pointer");
+  GemmArgs args{c, (const uint8_t*)a, (const uint8_t*)b, x_scale_t, w_scale, M, N, K};
+  return launch(KIND_FP8, EPI_BLOCK, out_dtype, variant, args, (hipStream_t)stream);
+}
+
+int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int32_t N, int32_t K,
+                         int32_t in_dtype, int32_t variant, void* stream) {
+  int rc = check_common(acc, a, b, M, N, K, variant);
+  if (rc) return rc;
+  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_INT4)
+    return fail(hipErrorInvalidValue, "in_dtype %d not supported", in_dtype);
+  GemmArgs args{acc, (const uint8_t*)a, (const uint8_t*)b, nullptr, nullptr, M, N, K};
+  return launch(in_dtype, EPI_RAW, FLYGEMM_OUT_BF16, variant, args, (hipStream_t)stream);
+}
+
+int32_t flygemm_num_variants(void) { return kNumShapes; }
+
+const char* flygemm_variant_name(int32_t v) {
+  if (v < 0 || v >= kNumShapes) return nullptr;
+  return kShapes[v].name;
+}
+
+int32_t flygemm_select_variant(int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t blockscale) {
+  return select_variant(M, N, K, in_dtype, blockscale ? EPI_BLOCK : EPI_ROWCOL);
+}
+
+const char* flygemm_last_error(void) { return g_err; }
+
+}  // extern "C"

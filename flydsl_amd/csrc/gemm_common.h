@@ -1,0 +1,92 @@
+// Shared device helpers for the gfx950 quantized preshuffle GEMM kernels.
+//
+// Operand conventions (all kernels):
+//   A    row-major [M][K] bytes (fp8 e4m3fn or int8).
+//   B    preshuffled bytes: B[n][k] lives at (n/16)*16*K + (k/16)*256 + (n%16)*16 + (k%16)
+//        (reference tests/utils.py:76-96 with layout=(16,16); device view
+//        kernels/preshuffle_gemm.py:226-241).  INT4 B is that buffer with every 8 bytes
+//        packed into 4 (test_preshuffle_gemm.py:165-174): B4[n][k] lives in the byte at
+//        (n/16)*8*K + (k/16)*128 + (n%16)*8 + ((k%16)/8)*4 + (k%4), low nibble when
+//        (k%8) < 4, high nibble otherwise.
+//   K tile = 128 elements.  Within a tile, the 16-byte K chunks c = 0..7 are handed to the
+//   MFMA so that lane l carries chunks (l/16) and (l/16)+4 of its row (A) / column (B).
+//   A and B use the same chunk assignment, so the dot product over K is exact regardless
+//   of how the hardware orders K inside one instruction.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <type_traits>
+
+namespace flygemm {
+
+typedef int   i32x2 __attribute__((ext_vector_type(2)));
+typedef int   i32x4 __attribute__((ext_vector_type(4)));
+typedef int   i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2 };
+enum Epi : int {
+  EPI_ROWCOL = 0,    // out = (acc * sa[m]) * sb[n]            (per-token / per-channel)
+  EPI_BLOCK = 1,     // acc += mfma_block * (sa[kb][m] * sb[n/128][kb]) per 128-K block
+  EPI_RAW = 2,       // raw accumulators: int32 (int8/int4) or fp32 (fp8), no scaling
+};
+
+constexpr int KT = 128;  // K elements per tile == blockscale K granularity
+
+// E8M0 1.0 in all four byte lanes: the block-scale operand of the gfx950 scaled MFMA
+// set to unity, so the instruction is the plain fp8 x fp8 -> fp32 product.
+constexpr int kScaleOne = 0x7F7F7F7F;
+
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kScaleOne, 0, kScaleOne);
+}
+
+__device__ __forceinline__ i32x4 mfma_i8(const i32x4& a, const i32x4& b, const i32x4& c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// 4 packed int4 bytes (8 nibbles, little-endian) -> 8 sign-extended int8 in two dwords:
+// the low nibbles of bytes 0..3 first, then the high nibbles
+// (kernels/mfma_preshuffle_pipeline.py:277-291).
+__device__ __forceinline__ void unpack_int4x8(uint32_t p, int& lo, int& hi) {
+  uint32_t e = (p & 0x0F0F0F0Fu) | ((p & 0x08080808u) * 0x1Eu);
+  uint32_t t = p >> 4;
+  uint32_t o = (t & 0x0F0F0F0Fu) | ((t & 0x08080808u) * 0x1Eu);
+  lo = (int)e;
+  hi = (int)o;
+}
+
+__device__ __forceinline__ i32x4 unpack_int4x16(i32x2 p) {
+  int a, b, c, d;
+  unpack_int4x8((uint32_t)p.x, a, b);
+  unpack_int4x8((uint32_t)p.y, c, d);
+  return i32x4{a, b, c, d};
+}
+
+template <bool BF16>
+struct OutT;
+template <>
+struct OutT<true> { typedef __bf16 type; };
+template <>
+struct OutT<false> { typedef _Float16 type; };
+
+// fp32 -> output type, round to nearest even.  The value is pinned in a register first:
+// otherwise the compiler folds the epilogue's last multiply into the fp16 conversion
+// (v_fma_mixlo_f16, one rounding), while the reference rounds the product to fp32 and
+// then to fp16.
+template <bool BF16>
+__device__ __forceinline__ typename OutT<BF16>::type cvt_out(float v) {
+  asm volatile("" : "+v"(v));
+  return static_cast<typename OutT<BF16>::type>(v);
+}
+
+struct GemmArgs {
+  void* c;            // output [M][N] bf16/fp16, or int32/fp32 for EPI_RAW
+  const uint8_t* a;   // [M][K]
+  const uint8_t* b;   // preshuffled B
+  const float* sa;    // EPI_ROWCOL: [M]; EPI_BLOCK: [K/128][M]
+  const float* sb;    // EPI_ROWCOL: [N]; EPI_BLOCK: [ceil(N/128)][K/128]
+  int M, N, K;
+};
+
+}  // namespace flygemm

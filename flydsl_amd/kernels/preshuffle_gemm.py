@@ -1,0 +1,168 @@
+"""MI355X preshuffle GEMM: the drop-in for the reference's ``kernels/preshuffle_gemm.py``.
+
+``compile_preshuffle_gemm_a8`` keeps the reference's name, keyword arguments, argument
+checks and launcher signature (reference ``kernels/preshuffle_gemm.py:39-202`` and
+``:1268-1303``)::
+
+    launch = compile_preshuffle_gemm_a8(K=K, tile_m=..., tile_n=..., tile_k=..., in_dtype="fp8",
+                                        out_dtype="bf16")
+    launch(c, a, b_preshuffled, scale_a, scale_b, M, N, stream)
+
+computes ``c[m, n] = out_dtype((acc[m, n] * scale_a[m]) * scale_b[n])`` with
+``acc = sum_k a[m, k] * b[n, k]`` (fp32 for fp8, exact int32 for int8/int4).  Behind the
+launcher there is no JIT: a ctypes call into the hand-written gfx950 kernels of
+``flydsl_amd/csrc`` (``flygemm_preshuffle`` in ``include/flygemm.h``).
+
+Differences from the reference, all on purpose:
+* ``tile_m/tile_n/tile_k``, ``lds_stage``, ``use_cshuffle_epilog``, ``waves_per_eu`` and
+  ``use_async_copy`` are validated exactly as the reference validates them and then serve
+  as hints only: the kernel variant comes from the library's MI355X table, keyed on the
+  run-time M, N, K.  ``variant=`` forces one (tests, tuning).
+* Any ``N % 16 == 0`` is computed in full (the reference's grid silently skips a tail
+  when ``N % tile_n != 0``); K must be a multiple of 128.
+* GPU errors raise ``RuntimeError`` (the reference prints them).
+* ``in_dtype`` "fp16"/"bf16"/"fp4" are accepted by the checks but not built for MI355X
+  yet: the launcher raises ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from ._launch import device_ptr, stream_handle
+
+_IN_DTYPES = ("fp8", "int8", "int4", "fp16", "bf16", "fp4")
+_OUT_TORCH = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+class PreshuffleGemm:
+    """Launcher returned by :func:`compile_preshuffle_gemm_a8`.
+
+    ``__call__(arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None)``.
+    """
+
+    def __init__(self, *, K, tile_m, tile_n, tile_k, in_dtype, out_dtype, variant=-1, **hints):
+        self.K = int(K)
+        self.tile_m, self.tile_n, self.tile_k = int(tile_m), int(tile_n), int(tile_k)
+        self.in_dtype = in_dtype
+        self.out_dtype = out_dtype
+        self.variant = int(variant)
+        self.hints = hints
+
+    def __call__(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):
+        if self.in_dtype not in _lib.FLYGEMM_IN:
+            raise NotImplementedError(f"in_dtype={self.in_dtype!r} has no MI355X kernel in this build")
+        M, N, K = int(M), int(N), self.K
+        h_stream = stream_handle(stream)
+        if M < 0 or N <= 0:
+            raise ValueError(f"invalid M={M}, N={N}")
+        if N % 16:
+            raise ValueError(f"N={N} must be a multiple of 16 (preshuffle block)")
+        if K % self.tile_k:
+            raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
+        if K % 128:
+            raise ValueError(f"K={K} must be a multiple of 128 on MI355X")
+        b_elems = N * K // 2 if self.in_dtype == "int4" else N * K
+        c = device_ptr(arg_c, "arg_c", M * N, dtypes=(_OUT_TORCH[self.out_dtype],))
+        a = device_ptr(arg_a, "arg_a", M * K, elem_bytes=1)
+        b = device_ptr(arg_b, "arg_b", b_elems, elem_bytes=1)
+        sa = device_ptr(arg_scale_a, "arg_scale_a", M, dtypes=(torch.float32,))
+        sb = device_ptr(arg_scale_b, "arg_scale_b", N, dtypes=(torch.float32,))
+        lib = _lib.load()
+        rc = lib.flygemm_preshuffle(c, a, b, sa, sb, M, N, K, _lib.FLYGEMM_IN[self.in_dtype],
+                                    _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
+        _lib.check(rc, "flygemm_preshuffle")
+
+
+def compile_preshuffle_gemm_a8(
+    *,
+    M: int = 0,
+    N: int = 0,
+    K: int,
+    tile_m: int,
+    tile_n: int,
+    tile_k: int,
+    in_dtype: str = "fp8",
+    out_dtype: str = "fp16",
+    lds_stage: int = 2,
+    use_cshuffle_epilog: bool = False,
+    waves_per_eu: Optional[int] = None,
+    use_async_copy: bool = False,
+    variant: int = -1,
+):
+    """Validate like the reference (``kernels/preshuffle_gemm.py:67-134,670-673``) and return
+    a launcher ``(c, a, b, scale_a, scale_b, M, N, stream)``."""
+    if in_dtype not in _IN_DTYPES:
+        raise ValueError(
+            "in_dtype must be one of ('fp8','int8','int4','fp16','bf16','fp4'), " f"got {in_dtype!r}"
+        )
+    if out_dtype not in ("fp16", "bf16"):
+        raise ValueError(f"out_dtype must be 'fp16' or 'bf16', got {out_dtype!r}")
+    is_fp4 = in_dtype == "fp4"
+    elem_bytes = 1 if in_dtype in ("fp8", "int8", "int4", "fp4") else 2
+    pack = 2 if is_fp4 else 1
+    tile_k_bytes = int(tile_k) * elem_bytes
+    if tile_k_bytes % 64 != 0:
+        raise ValueError(
+            f"tile_k_bytes must be divisible by 64, got tile_k_bytes={tile_k_bytes} "
+            f"(tile_k={tile_k}, elem_bytes={elem_bytes})"
+        )
+    if is_fp4 and tile_k_bytes // pack // 64 < 2 and int(tile_k) != 128:
+        raise ValueError(f"FP4 requires tile_k=128 or tile_k >= {64 * 2 * pack}, got tile_k={tile_k}")
+    if is_fp4 and int(tile_k) == 128 and lds_stage != 2:
+        raise NotImplementedError("FP4 tile_k=128 currently only supports lds_stage=2")
+    if int(lds_stage) not in (1, 2):
+        raise ValueError(f"lds_stage must be 1 or 2, got {lds_stage!r}")
+    bytes_a_per_tile = int(tile_m) * int(tile_k) * elem_bytes // pack
+    if bytes_a_per_tile % 256 != 0:
+        raise ValueError(
+            "tile_m*tile_k*elem_bytes/a_elem_vec_pack must be divisible by 256: "
+            f"tile_m={tile_m}, tile_k={tile_k}, elem_bytes={elem_bytes}, pack={pack}"
+        )
+    if (bytes_a_per_tile // 256) % 16 != 0:
+        raise ValueError(f"bytes_per_thread_a ({bytes_a_per_tile // 256}) must be divisible by 16")
+    if int(tile_n) % 64 != 0 or int(tile_m) % 16 != 0:
+        raise ValueError(f"tile_n must be a multiple of 64 and tile_m of 16, got {tile_m}x{tile_n}")
+    if in_dtype == "fp8" and int(tile_k) % 128 != 0:
+        raise ValueError(f"tile_k must be divisible by 128 for mfma_scale_x128, got tile_k={tile_k}")
+    return PreshuffleGemm(
+        K=K, tile_m=tile_m, tile_n=tile_n, tile_k=tile_k, in_dtype=in_dtype, out_dtype=out_dtype,
+        variant=variant, M=M, N=N, lds_stage=lds_stage, use_cshuffle_epilog=use_cshuffle_epilog,
+        waves_per_eu=waves_per_eu, use_async_copy=use_async_copy,
+    )
+
+
+def compile_preshuffle_gemm_w4(*, M: int = 0, N: int = 0, K: int, tile_m: int, tile_n: int, tile_k: int,
+                               a_dtype: str = "fp4", b_dtype: str = "fp4", out_dtype: str = "bf16",
+                               lds_stage: int = 2, use_cshuffle_epilog: bool = False,
+                               waves_per_eu: Optional[int] = None, use_async_copy: bool = False):
+    """MXFP4 entry (reference ``kernels/preshuffle_gemm.py:1306-1337``): same checks, no MI355X
+    kernel in this build yet."""
+    if a_dtype == "fp8":
+        raise NotImplementedError("fp8-A not yet supported with MXFP4 kernel (op_sel_a overflow)")
+    return compile_preshuffle_gemm_a8(
+        M=M, N=N, K=K, tile_m=tile_m, tile_n=tile_n, tile_k=tile_k, in_dtype="fp4",
+        out_dtype=out_dtype, lds_stage=lds_stage, use_cshuffle_epilog=use_cshuffle_epilog,
+        waves_per_eu=waves_per_eu, use_async_copy=use_async_copy,
+    )
+
+
+def accumulators(acc, a, b, M, N, K, in_dtype, variant=-1, stream=None):
+    """Raw accumulators of ``sum_k a[m,k] b[n,k]`` (int32 for int8/int4, fp32 for fp8), no
+    scaling: the value the kernels hold before the epilogue."""
+    if in_dtype not in _lib.FLYGEMM_IN:
+        raise ValueError(f"in_dtype must be one of {tuple(_lib.FLYGEMM_IN)}, got {in_dtype!r}")
+    b_elems = N * K // 2 if in_dtype == "int4" else N * K
+    want = torch.float32 if in_dtype == "fp8" else torch.int32
+    p_acc = device_ptr(acc, "acc", M * N, dtypes=(want,))
+    p_a = device_ptr(a, "a", M * K, elem_bytes=1)
+    p_b = device_ptr(b, "b", b_elems, elem_bytes=1)
+    lib = _lib.load()
+    rc = lib.flygemm_accumulators(p_acc, p_a, p_b, int(M), int(N), int(K), _lib.FLYGEMM_IN[in_dtype],
+                                  int(variant), stream_handle(stream))
+    _lib.check(rc, "flygemm_accumulators")
+
+
+__all__ = ["compile_preshuffle_gemm_a8", "compile_preshuffle_gemm_w4", "accumulators", "PreshuffleGemm"]

@@ -1,0 +1,92 @@
+"""The measured workloads and their seeded synthetic operands.
+
+Five configurations plus the large square FP8 shape used for the MFMA-throughput target.
+Operands are drawn on the CPU from ``torch.Generator().manual_seed(seed)`` (A first,
+then B), quantized with ``flydsl_amd.quant`` and preshuffled, so every process that asks
+for a configuration sees the same bytes.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import quant
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    kind: str          # "fp8" | "int8" | "int4" | "fp8_block"
+    M: int
+    N: int
+    K: int
+    seed: int
+    b_std: float = 1.0
+    note: str = ""
+
+    @property
+    def flops(self) -> int:
+        return 2 * self.M * self.N * self.K
+
+    @property
+    def bytes(self) -> int:
+        """Algorithmic bytes: A + B + C(bf16) + fp32 scales (reference test_preshuffle_gemm.py:254,
+        test_blockscale_preshuffle_gemm.py:222)."""
+        M, N, K = self.M, self.N, self.K
+        b = N * K // 2 if self.kind == "int4" else N * K
+        base = M * K + b + 2 * M * N
+        if self.kind == "fp8_block":
+            return base + 4 * (M * (K // 128) + ((N + 127) // 128) * (K // 128))
+        return base + 4 * (M + N)
+
+
+WORKLOADS = {
+    "C1": Workload("C1", "fp8", 128, 4096, 4096, 0, note="FP8 per-token/per-channel"),
+    "C2": Workload("C2", "fp8", 16, 28672, 8192, 1, note="FP8 decode, HBM-bound"),
+    "C3": Workload("C3", "int8", 4096, 4096, 4096, 2, note="INT8 W8A8"),
+    "C4": Workload("C4", "fp8_block", 1024, 7168, 7168, 3, note="FP8 1x128/128x128 blockscale"),
+    "C5": Workload("C5", "int4", 256, 14336, 4096, 4, b_std=0.02, note="W4A8"),
+    "T": Workload("T", "fp8", 8192, 8192, 8192, 5, note="FP8 8192^3, MFMA-bound target"),
+}
+
+
+def custom(kind: str, M: int, N: int, K: int, seed: int, b_std: float = 1.0) -> Workload:
+    return Workload(f"{kind}_{M}x{N}x{K}_s{seed}", kind, M, N, K, seed, b_std)
+
+
+def make_operands(w: Workload) -> dict:
+    """CPU operands for workload ``w``.
+
+    Keys: ``a`` (A quantized, [M, K]), ``b`` (B quantized, unshuffled [N, K], int8 values for
+    int4), ``b_dev`` (the B buffer the kernel reads: shuffled, int4 packed), ``sa``, ``sb``
+    (fp32 scales; blockscale: ``sa`` is [M, K/128] and ``sa_t`` its [K/128, M] transpose,
+    ``sb`` is [N/128, K/128]).
+    """
+    g = torch.Generator().manual_seed(w.seed)
+    a32 = torch.randn(w.M, w.K, generator=g, dtype=torch.float32)
+    b32 = torch.randn(w.N, w.K, generator=g, dtype=torch.float32) * w.b_std
+    out = {"workload": w}
+    if w.kind == "fp8":
+        a, sa = quant.pertoken_quant(a32, quant_dtype=quant.FP8)
+        b, sb = quant.pertoken_quant(b32, quant_dtype=quant.FP8)
+    elif w.kind == "int8":
+        a, sa = quant.pertoken_quant(a32, quant_dtype=torch.int8)
+        b, sb = quant.pertoken_quant(b32, quant_dtype=torch.int8)
+    elif w.kind == "int4":
+        a, sa = quant.pertoken_quant(a32, quant_dtype=torch.int8)
+        b, sb = quant.pertoken_quant(b32, quant_dtype=torch.int8, dtypeMax=7)
+    elif w.kind == "fp8_block":
+        a, sa = quant.blockscale_quant(a32, 1, 128)
+        pad = (-w.N) % 128
+        b32p = torch.cat([b32, torch.zeros(pad, w.K)]) if pad else b32
+        b, sb = quant.blockscale_quant(b32p, 128, 128)
+        b = b[: w.N].contiguous()
+        out["sa_t"] = sa.t().contiguous()
+    else:
+        raise ValueError(f"unknown kind {w.kind!r}")
+    del a32, b32
+    b_shuf = quant.shuffle_weight(b)
+    out["b_dev"] = quant.pack_int4(b_shuf) if w.kind == "int4" else b_shuf
+    out.update(a=a.contiguous(), b=b.contiguous(), sa=sa.contiguous(), sb=sb.contiguous())
+    return out

@@ -1,0 +1,79 @@
+/* flygemm -- C ABI of the gfx950 (MI355X) quantized preshuffle GEMM library.
+ *
+ * Replaces, for the preshuffle GEMM path, the launch boundary the reference reaches through
+ * its JIT: the JIT'd host entry `void entry(void** args)` that packs
+ * (c, a, b, scale_a, scale_b, i32 M, i32 N, stream) and calls hipModuleLaunchKernel
+ * (reference python/flydsl/compiler/jit_executor.py:105-121, jit_function.py:593-617,
+ * lib/Runtime/FlyRocmRuntimeWrappers.cpp:58-67).
+ *
+ * Conventions shared by every entry point:
+ *  - All pointers are device pointers the caller allocated; nothing is allocated,
+ *    freed or synchronized here.  Launches are asynchronous on `stream` (a hipStream_t,
+ *    NULL = default stream).  Callers keep buffers alive until the stream has finished.
+ *  - A is row-major [M][K] bytes.  B is the preshuffled [N][K] buffer produced by the
+ *    reference's `shuffle_weight(b, layout=(16, 16))` (tests/utils.py:76-96): element
+ *    (n, k) at byte (n/16)*16*K + (k/16)*256 + (n%16)*16 + (k%16).  INT4 B is that buffer
+ *    packed two values per byte as in tests/kernels/test_preshuffle_gemm.py:165-174.
+ *  - Requirements: N % 16 == 0, K % 128 == 0, M >= 0 (M == 0 is a no-op), every operand
+ *    below 2^31 elements.  Violations return nonzero without launching.
+ *  - Return value: 0 on success, otherwise a hipError_t code; flygemm_last_error() gives
+ *    the message of the calling thread's last failure.
+ *  - `variant`: -1 picks the kernel from the built-in table; 0..flygemm_num_variants()-1
+ *    forces one (for tests and tuning).
+ */
+#ifndef FLYGEMM_H
+#define FLYGEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FLYGEMM_IN_FP8 = 0,  /* OCP e4m3fn (torch.float8_e4m3fn) */
+  FLYGEMM_IN_INT8 = 1, /* int8 A and B */
+  FLYGEMM_IN_INT4 = 2  /* int8 A, packed signed int4 B */
+};
+enum { FLYGEMM_OUT_BF16 = 0, FLYGEMM_OUT_FP16 = 1 };
+
+/* C[M][N] = out_dtype((acc[m][n] * scale_a[m]) * scale_b[n]),
+ * acc = sum_k A[m][k] * B[n][k] in fp32 (fp8) or int32 (int8/int4).
+ * scale_a: fp32 [M] per token; scale_b: fp32 [N] per output channel.
+ * Replaces the launcher returned by compile_preshuffle_gemm_a8
+ * (reference kernels/preshuffle_gemm.py:39-57, launch_gemm :1268-1301; epilogue :863-883). */
+int flygemm_preshuffle(void* c, const void* a, const void* b, const float* scale_a, const float* scale_b,
+                       int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t out_dtype,
+                       int32_t variant, void* stream);
+
+/* FP8 blockscale GEMM: C[m][n] = out_dtype(sum_kb (sum_{k in kb} A*B) * x_scale_t[kb][m]
+ *                                                 * w_scale[n/128][kb]),
+ * x_scale_t: fp32 [K/128][M] (K-block major), w_scale: fp32 [ceil(N/128)][K/128].
+ * scale_block_k must be 128.  Replaces the launcher of compile_blockscale_preshuffle_gemm,
+ * whose contract is its call site tests/kernels/test_blockscale_preshuffle_gemm.py:173-204
+ * and oracle :86-109 (the kernel source is absent from the reference snapshot). */
+int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_scale_t, const float* w_scale,
+                       int32_t M, int32_t N, int32_t K, int32_t scale_block_k, int32_t out_dtype,
+                       int32_t variant, void* stream);
+
+/* Raw accumulators, no scaling: int32 [M][N] for int8/int4, fp32 [M][N] for fp8.
+ * Exposes the value the reference's kernels hold before their epilogue
+ * (kernels/preshuffle_gemm.py:643-797) so integer paths can be checked bit-exactly. */
+int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int32_t N, int32_t K,
+                         int32_t in_dtype, int32_t variant, void* stream);
+
+/* Kernel variant table (replaces the reference's per-call tile kwargs,
+ * kernels/preshuffle_gemm.py:39-53, with a static table). */
+int32_t flygemm_num_variants(void);
+const char* flygemm_variant_name(int32_t variant);
+int32_t flygemm_select_variant(int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t blockscale);
+
+/* Message of the calling thread's last failure ("" if none).  The reference prints HIP
+ * errors instead of returning them (lib/Runtime/FlyRocmRuntimeWrappers.cpp:22-30). */
+const char* flygemm_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLYGEMM_H */

@@ -1,0 +1,187 @@
+"""GPU parity: the gfx950 kernels, called through the drop-in launchers / C ABI, against the
+CPU oracle on the same seeded operands.
+
+Bars: int8/int4 -- raw int32 accumulators and bf16 outputs bit-exact; fp8 paths --
+|out - ref| <= 1e-2 |ref| + 1e-2 RMS(ref) with ref the float64 dequantize-then-matmul."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from flydsl_amd import _lib, workloads
+from tests import helpers as H
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+VARIANTS = _lib.variants()
+MAIN = [i for i, n in enumerate(VARIANTS) if n.startswith("main_")]
+DECODE = [i for i, n in enumerate(VARIANTS) if n.startswith("decode_")]
+DECODE_ROWS = {i: 16 * int(VARIANTS[i].split("_m")[1].split("_")[0]) for i in DECODE}
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+_OPS = {}
+
+
+def _ops(name):
+    if name not in _OPS:
+        _OPS.clear()
+        _OPS[name] = workloads.make_operands(workloads.WORKLOADS[name])
+    return _OPS[name]
+
+
+# ---------------------------------------------------------------- committed fixtures
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "fp8_block"])
+def test_golden_fixture(gpu, kind):
+    z = np.load(os.path.join(GOLDEN, f"small_{kind}.npz"), allow_pickle=False)
+    M, N, K = int(z["M"]), int(z["N"]), int(z["K"])
+    _say(f"golden {kind} {M}x{N}x{K}")
+    a = torch.from_numpy(z["a"]).to(gpu).view(torch.int8).view(-1)
+    b = torch.from_numpy(z["b_dev"]).to(gpu).view(torch.int8)
+    sa = torch.from_numpy(z["sa"]).to(gpu)
+    sb = torch.from_numpy(z["sb"]).to(gpu)
+    from oracle import gemm as og, numerics as on
+    for v in [-1] + MAIN + [d for d in DECODE if DECODE_ROWS[d] >= M]:
+        c = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+        if kind == "fp8_block":
+            rc = _lib.load().flygemm_blockscale(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(),
+                                                sb.data_ptr(), M, N, K, 128, 0, v, None)
+        else:
+            rc = _lib.load().flygemm_preshuffle(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(),
+                                                sb.data_ptr(), M, N, K, _lib.FLYGEMM_IN[kind], 0, v, None)
+        _lib.check(rc, "golden")
+        torch.cuda.synchronize()
+        out = c.float().cpu().numpy()
+        exp = z["expected"]
+        if kind in ("int8", "int4"):
+            want = on.bf16_to_f32(og.epilogue_int_bf16(exp, z["sa"], z["sb"]))
+            assert np.array_equal(out, want), f"variant {v}"
+        else:
+            assert og.within_bar(out, exp)[0], f"variant {v}"
+
+
+def test_workload_operands_match_committed_hashes(gpu):
+    """The box generates the same operand bytes as the machine that wrote the fixtures."""
+    with open(os.path.join(GOLDEN, "workload_sha256.json")) as f:
+        want = json.load(f)
+    for name in ["C1", "C3", "C5"]:
+        ops = workloads.make_operands(workloads.WORKLOADS[name])
+        got = hashlib.sha256(H.u8(ops["b_dev"]).tobytes()).hexdigest()
+        assert got == want[name]["b_dev"], name
+
+
+# ---------------------------------------------------------------- full-size configurations
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+def test_config_parity(gpu, name):
+    ops = _ops(name)
+    w = ops["workload"]
+    _say(f"config {name} {w.kind} {w.M}x{w.N}x{w.K} variant={VARIANTS[_lib.load().flygemm_select_variant(w.M, w.N, w.K, 0, 0)]}")
+    out = H.launch(ops, gpu)
+    torch.cuda.synchronize()
+    ref = H.check(ops, out)
+    if w.kind in ("int8", "int4"):
+        acc = H.raw_acc(ops, gpu).cpu().numpy()
+        assert np.array_equal(acc, ref), f"{name}: int32 accumulators differ"
+
+
+def test_config_T_sampled_rows(gpu):
+    ops = _ops("T")
+    _say("config T fp8 8192^3 (sampled rows)")
+    out = H.launch(ops, gpu)
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(0).choice(8192, 96, replace=False)
+    rows.sort()
+    H.check(ops, out, rows=rows)
+
+
+# ---------------------------------------------------------------- every variant, ragged shapes
+SHAPES = [(1, 64, 128), (7, 2112, 256), (16, 1024, 2048), (33, 1040, 384), (100, 272, 384), (300, 528, 640)]
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "fp8_block"])
+@pytest.mark.parametrize("variant", list(range(len(VARIANTS))))
+def test_variants_ragged(gpu, kind, variant):
+    for (M, N, K) in SHAPES:
+        if variant in DECODE and M > DECODE_ROWS[variant]:
+            continue
+        w = workloads.custom(kind, M, N, K, seed=M + N + K, b_std=0.02 if kind == "int4" else 1.0)
+        ops = workloads.make_operands(w)
+        _say(f"variant {VARIANTS[variant]} {kind} {M}x{N}x{K}")
+        out = H.launch(ops, gpu, variant=variant)
+        torch.cuda.synchronize()
+        ref = H.check(ops, out)
+        if kind in ("int8", "int4"):
+            assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+def test_odd_k_tile_count_and_fp16_out(gpu, kind):
+    """K = 8320 = 65 K tiles (reference test shape), fp16 output."""
+    w = workloads.custom(kind, 160, 512, 8320, seed=9)
+    ops = workloads.make_operands(w)
+    _say(f"odd-k {kind} fp16")
+    out = H.launch(ops, gpu, out_dtype="fp16")
+    torch.cuda.synchronize()
+    H.check(ops, out, out_dtype="fp16")
+
+
+@pytest.mark.parametrize("M", [1, 7, 16, 33, 64])
+@pytest.mark.parametrize("N,K", [(7168, 2304), (2112, 7168), (3072, 1536)])
+def test_blockscale_reference_shapes(gpu, M, N, K):
+    """The reference's DeepSeek-V3 blockscale shapes (test_blockscale_preshuffle_gemm.py:111-149)."""
+    ops = workloads.make_operands(workloads.custom("fp8_block", M, N, K, seed=M * 7 + N))
+    _say(f"blockscale {M}x{N}x{K}")
+    out = H.launch(ops, gpu)
+    torch.cuda.synchronize()
+    H.check(ops, out)
+
+
+# ---------------------------------------------------------------- streams, graphs, no-ops
+def test_side_stream_and_zero_m(gpu):
+    ops = workloads.make_operands(workloads.custom("int8", 48, 256, 512, seed=21))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        out = H.launch(ops, gpu, stream=s)
+    s.synchronize()
+    H.check(ops, out)
+    c = torch.full((4,), 7.0, dtype=torch.bfloat16, device=gpu)
+    lib = _lib.load()
+    assert lib.flygemm_preshuffle(c.data_ptr(), c.data_ptr(), c.data_ptr(), c.data_ptr(), c.data_ptr(),
+                                  0, 64, 128, 0, 0, -1, None) == 0
+    torch.cuda.synchronize()
+    assert (c.float() == 7.0).all()
+
+
+def test_graph_replay(gpu):
+    """Capture the launcher in a HIP graph; every replay (with eager work in between) must
+    equal the eager result."""
+    ops = workloads.make_operands(workloads.custom("fp8", 64, 1024, 1024, seed=31))
+    eager = H.launch(ops, gpu)
+    torch.cuda.synchronize()
+    a = ops["a"].to(gpu).view(torch.int8).view(-1)
+    b = ops["b_dev"].to(gpu).view(torch.int8).view(-1)
+    sa, sb = ops["sa"].to(gpu).view(-1), ops["sb"].to(gpu).view(-1)
+    c = torch.empty(64, 1024, dtype=torch.bfloat16, device=gpu)
+    from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
+    fn = compile_preshuffle_gemm_a8(K=1024, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(c.view(-1), a, b, sa, sb, 64, 1024, s)  # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn(c.view(-1), a, b, sa, sb, 64, 1024, torch.cuda.current_stream())
+    for i in range(3):
+        c.fill_(0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, eager), f"replay {i}"

@@ -1,0 +1,132 @@
+"""CPU-only tests of the host side: the C-ABI library loads and exports every declared
+symbol, the drop-in entry points validate arguments like the reference, the variant
+table and workload arithmetic are what the kernels and the measurements assume.  No
+GPU compute is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from flydsl_amd import _lib, workloads
+from flydsl_amd.kernels.blockscale_preshuffle_gemm import compile_blockscale_preshuffle_gemm
+from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8, compile_preshuffle_gemm_w4
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "flygemm.h")).read()
+    return sorted(set(re.findall(r"\b(flygemm_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_symbols()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), n
+    bound = {n for n, _, _ in _lib.SIGNATURES}
+    assert bound == set(names)
+
+
+def test_variant_table():
+    names = _lib.variants()
+    assert any(n.startswith("main_") for n in names) and any(n.startswith("decode_") for n in names)
+    lib = _lib.load()
+    assert names[lib.flygemm_select_variant(16, 28672, 8192, 0, 0)].startswith("decode_m1")
+    assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
+    assert lib.flygemm_variant_name(-1) is None and lib.flygemm_variant_name(len(names)) is None
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    """Validation returns an error code and message without touching the GPU."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 100, 256, 0, 0, -1, None)
+    assert rc != 0 and b"multiple of 16" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 200, 0, 0, -1, None)
+    assert rc != 0 and b"multiple of 128" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(None, p, p, p, p, 16, 128, 256, 0, 0, -1, None)
+    assert rc != 0 and b"null" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 256, 7, 0, -1, None)
+    assert rc != 0 and b"in_dtype" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 256, 0, 0, 99, None)
+    assert rc != 0 and b"variant" in lib.flygemm_last_error()
+    rc = lib.flygemm_blockscale(p, p, p, p, p, 16, 128, 256, 64, 0, -1, None)
+    assert rc != 0 and b"scale_block_k" in lib.flygemm_last_error()
+    rc = lib.flygemm_accumulators(p, p, p, -1, 128, 256, 0, -1, None)
+    assert rc != 0 and b"invalid sizes" in lib.flygemm_last_error()
+    # M == 0 is a no-op that succeeds without launching
+    assert lib.flygemm_preshuffle(p, p, p, p, p, 0, 128, 256, 0, 0, -1, None) == 0
+
+
+@pytest.mark.parametrize("kw, exc", [
+    (dict(in_dtype="fp32"), ValueError),
+    (dict(out_dtype="fp32"), ValueError),
+    (dict(tile_k=17), ValueError),          # the reference AOT example's bad tile (aot_example.py:226-240)
+    (dict(tile_k=32), ValueError),          # tile_k bytes not a multiple of 64
+    (dict(tile_m=8), ValueError),           # tile_m*tile_k not a multiple of 256
+    (dict(in_dtype="fp8", tile_k=64), ValueError),  # gfx950 fp8 needs tile_k % 128 == 0
+    (dict(lds_stage=3), ValueError),
+])
+def test_compile_validation_matches_reference(kw, exc):
+    args = dict(K=4096, tile_m=64, tile_n=128, tile_k=128, in_dtype="int8", out_dtype="bf16")
+    args.update(kw)
+    with pytest.raises(exc):
+        compile_preshuffle_gemm_a8(**args)
+
+
+def test_w4_entry_and_unbuilt_dtypes():
+    with pytest.raises(NotImplementedError):
+        compile_preshuffle_gemm_w4(K=256, tile_m=64, tile_n=128, tile_k=128, a_dtype="fp8")
+    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="bf16")
+    with pytest.raises(NotImplementedError):
+        fn(None, None, None, None, None, 16, 128, None)
+
+
+def test_launcher_rejects_host_tensors_and_bad_shapes():
+    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
+    c = torch.empty(16 * 128, dtype=torch.bfloat16)
+    a = torch.empty(16 * 256, dtype=torch.int8)
+    b = torch.empty(128 * 256, dtype=torch.int8)
+    s = torch.empty(128, dtype=torch.float32)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        fn(c, a, b, s, s, 16, 128, None)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        fn(c, a, b, s, s, 16, 120, None)
+    with pytest.raises(TypeError):
+        fn(c, a, b, s, s, 16, 128, "stream")
+
+
+def test_blockscale_compile_validation():
+    with pytest.raises(ValueError):
+        compile_blockscale_preshuffle_gemm(K=7168, tile_m=64, tile_n=128, tile_k=128, scale_block_k=64)
+    with pytest.raises(ValueError):
+        compile_blockscale_preshuffle_gemm(K=7168, tile_m=64, tile_n=128, tile_k=192)
+    compile_blockscale_preshuffle_gemm(K=7168, tile_m=64, tile_n=128, tile_k=128)
+
+
+def test_workload_arithmetic_matches_baseline():
+    W = workloads.WORKLOADS
+    assert round(W["C2"].bytes / 1e6, 3) == 236.044
+    assert round(W["C1"].bytes / 1e6, 3) == 18.367
+    assert round(W["C4"].bytes / 1e6, 3) == 73.642
+    assert round(W["C5"].bytes / 1e6, 3) == 37.807
+    assert W["T"].flops == 2 * 8192 ** 3
+
+
+def test_small_operands_roundtrip_through_oracle():
+    """Product preparation (quantize, shuffle, pack) agrees with the oracle's restatement."""
+    import numpy as np
+    from oracle import layout as ol, quant as oq
+    w = workloads.custom("int4", 32, 64, 256, seed=11, b_std=0.02)
+    ops = workloads.make_operands(w)
+    b = ops["b"].numpy()
+    assert np.array_equal(ops["b_dev"].numpy(), ol.pack_int4(ol.shuffle_weight(b)))
+    assert np.array_equal(ol.unpack_int4(ops["b_dev"].numpy()), ol.shuffle_weight(b))
+    g = torch.Generator().manual_seed(11)
+    a32 = torch.randn(32, 256, generator=g)
+    q, s = oq.quant_rows(a32.numpy(), "int8")
+    assert np.array_equal(ops["a"].numpy(), q)

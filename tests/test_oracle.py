@@ -1,0 +1,291 @@
+"""Pins for the CPU oracle (``oracle/``): every oracle function is checked here against
+something other than its own formula -- torch's casts, brute-force loops, exact integer
+arithmetic, algebraically different formulations, and planted mistakes that must fail."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as og
+from oracle import layout as ol
+from oracle import numerics as on
+from oracle import quant as oq
+
+
+# ---------------------------------------------------------------- numerics
+def test_e4m3fn_known_values():
+    d = on.e4m3fn_decode(np.array([0x7E, 0x08, 0x01, 0x38, 0x00, 0x80, 0xFE, 0x07], dtype=np.uint8))
+    assert d[0] == 448.0 and d[1] == 2.0 ** -6 and d[2] == 2.0 ** -9 and d[3] == 1.0
+    assert d[4] == 0.0 and d[5] == 0.0 and np.signbit(d[5]) and d[6] == -448.0
+    assert d[7] == 7 * 2.0 ** -9
+    assert np.isnan(on.e4m3fn_decode(np.array([0x7F, 0xFF], dtype=np.uint8))).all()
+
+
+def test_e4m3fn_decode_matches_torch_all_codes():
+    codes = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    d = on.e4m3fn_decode(codes)
+    assert np.array_equal(np.isnan(t), np.isnan(d))
+    ok = ~np.isnan(t)
+    assert np.array_equal(t[ok].view(np.uint32), d[ok].view(np.uint32))
+
+
+def test_e4m3fn_encode_roundtrip_and_ties():
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=np.uint8)
+    assert np.array_equal(on.e4m3fn_encode(on.e4m3fn_decode(codes)), codes)
+    # exact midpoints between neighbouring positive codes round to the even code
+    pos = on.e4m3fn_decode(np.arange(0, 0x7E, dtype=np.uint8)).astype(np.float64)
+    nxt = on.e4m3fn_decode(np.arange(1, 0x7F, dtype=np.uint8)).astype(np.float64)
+    mid = ((pos + nxt) / 2).astype(np.float32)
+    enc = on.e4m3fn_encode(mid)
+    lo = np.arange(0, 0x7E)
+    want = np.where(lo % 2 == 0, lo, lo + 1)
+    assert np.array_equal(enc, want.astype(np.uint8))
+
+
+def test_e4m3fn_encode_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        (rng.standard_normal(1_000_000) * 50).astype(np.float32),
+        (rng.standard_normal(100_000) * 1e-3).astype(np.float32),
+        np.array([0.0, -0.0, 448.0, -448.0, 460.0, 464.0, 470.0, 479.9, 480.0, 1e9, np.inf, -np.inf, np.nan],
+                 dtype=np.float32),
+    ])
+    pos = on.e4m3fn_decode(np.arange(0, 0x7E, dtype=np.uint8)).astype(np.float64)
+    nxt = on.e4m3fn_decode(np.arange(1, 0x7F, dtype=np.uint8)).astype(np.float64)
+    x = np.concatenate([x, ((pos + nxt) / 2).astype(np.float32), -((pos + nxt) / 2).astype(np.float32)])
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = on.e4m3fn_encode(x)
+    # NaN payload/sign may differ; compare NaN-ness, then exact codes elsewhere
+    ref_nan = np.isnan(on.e4m3fn_decode(ref))
+    got_nan = np.isnan(on.e4m3fn_decode(got))
+    assert np.array_equal(ref_nan, got_nan)
+    assert np.array_equal(ref[~ref_nan], got[~got_nan])
+
+
+def test_bf16_rne_matches_torch():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(200_000).astype(np.float32) * 1e3,
+                        rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32)])
+    x = x[np.isfinite(x)]
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(on.bf16_rne(x), ref)
+    exact = on.bf16_to_f32(ref)
+    assert np.array_equal(on.bf16_rne(exact), ref)
+
+
+# ---------------------------------------------------------------- quantizers
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4"])
+def test_quant_rows_invariants(kind):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((64, 512)).astype(np.float32)
+    x[3] = 0.0
+    q, s = oq.quant_rows(x, kind)
+    qmax = oq.QMAX[kind]
+    v = on.e4m3fn_decode(q) if kind == "fp8" else q.astype(np.float32)
+    assert np.all(np.abs(v) <= qmax)
+    assert s[3] == 1.0 and np.all(v[3] == 0)
+    # the row's amax maps to +-qmax exactly
+    i = np.abs(x).argmax(axis=1)
+    peak = np.abs(v[np.arange(64), i])
+    assert np.all(peak[np.arange(64) != 3] == qmax)
+    err = np.abs(v * s[:, None] - x)
+    if kind == "fp8":
+        # half an fp8 ulp at the value's binade (3 mantissa bits), plus subnormal quantum
+        y = np.abs(x / s[:, None])
+        ulp = 2.0 ** (np.maximum(np.floor(np.log2(np.maximum(y, 1e-30))), -6) - 3)
+        assert np.all(np.abs(v - x / s[:, None]) <= ulp / 2 + 1e-6)
+    else:
+        assert np.all(err <= s[:, None] / 2 * (1 + 1e-5))
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+def test_quant_rows_matches_product_quantizer(kind):
+    from flydsl_amd import quant as pq
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(96, 384, generator=g)
+    qd = pq.FP8 if kind == "fp8" else torch.int8
+    q_t, s_t = pq.pertoken_quant(x, quant_dtype=qd)
+    q_o, s_o = oq.quant_rows(x.numpy(), kind)
+    assert np.array_equal(s_t.view(-1).numpy(), s_o)
+    assert np.array_equal(q_t.view(torch.int8).numpy().view(np.uint8), q_o.view(np.uint8))
+
+
+def test_quant_int4_matches_product_quantizer():
+    from flydsl_amd import quant as pq
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(64, 256, generator=g) * 0.02
+    q_t, s_t = pq.pertoken_quant(x, quant_dtype=torch.int8, dtypeMax=7)
+    q_o, s_o = oq.quant_rows(x.numpy(), "int4")
+    assert np.array_equal(s_t.view(-1).numpy(), s_o)
+    assert np.array_equal(q_t.numpy(), q_o)
+
+
+def test_reference_int8_cast_truncates():
+    """The reference's own int8 cast (``.to(torch.int8)``) truncates; the product offers it as
+    rounding='trunc' and defaults to round-half-even."""
+    from flydsl_amd import quant as pq
+    x = torch.tensor([[127.0, 1.7, 2.5, -1.7, -2.5, 0.4]])
+    q_tr, _ = pq.pertoken_quant(x, quant_dtype=torch.int8, rounding="trunc")
+    q_rn, _ = pq.pertoken_quant(x, quant_dtype=torch.int8)
+    assert q_tr.tolist() == [[127, 1, 2, -1, -2, 0]]
+    assert q_rn.tolist() == [[127, 2, 2, -2, -2, 0]]
+
+
+def test_quant_blocks_reduces_to_rows_and_matches_product():
+    from flydsl_amd import quant as pq
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((32, 256)).astype(np.float32)
+    qb, sb = oq.quant_blocks(x, 1, 256)
+    qr, sr = oq.quant_rows(x, "fp8")
+    assert np.array_equal(qb, qr) and np.array_equal(sb.reshape(-1), sr)
+    for br, bc in [(1, 128), (128, 128)]:
+        xx = rng.standard_normal((256, 384)).astype(np.float32)
+        q_o, s_o = oq.quant_blocks(xx, br, bc)
+        q_t, s_t = pq.blockscale_quant(torch.from_numpy(xx), br, bc)
+        assert np.array_equal(s_t.numpy(), s_o)
+        assert np.array_equal(q_t.view(torch.uint8).numpy(), q_o)
+
+
+# ---------------------------------------------------------------- layouts
+def test_shuffle_bruteforce_and_inverse():
+    N, K = 48, 96
+    b = (np.arange(N * K) % 251).astype(np.uint8).reshape(N, K)
+    flat = ol.shuffle_weight(b)
+    for n in range(N):
+        for k in range(K):
+            assert flat[ol.shuffle_index(n, k, K)] == b[n, k]
+    assert np.array_equal(ol.unshuffle_weight(flat, N, K), b)
+
+
+def test_shuffle_matches_product():
+    from flydsl_amd import quant as pq
+    rng = np.random.default_rng(4)
+    b = rng.integers(-128, 128, (64, 256), dtype=np.int8)
+    got = pq.shuffle_weight(torch.from_numpy(b)).numpy().reshape(-1)
+    assert np.array_equal(got, ol.shuffle_weight(b))
+
+
+def test_int4_pack_unpack_exhaustive():
+    from flydsl_amd import quant as pq
+    vals = np.arange(-8, 8, dtype=np.int8)
+    # every value in every one of the 8 positions of a packing group
+    groups = []
+    for pos in range(8):
+        for v in vals:
+            g = np.zeros(8, dtype=np.int8)
+            g[pos] = v
+            g[(pos + 3) % 8] = -v - 1 if v != -8 else 7
+            groups.append(g)
+    x = np.concatenate(groups)
+    packed = ol.pack_int4(x)
+    assert packed.size == x.size // 2
+    assert np.array_equal(ol.unpack_int4(packed), x)
+    assert np.array_equal(pq.pack_int4(torch.from_numpy(x)).numpy(), packed)
+    # the nibble placement the kernel relies on: byte j = u[j] | u[j+4] << 4
+    g = np.array([1, 2, 3, 4, -1, -2, -3, -4], dtype=np.int8)
+    assert ol.pack_int4(g).view(np.uint8).tolist() == [0xF1, 0xE2, 0xD3, 0xC4]
+
+
+# ---------------------------------------------------------------- GEMM oracles
+def _brute(a, b):
+    M, K = a.shape
+    N = b.shape[0]
+    out = np.zeros((M, N), dtype=np.float64)
+    for m in range(M):
+        for n in range(N):
+            s = 0.0
+            for k in range(K):
+                s += float(a[m, k]) * float(b[n, k])
+            out[m, n] = s
+    return out
+
+
+def test_acc_int_exact():
+    rng = np.random.default_rng(5)
+    a = rng.integers(-127, 128, (5, 64), dtype=np.int8)
+    b = rng.integers(-127, 128, (7, 64), dtype=np.int8)
+    assert np.array_equal(og.acc_int(a, b), _brute(a, b).astype(np.int32))
+    a = rng.integers(-127, 128, (64, 1024), dtype=np.int8)
+    b = rng.integers(-127, 128, (48, 1024), dtype=np.int8)
+    ref = torch._int_mm(torch.from_numpy(a), torch.from_numpy(b).t().contiguous()).numpy()
+    assert np.array_equal(og.acc_int(a, b), ref)
+    # extreme magnitudes: all -127 x -127 over a long K stays exact
+    a = np.full((2, 8192), -127, dtype=np.int8)
+    assert og.acc_int(a, a)[0, 0] == 127 * 127 * 8192
+
+
+def test_run_torch_matches_bruteforce_and_f32():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((6, 128)).astype(np.float32)
+    w = rng.standard_normal((5, 128)).astype(np.float32)
+    qa, sa = oq.quant_rows(x, "fp8")
+    qb, sb = oq.quant_rows(w, "fp8")
+    da = on.e4m3fn_decode(qa).astype(np.float64) * sa[:, None]
+    db = on.e4m3fn_decode(qb).astype(np.float64) * sb[:, None]
+    ref = og.run_torch(qa, qb, sa, sb, "fp8", "f64")
+    assert np.allclose(ref, _brute(da, db), rtol=1e-6, atol=1e-6)
+    f32 = og.run_torch(qa, qb, sa, sb, "fp8", "f32")
+    tt = torch.mm(torch.from_numpy(on.e4m3fn_decode(qa)) * torch.from_numpy(sa)[:, None],
+                  (torch.from_numpy(on.e4m3fn_decode(qb)) * torch.from_numpy(sb)[:, None]).T).numpy()
+    assert np.allclose(f32, tt, rtol=1e-5, atol=1e-5)
+
+
+def test_epilogue_int_matches_torch():
+    rng = np.random.default_rng(7)
+    acc = rng.integers(-2 ** 26, 2 ** 26, (16, 32)).astype(np.int32)
+    sa = rng.random(16).astype(np.float32) * 0.01
+    sb = rng.random(32).astype(np.float32) * 0.01
+    ref = ((torch.from_numpy(acc).float() * torch.from_numpy(sa)[:, None]) * torch.from_numpy(sb)[None, :])
+    ref = ref.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(og.epilogue_int_bf16(acc, sa, sb), ref)
+
+
+def test_blockscale_two_formulations_agree():
+    rng = np.random.default_rng(8)
+    M, N, K = 8, 272, 384  # N not a multiple of 128 -> last scale block partial
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    qx, sx = oq.quant_blocks(x, 1, 128)
+    wp = np.concatenate([w, np.zeros(((-N) % 128, K), np.float32)])
+    qw, sw = oq.quant_blocks(wp, 128, 128)
+    qw = qw[:N]
+    a = og.run_torch_blockscale(qx, qw, sx, sw, "f64")
+    b = og.blockscale_per_block(qx, qw, sx, sw)
+    # the reference rounds each dequantized element to fp32 before the product; the
+    # per-block form scales exact partial sums: they agree to fp32 rounding
+    assert np.allclose(a, b, rtol=1e-5, atol=1e-4)
+    # uniform per-row / per-column scales reduce blockscale to the per-token GEMM
+    sx_u = np.repeat(sx[:, :1], K // 128, axis=1)
+    sw_u = np.repeat(sw[:, :1], K // 128, axis=1)
+    c = og.run_torch_blockscale(qx, qw, sx_u, sw_u, "f64")
+    sbn = sw_u[np.arange(N) // 128, 0]
+    d = og.run_torch(qx, qw, sx_u[:, 0], sbn, "fp8", "f64")
+    assert np.allclose(c, d, rtol=1e-9, atol=1e-9)
+
+
+def test_bar_rejects_planted_mistakes():
+    """Plausible kernel mistakes, planted in the oracle, must fail the acceptance bar."""
+    rng = np.random.default_rng(9)
+    M, N, K = 32, 64, 512
+    qa, sa = oq.quant_rows(rng.standard_normal((M, K)).astype(np.float32), "fp8")
+    qb, sb = oq.quant_rows(rng.standard_normal((N, K)).astype(np.float32), "fp8")
+    ref = og.run_torch(qa, qb, sa, sb, "fp8", "f64")
+    assert og.within_bar(og.run_torch(qa, qb, sa, sb, "fp8", "f32"), ref)[0]
+    bad = {
+        "dropped_scale_b": og.run_torch(qa, qb, sa, np.ones_like(sb), "fp8", "f64"),
+        "swapped_scales": og.run_torch(qa, qb, sb[:M], sa.repeat(2)[:N], "fp8", "f64"),
+        "sign": -ref,
+        "last_k_tile_dropped": og.run_torch(qa[:, :K - 128], qb[:, :K - 128], sa, sb, "fp8", "f64"),
+        "k_chunks_misaligned": og.run_torch(qa, np.roll(qb, 16, axis=1), sa, sb, "fp8", "f64"),
+        "columns_shifted": np.roll(ref, 1, axis=1),
+    }
+    for name, out in bad.items():
+        assert not og.within_bar(out, ref)[0], name
+    # blockscale: A scale indexed [m][kb] instead of the transposed layout
+    x = rng.standard_normal((128, 256)).astype(np.float32)
+    w = rng.standard_normal((128, 256)).astype(np.float32)
+    qx, sx = oq.quant_blocks(x, 1, 128)
+    qw, sw = oq.quant_blocks(w, 128, 128)
+    good = og.run_torch_blockscale(qx, qw, sx, sw, "f64")
+    wrong = og.run_torch_blockscale(qx, qw, sx.T.reshape(sx.shape), sw, "f64")
+    assert not og.within_bar(wrong, good)[0]
