@@ -38,10 +38,12 @@ struct Shape {
   int bm, bn, threads;  // main: workgroup tile; decode: bm = 16*MR rows, bn = 16*NBW cols
 };
 
-#define MAIN_SHAPES(X)        \
-  X(256, 256, 2, 4)           \
-  X(128, 256, 2, 4)           \
-  X(128, 128, 2, 2)           \
+#define MAIN_SHAPES(X) \
+  X(256, 256, 2, 2)    \
+  X(256, 256, 2, 4)    \
+  X(256, 256, 4, 2)    \
+  X(128, 256, 2, 2)    \
+  X(128, 128, 2, 2)    \
   X(64, 128, 1, 4)
 
 #define DECODE_SHAPES(X) \
@@ -58,6 +60,9 @@ const Shape kShapes[] = {
 #undef DS
 };
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+#define COUNT(...) +1
+constexpr int kFirstDecode = 0 MAIN_SHAPES(COUNT);
+#undef COUNT
 
 // One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
@@ -96,22 +101,22 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   (void)K;
   (void)kind;
   (void)epi;
-  if (M <= 16) return 4;
-  if (M <= 32) return 5;
-  if (M <= 64) return 6;
+  if (M <= 16) return kFirstDecode;
+  if (M <= 32) return kFirstDecode + 1;
+  if (M <= 64) return kFirstDecode + 2;
   // main family: largest tile that still gives every CU work
-  for (int v = 0; v < 4; ++v) {
+  for (int v = 0; v < kFirstDecode; ++v) {
     const long wg = (long)((M + kShapes[v].bm - 1) / kShapes[v].bm) * ((N + kShapes[v].bn - 1) / kShapes[v].bn);
     if (wg >= 240) return v;
   }
-  return 3;
+  return kFirstDecode - 1;
 }
 
 int check_common(const void* c, const void* a, const void* b, int M, int N, int K, int variant) {
   if (M < 0 || N <= 0 || K <= 0) return fail(hipErrorInvalidValue, "invalid sizes M=%d N=%d K=%d", M, N, K);
   if (N % 16 != 0) return fail(hipErrorInvalidValue, "N=%d must be a multiple of 16 (preshuffle block)", N);
   if (K % 128 != 0) return fail(hipErrorInvalidValue, "K=%d must be a multiple of 128 (K tile)", K);
-  if ((long)M * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N >= (1L << 31))
+  if ((long)(M + 256) * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N >= (1L << 31))
     return fail(hipErrorInvalidValue, "operand too large for 32-bit element offsets (M=%d N=%d K=%d)", M, N, K);
   if (M > 0 && (!c || !a || !b)) return fail(hipErrorInvalidValue, "null tensor pointer");
   if (variant < -1 || variant >= kNumShapes) return fail(hipErrorInvalidValue, "unknown variant %d", variant);

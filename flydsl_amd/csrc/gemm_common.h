@@ -80,6 +80,19 @@ __device__ __forceinline__ typename OutT<BF16>::type cvt_out(float v) {
   return static_cast<typename OutT<BF16>::type>(v);
 }
 
+// Four consecutive outputs (fp32) -> one 8-byte store of bf16/fp16 at element idx.
+template <bool BF16>
+__device__ __forceinline__ void store_out4(void* c, size_t idx, const float (&v)[4]) {
+  typedef typename OutT<BF16>::type OT;
+  typedef OT OT4 __attribute__((ext_vector_type(4)));
+  OT4 o;
+  o.x = cvt_out<BF16>(v[0]);
+  o.y = cvt_out<BF16>(v[1]);
+  o.z = cvt_out<BF16>(v[2]);
+  o.w = cvt_out<BF16>(v[3]);
+  *(OT4*)((OT*)c + idx) = o;
+}
+
 struct GemmArgs {
   void* c;            // output [M][N] bf16/fp16, or int32/fp32 for EPI_RAW
   const uint8_t* a;   // [M][K]

@@ -3,26 +3,34 @@
 //   C[M][N] = epilogue( sum_k A[m][k] * B[n][k] )
 //
 // Workgroup tile BM x BN, K tile 128.  WM x WN waves; each wave owns a (BM/WM) x (BN/WN)
-// block of 16x16 MFMA tiles.  Per K tile every thread moves its share of A and B
-// global -> registers (16-byte loads, issued one tile ahead) -> LDS; the next tile's loads
-// are in flight while the current tile's MFMAs run.  One barrier per K tile.
+// block of 16x16 MFMA tiles.  Operands go global -> LDS with the gfx950 LDS-DMA load
+// (buffer_load_dwordx4 ... lds: each lane fetches 16 bytes from its own offset and the wave
+// writes 64 x 16 contiguous bytes of LDS), so no registers are spent on staging.  Two LDS
+// stages (ping/pong): while the MFMAs consume one stage the DMA of the next K tile fills
+// the other.  One barrier per K tile.
 //
 // LDS per stage:
 //   A: row-major [BM][128 B]; the 16-byte chunk c of row r sits at chunk slot
-//      c ^ ((r >> 1) & 7), so the 16 lanes that read one chunk column of 16 rows hit
-//      16 distinct 16-byte bank groups (64 banks x 4 B), and the 8 threads that write one
-//      row write one 128-byte line.
+//      c ^ ((r >> 1) & 7).  One DMA instruction fills 8 rows (1 KB): lane l brings the
+//      chunk that belongs in slot (l % 8) of row (l / 8), so each wave load reads eight
+//      whole 128-byte row segments of A, and the 16 lanes that later read one chunk column
+//      of 16 consecutive rows hit 16 distinct 16-byte bank groups (64 banks x 4 B).
 //   B: the preshuffled bytes copied verbatim: per 16-column block a 2 KB run
 //      [chunk 0..7][col 0..15][16 B] (INT4: 1 KB [chunk][col][8 B]); lanes that read one
 //      chunk read 256 (128) contiguous bytes.
 #pragma once
 #include "gemm_common.h"
 
+#ifndef FLY_SCHED
+#define FLY_SCHED 1
+#endif
+
 namespace flygemm {
 
-template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16>
+template <int BM, int BN, int WM, int WN, int KIND>
 struct MainCfg {
-  static constexpr int NT = WM * WN * 64;
+  static constexpr int NW = WM * WN;
+  static constexpr int NT = NW * 64;
   static constexpr int TM = BM / WM;
   static constexpr int TN = BN / WN;
   static constexpr int MR = TM / 16;
@@ -31,11 +39,10 @@ struct MainCfg {
   static constexpr int B_BLK = (KIND == KIND_INT4) ? 1024 : 2048;  // bytes per 16 cols per K tile
   static constexpr int B_BYTES = (BN / 16) * B_BLK;
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int A_LD = A_BYTES / (NT * 16);
-  static constexpr int B_LD = B_BYTES / (NT * 16);
-  static constexpr int LDS = 2 * STAGE;
+  static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB DMA instructions per wave per tile
+  static constexpr int B_DMA = B_BYTES / 1024 / NW;
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
-  static_assert(A_BYTES % (NT * 16) == 0 && B_BYTES % (NT * 16) == 0, "tile not divisible into 16B loads");
+  static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "tile not divisible into wave DMAs");
 };
 
 // Workgroup id -> (tile_m, tile_n).  Workgroups are handed to the 8 XCDs round-robin;
@@ -55,11 +62,30 @@ __device__ __forceinline__ void tile_coords(int nbm, int nbn, int& bm, int& bn) 
   bn = r / gsz;
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw buffer resource over [base, base + bytes); dword3 0x00020000 = 32-bit data format,
+// the gfx9 setting for untyped raw buffer access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, 0x00020000);
+}
+
+// One wave-wide LDS-DMA load: lane l reads 16 bytes at voffset(l) + soffset of the buffer
+// and the wave writes them to lds_wave_base + 16*l.  Lanes whose voffset lies outside the
+// buffer write zeros.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_wave_base, uint32_t voffset,
+                                      uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_wave_base, 16, voffset, soffset, 0, 0);
+}
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) {
-  using C = MainCfg<BM, BN, WM, WN, KIND, EPI, OUT_BF16>;
-  constexpr int MR = C::MR, NR = C::NR;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
+  using C = MainCfg<BM, BN, WM, WN, KIND>;
+  constexpr int MR = C::MR, NR = C::NR, NW = C::NW;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
 
   const int M = p.M, N = p.N, K = p.K;
   const int nbm = (M + BM - 1) / BM;
@@ -73,50 +99,44 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int l16 = lane & 15;
   const int lq = lane >> 4;  // 0..3
 
-  // ---- global source pointers for this thread's 16-byte pieces (advanced per K tile) ----
-  const uint8_t* ga[C::A_LD];
-  int la[C::A_LD];
+  // ---- DMA addressing ----
+  // A: buffer resource over the rows still ahead of this K tile; the per-lane VGPR offset
+  // carries the row, so rows >= M fall outside num_records and read as zero.
+  // B: one resource over the whole buffer; the 16-column block offset is wave-uniform
+  // (SGPR soffset), column blocks past N are clamped to the last one.
+  uint32_t va[C::A_DMA];
 #pragma unroll
-  for (int j = 0; j < C::A_LD; ++j) {
-    const int q = tid + j * C::NT;
-    const int row = q >> 3;
-    const int c = q & 7;
-    const int grow = min(m0 + row, M - 1);
-    ga[j] = p.a + (size_t)grow * K + c * 16;
-    la[j] = row * KT + ((c ^ ((row >> 1) & 7)) << 4);
+  for (int j = 0; j < C::A_DMA; ++j) {
+    const int row = m0 + (wave + j * NW) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    va[j] = (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16);
   }
-  const uint8_t* gb[C::B_LD];
-  int lb[C::B_LD];
-  constexpr int CH_PER_BLK = C::B_BLK / 16;
+  constexpr int PARTS = C::B_BLK / 1024;
+  const uint32_t vb = (uint32_t)lane * 16u;
+  uint32_t sbo[C::B_DMA];
 #pragma unroll
-  for (int j = 0; j < C::B_LD; ++j) {
-    const int q = tid + j * C::NT;
-    const int nbl = q / CH_PER_BLK;
-    const int w = q % CH_PER_BLK;
-    const int nb = min(n0 / 16 + nbl, nblk_max);
-    gb[j] = p.b + (size_t)nb * (C::B_BLK / KT) * (size_t)K + w * 16;  // block nb starts at nb*16*K (int4: nb*8*K)
-    lb[j] = nbl * C::B_BLK + w * 16;
+  for (int j = 0; j < C::B_DMA; ++j) {
+    const int q = wave + j * NW;
+    const int nb = min(n0 / 16 + q / PARTS, nblk_max);
+    sbo[j] = __builtin_amdgcn_readfirstlane((uint32_t)nb * (uint32_t)(C::B_BLK / KT) * (uint32_t)K +
+                                            (uint32_t)((q % PARTS) * 1024));
   }
+  const int b_bytes = (KIND == KIND_INT4) ? (N / 2) * K : N * K;
+  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(p.b, b_bytes);
 
-  i32x4 ra[C::A_LD], rb[C::B_LD];
-  auto load_tile = [&](int kt) {
+  auto issue = [&](uint8_t* s, int kt) {
+    const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(p.a + (size_t)kt * KT, M * K - kt * KT);
 #pragma unroll
-    for (int j = 0; j < C::A_LD; ++j) ra[j] = *(const i32x4*)(ga[j] + (size_t)kt * KT);
+    for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, va[j], 0);
 #pragma unroll
-    for (int j = 0; j < C::B_LD; ++j) rb[j] = *(const i32x4*)(gb[j] + (size_t)kt * C::B_BLK);
-  };
-  auto store_tile = [&](int stage) {
-    uint8_t* s = smem + stage * C::STAGE;
-#pragma unroll
-    for (int j = 0; j < C::A_LD; ++j) *(i32x4*)(s + la[j]) = ra[j];
-#pragma unroll
-    for (int j = 0; j < C::B_LD; ++j) *(i32x4*)(s + C::A_BYTES + lb[j]) = rb[j];
+    for (int j = 0; j < C::B_DMA; ++j)
+      dma16(rsrc_b, s + C::A_BYTES + (wave + j * NW) * 1024, vb, sbo[j] + (uint32_t)kt * C::B_BLK);
   };
 
   typedef typename std::conditional<KIND == KIND_FP8, f32x4, i32x4>::type AccT;
@@ -126,41 +146,36 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < NR; ++j) acc[i][j] = AccT{0, 0, 0, 0};
 
-  // blockscale: per-row A scales (4 rows per mi) and per-column-block B scales
-  float sa_cur[MR][4], sb_cur[NR], sa_nxt[MR][4], sb_nxt[NR];
-  auto load_scales = [&](int kt, float (&sa_o)[MR][4], float (&sb_o)[NR]) {
+  // blockscale: the A scale of this lane's row in each MFMA row block and the B scale of
+  // each 16-column block, for one K tile
+  float sa_t[MR], sb_t[NR];
+  auto load_scales = [&](int kt) {
     if constexpr (EPI == EPI_BLOCK) {
-      const int nkb = nk;
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = min(m0 + wm * C::TM + mi * 16 + lq * 4 + i, M - 1);
-          sa_o[mi][i] = p.sa[(size_t)kt * M + row];
-        }
+        sa_t[mi] = p.sa[(size_t)kt * M + min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
 #pragma unroll
       for (int ni = 0; ni < NR; ++ni) {
         const int col = min(n0 + wn * C::TN + ni * 16, N - 1);
-        sb_o[ni] = p.sb[(size_t)(col >> 7) * nkb + kt];
+        sb_t[ni] = p.sb[(size_t)(col >> 7) * nk + kt];
       }
     }
   };
 
-  load_scales(0, sa_cur, sb_cur);
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  // A fragment of MFMA row mi: lane holds 16-byte chunks lq and lq+4 of its row
+  auto load_a = [&](const uint8_t* sA, int mi, i32x4& lo, i32x4& hi) {
+    const int row = wm * C::TM + mi * 16 + l16;
+    const int sw = (row >> 1) & 7;
+    lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
+    hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
+  };
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = (kt + 1) < nk;
-    if (more) {
-      load_scales(kt + 1, sa_nxt, sb_nxt);
-      load_tile(kt + 1);
-    }
-    const uint8_t* sA = smem + cur * C::STAGE;
+  // One K tile.  The A fragment of row mi+1 is requested before the MFMAs of row mi are
+  // issued, so its LDS latency hides behind NR MFMAs.
+  auto compute = [&](const uint8_t* sA) {
     const uint8_t* sB = sA + C::A_BYTES;
-
+    i32x4 alo, ahi;
+    load_a(sA, 0, alo, ahi);
     if constexpr (KIND == KIND_FP8) {
       i32x8 bf[NR];
 #pragma unroll
@@ -172,24 +187,28 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       }
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) {
-        const int row = wm * C::TM + mi * 16 + l16;
-        const int sw = (row >> 1) & 7;
-        const i32x4 lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
-        const i32x4 hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
-        const i32x8 af = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const i32x8 af = i32x8{alo.x, alo.y, alo.z, alo.w, ahi.x, ahi.y, ahi.z, ahi.w};
+        if (mi + 1 < MR) load_a(sA, mi + 1, alo, ahi);
         if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
           for (int ni = 0; ni < NR; ++ni) {
-            const f32x4 part = mfma_fp8(af, bf[ni], f32x4{0.f, 0.f, 0.f, 0.f});
-            const float s = sb_cur[ni];
-            acc[mi][ni].x = __builtin_fmaf(part.x, sa_cur[mi][0] * s, acc[mi][ni].x);
-            acc[mi][ni].y = __builtin_fmaf(part.y, sa_cur[mi][1] * s, acc[mi][ni].y);
-            acc[mi][ni].z = __builtin_fmaf(part.z, sa_cur[mi][2] * s, acc[mi][ni].z);
-            acc[mi][ni].w = __builtin_fmaf(part.w, sa_cur[mi][3] * s, acc[mi][ni].w);
+            const f32x4 part = mfma_fp8(bf[ni], af, f32x4{0.f, 0.f, 0.f, 0.f});
+            const float s = sa_t[mi] * sb_t[ni];
+            acc[mi][ni].x = __builtin_fmaf(part.x, s, acc[mi][ni].x);
+            acc[mi][ni].y = __builtin_fmaf(part.y, s, acc[mi][ni].y);
+            acc[mi][ni].z = __builtin_fmaf(part.z, s, acc[mi][ni].z);
+            acc[mi][ni].w = __builtin_fmaf(part.w, s, acc[mi][ni].w);
           }
         } else {
+#if FLY_SCHED
+          // the next row's A reads stay ahead of this row's MFMAs
+          __builtin_amdgcn_sched_barrier(0);
+#endif
 #pragma unroll
-          for (int ni = 0; ni < NR; ++ni) acc[mi][ni] = mfma_fp8(af, bf[ni], acc[mi][ni]);
+          for (int ni = 0; ni < NR; ++ni) acc[mi][ni] = mfma_fp8(bf[ni], af, acc[mi][ni]);
+#if FLY_SCHED
+          __builtin_amdgcn_sched_barrier(0);
+#endif
         }
       }
     } else {
@@ -208,61 +227,66 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       }
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) {
-        const int row = wm * C::TM + mi * 16 + l16;
-        const int sw = (row >> 1) & 7;
-        const i32x4 lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
-        const i32x4 hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
+        const i32x4 lo = alo, hi = ahi;
+        if (mi + 1 < MR) load_a(sA, mi + 1, alo, ahi);
 #pragma unroll
         for (int ni = 0; ni < NR; ++ni) {
-          acc[mi][ni] = mfma_i8(lo, bl[ni], acc[mi][ni]);
-          acc[mi][ni] = mfma_i8(hi, bh[ni], acc[mi][ni]);
+          acc[mi][ni] = mfma_i8(bl[ni], lo, acc[mi][ni]);
+          acc[mi][ni] = mfma_i8(bh[ni], hi, acc[mi][ni]);
         }
       }
     }
+  };
 
-    if (more) {
-      store_tile(cur ^ 1);
-      if constexpr (EPI == EPI_BLOCK) {
-#pragma unroll
-        for (int mi = 0; mi < MR; ++mi)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sa_cur[mi][i] = sa_nxt[mi][i];
-#pragma unroll
-        for (int ni = 0; ni < NR; ++ni) sb_cur[ni] = sb_nxt[ni];
-      }
-    }
-    __syncthreads();
+  // ---- main loop: DMA of tile kt+1 overlaps the MFMAs of tile kt ----
+  // (one loop body for both stages: two unrolled bodies would make the accumulators
+  // alternate between two register sets)
+  issue(lds0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_dma();
+    __syncthreads();  // tile kt has landed; every wave is done reading the other stage
+    uint8_t* cur = (kt & 1) ? lds1 : lds0;
+    uint8_t* nxt = (kt & 1) ? lds0 : lds1;
+    load_scales(kt);
+    if (kt + 1 < nk) issue(nxt, kt + 1);
+    compute(cur);
   }
 
-  // ---- epilogue: lane holds rows (lq*4 + i), column l16 of every 16x16 tile ----
-  typedef typename OutT<OUT_BF16>::type OT;
+  // ---- epilogue ----
+  // B is the MFMA's first operand, so each 16x16 accumulator tile is C transposed: lane
+  // (lq, l16) holds row l16, columns 4*lq .. 4*lq+3 -- one 8-byte bf16/fp16 store (16 bytes
+  // for raw accumulators) per tile.  All scale loads are issued before the first store.
+  float sa_e[MR];
+  f32x4 sb_e[NR];
+  if constexpr (EPI == EPI_ROWCOL) {
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) sa_e[mi] = p.sa[min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
+#pragma unroll
+    for (int ni = 0; ni < NR; ++ni)
+      sb_e[ni] = *(const f32x4*)(p.sb + min(n0 + wn * C::TN + ni * 16 + lq * 4, N - 4));
+  }
 #pragma unroll
   for (int mi = 0; mi < MR; ++mi) {
+    const int row = m0 + wm * C::TM + mi * 16 + l16;
+    if (row >= M) continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = m0 + wm * C::TM + mi * 16 + lq * 4 + i;
-      if (row >= M) continue;
-      float s_a = 1.f;
-      if constexpr (EPI == EPI_ROWCOL) s_a = p.sa[row];
+    for (int ni = 0; ni < NR; ++ni) {
+      const int col = n0 + wn * C::TN + ni * 16 + lq * 4;
+      if (col >= N) continue;
+      const size_t idx = (size_t)row * N + col;
+      if constexpr (EPI == EPI_RAW) {
+        *(AccT*)((typename std::conditional<KIND == KIND_FP8, float, int>::type*)p.c + idx) = acc[mi][ni];
+      } else {
+        float v[4];
 #pragma unroll
-      for (int ni = 0; ni < NR; ++ni) {
-        const int col = n0 + wn * C::TN + ni * 16 + l16;
-        if (col >= N) continue;
-        const size_t idx = (size_t)row * N + col;
-        if constexpr (EPI == EPI_RAW) {
+        for (int r = 0; r < 4; ++r) {
           if constexpr (KIND == KIND_FP8)
-            ((float*)p.c)[idx] = acc[mi][ni][i];
+            v[r] = acc[mi][ni][r];
           else
-            ((int*)p.c)[idx] = acc[mi][ni][i];
-        } else {
-          float v;
-          if constexpr (KIND == KIND_FP8)
-            v = acc[mi][ni][i];
-          else
-            v = (float)acc[mi][ni][i];
-          if constexpr (EPI == EPI_ROWCOL) v = (v * s_a) * p.sb[col];
-          ((OT*)p.c)[idx] = cvt_out<OUT_BF16>(v);
+            v[r] = (float)acc[mi][ni][r];
+          if constexpr (EPI == EPI_ROWCOL) v[r] = (v[r] * sa_e[mi]) * sb_e[ni][r];
         }
+        store_out4<OUT_BF16>(p.c, idx, v);
       }
     }
   }
