@@ -9,6 +9,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "../../include/flygemm.h"
 #include "gemm_decode.h"
 #include "gemm_main.h"
@@ -47,9 +51,14 @@ struct Shape {
   X(64, 128, 1, 4)
 
 #define DECODE_SHAPES(X) \
-  X(1, 1, 4, 4)          \
-  X(2, 1, 4, 2)          \
-  X(4, 1, 4, 2)
+  X(1, 1, 8, 4)          \
+  X(1, 2, 8, 4)          \
+  X(1, 4, 8, 2)          \
+  X(1, 7, 8, 2)          \
+  X(2, 1, 8, 4)          \
+  X(2, 2, 8, 2)          \
+  X(4, 1, 8, 2)          \
+  X(4, 2, 8, 2)
 
 const Shape kShapes[] = {
 #define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64},
@@ -101,9 +110,19 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   (void)K;
   (void)kind;
   (void)epi;
-  if (M <= 16) return kFirstDecode;
-  if (M <= 32) return kFirstDecode + 1;
-  if (M <= 64) return kFirstDecode + 2;
+  if (M <= 64) {
+    // decode family: fewest rows that cover M, then the most column blocks per workgroup
+    // that still leaves about one workgroup per CU
+    const int rows = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
+    const int nblk = N / 16;
+    int best = -1;
+    for (int v = kFirstDecode; v < kNumShapes; ++v) {
+      if (kShapes[v].bm != rows) continue;
+      const int nbw = kShapes[v].bn / 16;
+      if (best < 0 || (nblk / nbw >= 240 && nbw > kShapes[best].bn / 16)) best = v;
+    }
+    return best;
+  }
   // main family: largest tile that still gives every CU work
   for (int v = 0; v < kFirstDecode; ++v) {
     const long wg = (long)((M + kShapes[v].bm - 1) / kShapes[v].bm) * ((N + kShapes[v].bn - 1) / kShapes[v].bn);
@@ -112,11 +131,41 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   return kFirstDecode - 1;
 }
 
+// Persistent grid for the large-M kernel: as many workgroups as can be resident at once
+// (CUs x workgroups per CU), at most one per tile, and a multiple of 8 when it is smaller
+// than the tile count so every workgroup keeps to one XCD's share of the tiles.
+// Occupancy is queried once per kernel and cached.
+int persistent_grid(KernelFn fn, int threads, long ntiles, int* grid) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(e, "hipGetDevice: %s", hipGetErrorString(e));
+  int slots;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto key = std::make_pair(dev, (const void*)fn);
+    auto it = cache.find(key);
+    if (it == cache.end()) {
+      int ncu = 0, per_cu = 0;
+      e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e != hipSuccess) return fail(e, "device attribute query: %s", hipGetErrorString(e));
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)fn, threads, 0);
+      if (e != hipSuccess) return fail(e, "occupancy query: %s", hipGetErrorString(e));
+      it = cache.emplace(key, ncu * (per_cu > 0 ? per_cu : 1)).first;
+    }
+    slots = it->second;
+  }
+  long g = ntiles <= slots ? ntiles : (slots >= 8 ? slots - slots % 8 : slots);
+  *grid = (int)g;
+  return 0;
+}
+
 int check_common(const void* c, const void* a, const void* b, int M, int N, int K, int variant) {
   if (M < 0 || N <= 0 || K <= 0) return fail(hipErrorInvalidValue, "invalid sizes M=%d N=%d K=%d", M, N, K);
   if (N % 16 != 0) return fail(hipErrorInvalidValue, "N=%d must be a multiple of 16 (preshuffle block)", N);
   if (K % 128 != 0) return fail(hipErrorInvalidValue, "K=%d must be a multiple of 128 (K tile)", K);
-  if ((long)(M + 256) * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N >= (1L << 31))
+  if ((long)(M + 256) * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N * 4 >= (1L << 31))
     return fail(hipErrorInvalidValue, "operand too large for 32-bit element offsets (M=%d N=%d K=%d)", M, N, K);
   if (M > 0 && (!c || !a || !b)) return fail(hipErrorInvalidValue, "null tensor pointer");
   if (variant < -1 || variant >= kNumShapes) return fail(hipErrorInvalidValue, "unknown variant %d", variant);
@@ -133,7 +182,11 @@ int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, 
   if (!row) return fail(hipErrorInvalidValue, "unsupported combination kind=%d epilogue=%d", kind, epi);
   dim3 grid;
   if (s.family == FAM_MAIN) {
-    grid = dim3(((args.M + s.bm - 1) / s.bm) * ((args.N + s.bn - 1) / s.bn));
+    const long ntiles = (long)((args.M + s.bm - 1) / s.bm) * ((args.N + s.bn - 1) / s.bn);
+    int g = 0;
+    int rc = persistent_grid(row[v], s.threads, ntiles, &g);
+    if (rc) return rc;
+    grid = dim3(g);
   } else {
     grid = dim3((args.N + s.bn - 1) / s.bn);
   }

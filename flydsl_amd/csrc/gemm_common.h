@@ -93,6 +93,19 @@ __device__ __forceinline__ void store_out4(void* c, size_t idx, const float (&v)
   *(OT4*)((OT*)c + idx) = o;
 }
 
+// Four fp32 outputs -> four bf16/fp16 packed in two dwords (for one 8-byte store).
+template <bool BF16>
+__device__ __forceinline__ i32x2 pack_out4(const float (&v)[4]) {
+  typedef typename OutT<BF16>::type OT;
+  typedef OT OT4 __attribute__((ext_vector_type(4)));
+  OT4 o;
+  o.x = cvt_out<BF16>(v[0]);
+  o.y = cvt_out<BF16>(v[1]);
+  o.z = cvt_out<BF16>(v[2]);
+  o.w = cvt_out<BF16>(v[3]);
+  return __builtin_bit_cast(i32x2, o);
+}
+
 struct GemmArgs {
   void* c;            // output [M][N] bf16/fp16, or int32/fp32 for EPI_RAW
   const uint8_t* a;   // [M][K]

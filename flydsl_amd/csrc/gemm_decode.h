@@ -5,12 +5,14 @@
 // waves split K (wave w takes K tiles w, w+NW, ...), each wave keeps UNROLL K tiles of
 // loads in flight, and the NW partial accumulators are summed through LDS before the
 // fused epilogue.  The reduction is inside the workgroup: no workspace, no atomics, and
-// the int32 sums stay exact.
+// the int32 sums stay exact.  Owning several column blocks per workgroup divides the A
+// traffic (one A fragment serves NBW blocks).
 //
 // Per K tile a lane loads, for every owned 16-column block, the two 16-byte chunks
 // (lane/16) and (lane/16)+4 of column (lane%16) -- the preshuffled layout makes each
-// wave-wide load one contiguous 1 KB read -- and the matching two chunks of A row
-// (lane%16).
+// wave-wide load one contiguous 1 KB read, issued non-temporal because B is used once --
+// and the matching two chunks of A row (lane%16).  As in the large-M kernel, B is the
+// MFMA's first operand, so a lane ends with row (lane%16) and four consecutive columns.
 #pragma once
 #include "gemm_common.h"
 
@@ -40,7 +42,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
 
   const uint8_t* arow[MR];
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) arow[mi] = p.a + (size_t)min(mi * 16 + l16, M - 1) * K;
+  for (int mi = 0; mi < MR; ++mi) arow[mi] = p.a + (size_t)min(mi * 16 + l16, M - 1) * K + lq * 16;
   const uint8_t* bblk[NBW];
 #pragma unroll
   for (int j = 0; j < NBW; ++j) {
@@ -62,19 +64,18 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       if (kt < nk) {
 #pragma unroll
         for (int j = 0; j < NBW; ++j) {
+          const uint8_t* src = bblk[j] + (size_t)kt * B_BLK;
           if constexpr (KIND == KIND_INT4) {
-            const uint8_t* src = bblk[j] + (size_t)kt * B_BLK;
             b4lo[u][j] = __builtin_nontemporal_load((const i32x2*)src);
             b4hi[u][j] = __builtin_nontemporal_load((const i32x2*)(src + 512));
           } else {
-            const uint8_t* src = bblk[j] + (size_t)kt * B_BLK;
             blo[u][j] = __builtin_nontemporal_load((const i32x4*)src);
             bhi[u][j] = __builtin_nontemporal_load((const i32x4*)(src + 1024));
           }
         }
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) {
-          const uint8_t* src = arow[mi] + (size_t)kt * KT + lq * 16;
+          const uint8_t* src = arow[mi] + (size_t)kt * KT;
           alo[u][mi] = *(const i32x4*)src;
           ahi[u][mi] = *(const i32x4*)(src + 64);
         }
@@ -89,25 +90,22 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
           for (int mi = 0; mi < MR; ++mi) {
             const i32x8 af = i32x8{alo[u][mi].x, alo[u][mi].y, alo[u][mi].z, alo[u][mi].w,
                                    ahi[u][mi].x, ahi[u][mi].y, ahi[u][mi].z, ahi[u][mi].w};
-            float sa4[4] = {0.f, 0.f, 0.f, 0.f};
-            if constexpr (EPI == EPI_BLOCK) {
-#pragma unroll
-              for (int i = 0; i < 4; ++i) sa4[i] = p.sa[(size_t)kt * M + min(mi * 16 + lq * 4 + i, M - 1)];
-            }
+            float s_a = 0.f;
+            if constexpr (EPI == EPI_BLOCK) s_a = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
 #pragma unroll
             for (int j = 0; j < NBW; ++j) {
               const i32x8 bf = i32x8{blo[u][j].x, blo[u][j].y, blo[u][j].z, blo[u][j].w,
                                      bhi[u][j].x, bhi[u][j].y, bhi[u][j].z, bhi[u][j].w};
               if constexpr (EPI == EPI_BLOCK) {
                 const int col = min((nb0 + j) * 16, N - 1);
-                const float s = p.sb[(size_t)(col >> 7) * nk + kt];
-                const f32x4 part = mfma_fp8(af, bf, f32x4{0.f, 0.f, 0.f, 0.f});
-                acc[mi][j].x = __builtin_fmaf(part.x, sa4[0] * s, acc[mi][j].x);
-                acc[mi][j].y = __builtin_fmaf(part.y, sa4[1] * s, acc[mi][j].y);
-                acc[mi][j].z = __builtin_fmaf(part.z, sa4[2] * s, acc[mi][j].z);
-                acc[mi][j].w = __builtin_fmaf(part.w, sa4[3] * s, acc[mi][j].w);
+                const float s = s_a * p.sb[(size_t)(col >> 7) * nk + kt];
+                const f32x4 part = mfma_fp8(bf, af, f32x4{0.f, 0.f, 0.f, 0.f});
+                acc[mi][j].x = __builtin_fmaf(part.x, s, acc[mi][j].x);
+                acc[mi][j].y = __builtin_fmaf(part.y, s, acc[mi][j].y);
+                acc[mi][j].z = __builtin_fmaf(part.z, s, acc[mi][j].z);
+                acc[mi][j].w = __builtin_fmaf(part.w, s, acc[mi][j].w);
               } else {
-                acc[mi][j] = mfma_fp8(af, bf, acc[mi][j]);
+                acc[mi][j] = mfma_fp8(bf, af, acc[mi][j]);
               }
             }
           }
@@ -124,8 +122,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
             }
 #pragma unroll
             for (int mi = 0; mi < MR; ++mi) {
-              acc[mi][j] = mfma_i8(alo[u][mi], bl, acc[mi][j]);
-              acc[mi][j] = mfma_i8(ahi[u][mi], bh, acc[mi][j]);
+              acc[mi][j] = mfma_i8(bl, alo[u][mi], acc[mi][j]);
+              acc[mi][j] = mfma_i8(bh, ahi[u][mi], acc[mi][j]);
             }
           }
         }
@@ -133,53 +131,42 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     }
   }
 
-  // ---- split-K reduction over the NW waves through LDS ----
-  __shared__ __attribute__((aligned(16))) AccT red[NW > 1 ? (NW - 1) : 1][MR * NBW][64];
-  if constexpr (NW > 1) {
-    if (wave > 0) {
+  // ---- split-K reduction over the NW waves through LDS: column block j is summed and
+  // written out by wave j % NW ----
+  __shared__ __attribute__((aligned(16))) AccT red[NW][MR * NBW][64];
 #pragma unroll
-      for (int mi = 0; mi < MR; ++mi)
+  for (int mi = 0; mi < MR; ++mi)
 #pragma unroll
-        for (int j = 0; j < NBW; ++j) red[wave - 1][mi * NBW + j][lane] = acc[mi][j];
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int w = 0; w < NW - 1; ++w)
-#pragma unroll
-      for (int mi = 0; mi < MR; ++mi)
-#pragma unroll
-        for (int j = 0; j < NBW; ++j) acc[mi][j] += red[w][mi * NBW + j][lane];
-  }
+    for (int j = 0; j < NBW; ++j) red[wave][mi * NBW + j][lane] = acc[mi][j];
+  __syncthreads();
 
-  typedef typename OutT<OUT_BF16>::type OT;
+  typedef typename std::conditional<KIND == KIND_FP8 || EPI == EPI_BLOCK, float, int>::type AccE;
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) {
+  for (int j = 0; j < NBW; ++j) {
+    if (j % NW != wave) continue;
+    const int col = (nb0 + j) * 16 + lq * 4;
+    if (col >= N) continue;
+    f32x4 sb4 = f32x4{1.f, 1.f, 1.f, 1.f};
+    if constexpr (EPI == EPI_ROWCOL) sb4 = *(const f32x4*)(p.sb + col);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = mi * 16 + lq * 4 + i;
+    for (int mi = 0; mi < MR; ++mi) {
+      AccT s = red[0][mi * NBW + j][lane];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) s += red[w][mi * NBW + j][lane];
+      const int row = mi * 16 + l16;
       if (row >= M) continue;
-      float s_a = 1.f;
-      if constexpr (EPI == EPI_ROWCOL) s_a = p.sa[row];
+      const size_t idx = (size_t)row * N + col;
+      if constexpr (EPI == EPI_RAW) {
+        *(AccT*)((AccE*)p.c + idx) = s;
+      } else {
+        const float s_a = (EPI == EPI_ROWCOL) ? p.sa[row] : 1.f;
+        float v[4];
 #pragma unroll
-      for (int j = 0; j < NBW; ++j) {
-        const int col = (nb0 + j) * 16 + l16;
-        if (col >= N) continue;
-        const size_t idx = (size_t)row * N + col;
-        if constexpr (EPI == EPI_RAW) {
-          if constexpr (KIND == KIND_FP8)
-            ((float*)p.c)[idx] = acc[mi][j][i];
-          else
-            ((int*)p.c)[idx] = acc[mi][j][i];
-        } else {
-          float v;
-          if constexpr (KIND == KIND_FP8 || EPI == EPI_BLOCK)
-            v = acc[mi][j][i];
-          else
-            v = (float)acc[mi][j][i];
-          if constexpr (EPI == EPI_ROWCOL) v = (v * s_a) * p.sb[col];
-          ((OT*)p.c)[idx] = cvt_out<OUT_BF16>(v);
+        for (int r = 0; r < 4; ++r) {
+          v[r] = (float)s[r];
+          if constexpr (EPI == EPI_ROWCOL) v[r] = (v[r] * s_a) * sb4[r];
         }
+        *(i32x2*)((typename OutT<OUT_BF16>::type*)p.c + idx) = pack_out4<OUT_BF16>(v);
       }
     }
   }

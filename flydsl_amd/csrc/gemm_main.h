@@ -7,7 +7,8 @@
 // (buffer_load_dwordx4 ... lds: each lane fetches 16 bytes from its own offset and the wave
 // writes 64 x 16 contiguous bytes of LDS), so no registers are spent on staging.  Two LDS
 // stages (ping/pong): while the MFMAs consume one stage the DMA of the next K tile fills
-// the other.  One barrier per K tile.
+// the other.  One barrier per K tile.  The grid is persistent (about one workgroup per CU
+// slot); each workgroup walks its tiles as one continuous pipeline.
 //
 // LDS per stage:
 //   A: row-major [BM][128 B]; the 16-byte chunk c of row r sits at chunk slot
@@ -23,6 +24,9 @@
 
 #ifndef FLY_SCHED
 #define FLY_SCHED 1
+#endif
+#ifndef FLY_GROUP_M
+#define FLY_GROUP_M 8
 #endif
 
 namespace flygemm {
@@ -45,19 +49,20 @@ struct MainCfg {
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "tile not divisible into wave DMAs");
 };
 
-// Workgroup id -> (tile_m, tile_n).  Workgroups are handed to the 8 XCDs round-robin;
-// the remap gives each XCD a contiguous range of logical ids, and the grouped order walks
-// GROUP_M tile-rows at a time so neighbouring workgroups share A rows and B columns in L2.
-__device__ __forceinline__ void tile_coords(int nbm, int nbn, int& bm, int& bn) {
-  const int nblk = nbm * nbn;
-  int bid = blockIdx.x;
-  if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  constexpr int GROUP_M = 8;
+// Tile index -> (tile_m, tile_n).  Workgroups are handed to the 8 XCDs round-robin, and a
+// persistent workgroup b visits tiles b, b + G, ... with G a multiple of 8, so tile t runs
+// on XCD t % 8.  The remap gives each XCD a contiguous range of logical ids, and the
+// grouped order walks GROUP_M tile-rows at a time so tiles in flight together share A rows
+// and B columns in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int t, int ntiles, int nbm, int& bm, int& bn) {
+  const int nbn = ntiles / nbm;
+  if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+  constexpr int GROUP_M = FLY_GROUP_M;
   const int per_group = GROUP_M * nbn;
-  const int g = bid / per_group;
+  const int g = t / per_group;
   const int first_m = g * GROUP_M;
   const int gsz = min(nbm - first_m, GROUP_M);
-  const int r = bid - g * per_group;
+  const int r = t - g * per_group;
   bm = first_m + r % gsz;
   bn = r / gsz;
 }
@@ -80,6 +85,22 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_wav
 
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Wait until at most N (capped at 63, the counter's range) vector memory operations of this
+// wave are outstanding.  Values without a case here fall back to waiting for all of them.
+template <int N>
+__device__ __forceinline__ void wait_vmem_leaving() {
+  if constexpr (N >= 63)
+    asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
+  else if constexpr (N == 32)
+    asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+  else if constexpr (N == 16)
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if constexpr (N == 8)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) {
   using C = MainCfg<BM, BN, WM, WN, KIND>;
@@ -90,10 +111,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   const int M = p.M, N = p.N, K = p.K;
   const int nbm = (M + BM - 1) / BM;
   const int nbn = (N + BN - 1) / BN;
-  int bm, bn;
-  tile_coords(nbm, nbn, bm, bn);
-  const int m0 = bm * BM;
-  const int n0 = bn * BN;
+  const int ntiles = nbm * nbn;
   const int nk = K / KT;
   const int nblk_max = N / 16 - 1;
 
@@ -107,49 +125,44 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
 
   // ---- DMA addressing ----
   // A: buffer resource over the rows still ahead of this K tile; the per-lane VGPR offset
-  // carries the row, so rows >= M fall outside num_records and read as zero.
+  // carries the row, so rows >= M fall outside num_records and read as zero.  The swizzled
+  // chunk depends only on the row inside the tile (tile rows start at multiples of 16).
   // B: one resource over the whole buffer; the 16-column block offset is wave-uniform
   // (SGPR soffset), column blocks past N are clamped to the last one.
-  uint32_t va[C::A_DMA];
+  uint32_t va0[C::A_DMA];
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j) {
-    const int row = m0 + (wave + j * NW) * 8 + (lane >> 3);
-    const int c = (lane & 7) ^ ((row >> 1) & 7);
-    va[j] = (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16);
+    const int rloc = (wave + j * NW) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((rloc >> 1) & 7);
+    va0[j] = (uint32_t)rloc * (uint32_t)K + (uint32_t)(c * 16);
   }
   constexpr int PARTS = C::B_BLK / 1024;
   const uint32_t vb = (uint32_t)lane * 16u;
-  uint32_t sbo[C::B_DMA];
-#pragma unroll
-  for (int j = 0; j < C::B_DMA; ++j) {
-    const int q = wave + j * NW;
-    const int nb = min(n0 / 16 + q / PARTS, nblk_max);
-    sbo[j] = __builtin_amdgcn_readfirstlane((uint32_t)nb * (uint32_t)(C::B_BLK / KT) * (uint32_t)K +
-                                            (uint32_t)((q % PARTS) * 1024));
-  }
   const int b_bytes = (KIND == KIND_INT4) ? (N / 2) * K : N * K;
   const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(p.b, b_bytes);
 
-  auto issue = [&](uint8_t* s, int kt) {
+  auto issue = [&](uint8_t* s, int m0, int n0, int kt) {
     const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(p.a + (size_t)kt * KT, M * K - kt * KT);
+    const uint32_t mo = (uint32_t)m0 * (uint32_t)K;
 #pragma unroll
-    for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, va[j], 0);
+    for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, va0[j] + mo, 0);
 #pragma unroll
-    for (int j = 0; j < C::B_DMA; ++j)
-      dma16(rsrc_b, s + C::A_BYTES + (wave + j * NW) * 1024, vb, sbo[j] + (uint32_t)kt * C::B_BLK);
+    for (int j = 0; j < C::B_DMA; ++j) {
+      const int q = wave + j * NW;
+      const int nb = min(n0 / 16 + q / PARTS, nblk_max);
+      const uint32_t so = (uint32_t)nb * (uint32_t)(C::B_BLK / KT) * (uint32_t)K + (uint32_t)((q % PARTS) * 1024) +
+                          (uint32_t)kt * C::B_BLK;
+      dma16(rsrc_b, s + C::A_BYTES + q * 1024, vb, __builtin_amdgcn_readfirstlane(so));
+    }
   };
 
   typedef typename std::conditional<KIND == KIND_FP8, f32x4, i32x4>::type AccT;
   AccT acc[MR][NR];
-#pragma unroll
-  for (int i = 0; i < MR; ++i)
-#pragma unroll
-    for (int j = 0; j < NR; ++j) acc[i][j] = AccT{0, 0, 0, 0};
 
   // blockscale: the A scale of this lane's row in each MFMA row block and the B scale of
   // each 16-column block, for one K tile
   float sa_t[MR], sb_t[NR];
-  auto load_scales = [&](int kt) {
+  auto load_scales = [&](int m0, int n0, int kt) {
     if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi)
@@ -171,7 +184,8 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   };
 
   // One K tile.  The A fragment of row mi+1 is requested before the MFMAs of row mi are
-  // issued, so its LDS latency hides behind NR MFMAs.
+  // issued, so its LDS latency hides behind NR MFMAs.  B is the MFMA's first operand, so
+  // each accumulator tile holds C transposed (see the epilogue).
   auto compute = [&](const uint8_t* sA) {
     const uint8_t* sB = sA + C::A_BYTES;
     i32x4 alo, ahi;
@@ -238,57 +252,93 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     }
   };
 
-  // ---- main loop: DMA of tile kt+1 overlaps the MFMAs of tile kt ----
-  // (one loop body for both stages: two unrolled bodies would make the accumulators
-  // alternate between two register sets)
-  issue(lds0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_dma();
-    __syncthreads();  // tile kt has landed; every wave is done reading the other stage
-    uint8_t* cur = (kt & 1) ? lds1 : lds0;
-    uint8_t* nxt = (kt & 1) ? lds0 : lds1;
-    load_scales(kt);
-    if (kt + 1 < nk) issue(nxt, kt + 1);
-    compute(cur);
-  }
-
   // ---- epilogue ----
   // B is the MFMA's first operand, so each 16x16 accumulator tile is C transposed: lane
   // (lq, l16) holds row l16, columns 4*lq .. 4*lq+3 -- one 8-byte bf16/fp16 store (16 bytes
-  // for raw accumulators) per tile.  All scale loads are issued before the first store.
-  float sa_e[MR];
-  f32x4 sb_e[NR];
-  if constexpr (EPI == EPI_ROWCOL) {
+  // for raw accumulators) per tile.  Every lane issues exactly MR*NR buffer stores; those
+  // outside C get an offset past the buffer end and are dropped by the bounds check, so the
+  // number of stores in flight is known when the next tile waits for its first loads.
+  constexpr int ESZ = (EPI == EPI_RAW) ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(p.c, M * N * ESZ);
+  auto epilogue = [&](int m0, int n0) {
+    float sa_e[MR];
+    f32x4 sb_e[NR];
+    if constexpr (EPI == EPI_ROWCOL) {
 #pragma unroll
-    for (int mi = 0; mi < MR; ++mi) sa_e[mi] = p.sa[min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
+      for (int mi = 0; mi < MR; ++mi) sa_e[mi] = p.sa[min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
 #pragma unroll
-    for (int ni = 0; ni < NR; ++ni)
-      sb_e[ni] = *(const f32x4*)(p.sb + min(n0 + wn * C::TN + ni * 16 + lq * 4, N - 4));
-  }
+      for (int ni = 0; ni < NR; ++ni)
+        sb_e[ni] = *(const f32x4*)(p.sb + min(n0 + wn * C::TN + ni * 16 + lq * 4, N - 4));
+    }
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) {
-    const int row = m0 + wm * C::TM + mi * 16 + l16;
-    if (row >= M) continue;
+    for (int mi = 0; mi < MR; ++mi) {
+      const int row = m0 + wm * C::TM + mi * 16 + l16;
 #pragma unroll
-    for (int ni = 0; ni < NR; ++ni) {
-      const int col = n0 + wn * C::TN + ni * 16 + lq * 4;
-      if (col >= N) continue;
-      const size_t idx = (size_t)row * N + col;
-      if constexpr (EPI == EPI_RAW) {
-        *(AccT*)((typename std::conditional<KIND == KIND_FP8, float, int>::type*)p.c + idx) = acc[mi][ni];
-      } else {
-        float v[4];
+      for (int ni = 0; ni < NR; ++ni) {
+        const int col = n0 + wn * C::TN + ni * 16 + lq * 4;
+        const uint32_t off = (row < M && col < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)col) * ESZ : 0x80000000u;
+        if constexpr (EPI == EPI_RAW) {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[mi][ni]), rsrc_c, off, 0, 0);
+        } else {
+          float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if constexpr (KIND == KIND_FP8)
-            v[r] = acc[mi][ni][r];
-          else
-            v[r] = (float)acc[mi][ni][r];
-          if constexpr (EPI == EPI_ROWCOL) v[r] = (v[r] * sa_e[mi]) * sb_e[ni][r];
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (KIND == KIND_FP8)
+              v[r] = acc[mi][ni][r];
+            else
+              v[r] = (float)acc[mi][ni][r];
+            if constexpr (EPI == EPI_ROWCOL) v[r] = (v[r] * sa_e[mi]) * sb_e[ni][r];
+          }
+          __builtin_amdgcn_raw_buffer_store_b64(pack_out4<OUT_BF16>(v), rsrc_c, off, 0, 0);
         }
-        store_out4<OUT_BF16>(p.c, idx, v);
       }
     }
+  };
+
+  // ---- persistent loop over this workgroup's tiles, one flattened (tile, K tile) pipeline:
+  // the DMA of the next step -- the next K tile, or the first K tile of the next tile --
+  // is in flight while the MFMAs of the current step run, so a tile's first loads overlap
+  // the previous tile's last MFMAs and its epilogue.
+  const int G = gridDim.x;
+  int t = blockIdx.x;
+  int bm, bn;
+  tile_coords(t, ntiles, nbm, bm, bn);
+  int m0 = bm * BM, n0 = bn * BN;
+  issue(lds0, m0, n0, 0);
+  int step = 0;
+  for (; t < ntiles; t += G) {
+    const int tn = t + G;
+    int nm0 = 0, nn0 = 0;
+    if (tn < ntiles) {
+      tile_coords(tn, ntiles, nbm, bm, bn);
+      nm0 = bm * BM;
+      nn0 = bn * BN;
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i)
+#pragma unroll
+      for (int j = 0; j < NR; ++j) acc[i][j] = AccT{0, 0, 0, 0};
+    for (int kt = 0; kt < nk; ++kt, ++step) {
+      // wait for this wave's loads of this step; at a tile's first step the previous
+      // tile's MR*NR epilogue stores were issued after them and may still be in flight
+      // (vector memory operations retire in issue order)
+      if (kt == 0 && step > 0)
+        wait_vmem_leaving<MR * NR>();
+      else
+        wait_dma();
+      __syncthreads();  // this step's tile has landed; every wave is done with the other stage
+      uint8_t* cur = (step & 1) ? lds1 : lds0;
+      uint8_t* nxt = (step & 1) ? lds0 : lds1;
+      load_scales(m0, n0, kt);
+      if (kt + 1 < nk)
+        issue(nxt, m0, n0, kt + 1);
+      else if (tn < ntiles)
+        issue(nxt, nm0, nn0, 0);
+      compute(cur);
+    }
+    epilogue(m0, n0);
+    m0 = nm0;
+    n0 = nn0;
   }
 }
 
