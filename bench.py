@@ -10,6 +10,13 @@ from HIP events recorded on the launch stream around the K timed launches; B (an
 rotated over several copies whose total exceeds the 256 MB last-level cache, so every
 launch streams its operands from HBM.  The CPU baseline times the oracle's
 dequantize-then-matmul restatement on the host cores for a bounded sample.
+
+Profiling helpers (used by the commands recorded under profiles/):
+    python bench.py --launches-only C2 --n 20   # only the GEMM launches of one workload
+    python bench.py --copy-bytes 268435456      # a device-to-device copy of known size,
+                                                # to calibrate FETCH_SIZE / WRITE_SIZE
+``roofline.traffic`` (HBM bytes per launch) is read from profiles/hbm_traffic.md, which
+records those counter runs; it is null when that file has no entry for the workload.
 """
 from __future__ import annotations
 
@@ -120,15 +127,50 @@ def cpu_baseline(w: workloads.Workload, budget_s: float = 12.0):
                       f"oracle.gemm.run_torch float32 numpy/BLAS; {w.flops / t / 1e12:.4f} TFLOP/s"}
 
 
+def traffic_from_profile(name: str):
+    """HBM bytes per launch recorded in profiles/hbm_traffic.md (line 'traffic <W> <bytes>')."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.strip().strip("`").split()
+        if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
+            return int(parts[2])
+    return None
+
+
+def launches_only(name: str, n: int):
+    dev = torch.device("cuda:0")
+    r = Runner(workloads.WORKLOADS[name], dev, min_rotation_bytes=0)
+    stream = torch.cuda.current_stream()
+    for i in range(n):
+        r.launch(i, stream)
+    torch.cuda.synchronize()
+    log(f"[bench] {n} launches of {name} ({r.variant}) done")
+
+
+def copy_bytes(nbytes: int, n: int = 5):
+    dev = torch.device("cuda:0")
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(n):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] {n} copies of {nbytes} bytes done")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="C2")
     ap.add_argument("--secondary", default="T", help="extra MFMA-bound workload ('' to skip)")
     ap.add_argument("--all", action="store_true", help="also time every configuration")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--launches-only", default="", help="profiling: only launch this workload --n times")
+    ap.add_argument("--n", type=int, default=20)
+    ap.add_argument("--copy-bytes", type=int, default=0, help="profiling: copy this many bytes on the GPU")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
@@ -139,6 +181,12 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     _lib.load()
+    if args.launches_only:
+        launches_only(args.launches_only, args.n)
+        return
+    if args.copy_bytes:
+        copy_bytes(args.copy_bytes)
+        return
 
     w = workloads.WORKLOADS[args.workload]
     log(f"[bench] preparing {w.name} {w.kind} {w.M}x{w.N}x{w.K}")
@@ -154,7 +202,7 @@ def main():
         "data": "synthetic (seeded N(0,1), quantized per BASELINE)",
         "config": {"workload": f"{w.name}: {w.note} {w.M}x{w.N}x{w.K} seed {w.seed}", "M": w.M, "N": w.N,
                    "K": w.K, "kernel": r.variant, "wall_s": round(wall, 4)},
-        "roofline": roofline(w, ms, "hbm"),
+        "roofline": roofline(w, ms, "hbm", traffic_from_profile(w.name)),
     }
     if bound == "mfma":
         result["roofline_mfma"] = roofline(w, ms, "mfma")
@@ -176,7 +224,7 @@ def main():
         b2 = "hbm" if name in ("C1", "C2") else "mfma"
         sec[name] = {"ms": round(ms2, 5), "TFLOP/s": round(w2.flops / ms2 / 1e9, 1),
                      "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
-                     "roofline": roofline(w2, ms2, b2)}
+                     "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
         del r2
         torch.cuda.empty_cache()
     if sec:

@@ -42,22 +42,21 @@ struct Shape {
   int bm, bn, threads;  // main: workgroup tile; decode: bm = 16*MR rows, bn = 16*NBW cols
 };
 
+// Ordered by preference: the selector takes the first tile that yields enough workgroups.
 #define MAIN_SHAPES(X) \
-  X(256, 256, 2, 2)    \
   X(256, 256, 2, 4)    \
   X(256, 256, 4, 2)    \
-  X(128, 256, 2, 2)    \
   X(128, 128, 2, 2)    \
   X(64, 128, 1, 4)
 
 #define DECODE_SHAPES(X) \
   X(1, 1, 8, 4)          \
   X(1, 2, 8, 4)          \
-  X(1, 4, 8, 2)          \
+  X(1, 4, 8, 3)          \
   X(1, 7, 8, 2)          \
   X(2, 1, 8, 4)          \
-  X(2, 2, 8, 2)          \
-  X(4, 1, 8, 2)          \
+  X(2, 2, 8, 3)          \
+  X(4, 1, 8, 3)          \
   X(4, 2, 8, 2)
 
 const Shape kShapes[] = {
@@ -109,7 +108,6 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
 int select_variant(int M, int N, int K, int kind, int epi) {
   (void)K;
   (void)kind;
-  (void)epi;
   if (M <= 64) {
     // decode family: fewest rows that cover M, then the most column blocks per workgroup
     // that still leaves about one workgroup per CU
@@ -123,8 +121,9 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     }
     return best;
   }
-  // main family: largest tile that still gives every CU work
-  for (int v = 0; v < kFirstDecode; ++v) {
+  // main family: largest tile that still gives every CU work (the blockscale epilogue's
+  // extra registers make the 256x256 tiles slower than 128x128 there)
+  for (int v = (epi == EPI_BLOCK ? 2 : 0); v < kFirstDecode; ++v) {
     const long wg = (long)((M + kShapes[v].bm - 1) / kShapes[v].bm) * ((N + kShapes[v].bn - 1) / kShapes[v].bn);
     if (wg >= 240) return v;
   }

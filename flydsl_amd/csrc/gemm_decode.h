@@ -2,9 +2,9 @@
 //
 // For M <= 16*MR the whole of A (a few hundred KB at most) is L2-resident, so the kernel is
 // bound by reading B once.  A workgroup owns NBW 16-column blocks and all M rows; its NW
-// waves split K (wave w takes K tiles w, w+NW, ...), each wave keeps UNROLL K tiles of
-// loads in flight, and the NW partial accumulators are summed through LDS before the
-// fused epilogue.  The reduction is inside the workgroup: no workspace, no atomics, and
+// waves split K (wave w takes K tiles w, w+NW, ...), each wave keeps UNROLL-1 K tiles of
+// loads in flight ahead of the one it multiplies, and the NW partial accumulators are
+// summed through LDS before the fused epilogue.  The reduction is inside the workgroup: no workspace, no atomics, and
 // the int32 sums stay exact.  Owning several column blocks per workgroup divides the A
 // traffic (one A fragment serves NBW blocks).
 //
@@ -24,7 +24,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   const int nk = K / KT;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wave-uniform (SGPR) wave index: every branch that guards an MFMA below depends only
+  // on it, so the compiler emits scalar branches.  Guarding an MFMA by EXEC masking instead
+  // would not skip it (the matrix core computes the whole tile), and a skipped tile's
+  // operand registers were never loaded.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15;
   const int lq = lane >> 4;
   const int nblk_max = N / 16 - 1;
@@ -53,81 +57,89 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       bblk[j] = p.b + (size_t)nb * B_PER_K * K + lq * 256 + l16 * 16;
   }
 
-  for (int kt0 = wave; kt0 < nk; kt0 += NW * UNROLL) {
-    i32x4 alo[UNROLL][MR], ahi[UNROLL][MR];
-    i32x4 blo[UNROLL][NBW], bhi[UNROLL][NBW];
-    i32x2 b4lo[UNROLL][NBW], b4hi[UNROLL][NBW];
-    // issue all loads of UNROLL K tiles first
+  // Rolling pipeline over this wave's K tiles (kt = wave, wave + NW, ...): UNROLL register
+  // stages, so the loads of the next UNROLL-1 tiles are in flight while one tile is
+  // multiplied; the stage index is a compile-time constant inside the unrolled body.
+  struct Stage {
+    i32x4 alo[MR], ahi[MR];
+    i32x4 blo[NBW], bhi[NBW];
+    i32x2 b4lo[NBW], b4hi[NBW];
+  };
+  Stage st[UNROLL];
+  auto load = [&](Stage& s, int kt) {
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int kt = kt0 + u * NW;
-      if (kt < nk) {
-#pragma unroll
-        for (int j = 0; j < NBW; ++j) {
-          const uint8_t* src = bblk[j] + (size_t)kt * B_BLK;
-          if constexpr (KIND == KIND_INT4) {
-            b4lo[u][j] = __builtin_nontemporal_load((const i32x2*)src);
-            b4hi[u][j] = __builtin_nontemporal_load((const i32x2*)(src + 512));
-          } else {
-            blo[u][j] = __builtin_nontemporal_load((const i32x4*)src);
-            bhi[u][j] = __builtin_nontemporal_load((const i32x4*)(src + 1024));
-          }
-        }
-#pragma unroll
-        for (int mi = 0; mi < MR; ++mi) {
-          const uint8_t* src = arow[mi] + (size_t)kt * KT;
-          alo[u][mi] = *(const i32x4*)src;
-          ahi[u][mi] = *(const i32x4*)(src + 64);
-        }
+    for (int j = 0; j < NBW; ++j) {
+      const uint8_t* src = bblk[j] + (size_t)kt * B_BLK;
+      if constexpr (KIND == KIND_INT4) {
+        s.b4lo[j] = __builtin_nontemporal_load((const i32x2*)src);
+        s.b4hi[j] = __builtin_nontemporal_load((const i32x2*)(src + 512));
+      } else {
+        s.blo[j] = __builtin_nontemporal_load((const i32x4*)src);
+        s.bhi[j] = __builtin_nontemporal_load((const i32x4*)(src + 1024));
       }
     }
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const int kt = kt0 + u * NW;
-      if (kt < nk) {
-        if constexpr (KIND == KIND_FP8) {
+    for (int mi = 0; mi < MR; ++mi) {
+      const uint8_t* src = arow[mi] + (size_t)kt * KT;
+      s.alo[mi] = *(const i32x4*)src;
+      s.ahi[mi] = *(const i32x4*)(src + 64);
+    }
+  };
+  auto compute = [&](const Stage& s, int kt) {
+    if constexpr (KIND == KIND_FP8) {
 #pragma unroll
-          for (int mi = 0; mi < MR; ++mi) {
-            const i32x8 af = i32x8{alo[u][mi].x, alo[u][mi].y, alo[u][mi].z, alo[u][mi].w,
-                                   ahi[u][mi].x, ahi[u][mi].y, ahi[u][mi].z, ahi[u][mi].w};
-            float s_a = 0.f;
-            if constexpr (EPI == EPI_BLOCK) s_a = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
+      for (int mi = 0; mi < MR; ++mi) {
+        const i32x8 af = i32x8{s.alo[mi].x, s.alo[mi].y, s.alo[mi].z, s.alo[mi].w,
+                               s.ahi[mi].x, s.ahi[mi].y, s.ahi[mi].z, s.ahi[mi].w};
+        float s_a = 0.f;
+        if constexpr (EPI == EPI_BLOCK) s_a = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
 #pragma unroll
-            for (int j = 0; j < NBW; ++j) {
-              const i32x8 bf = i32x8{blo[u][j].x, blo[u][j].y, blo[u][j].z, blo[u][j].w,
-                                     bhi[u][j].x, bhi[u][j].y, bhi[u][j].z, bhi[u][j].w};
-              if constexpr (EPI == EPI_BLOCK) {
-                const int col = min((nb0 + j) * 16, N - 1);
-                const float s = s_a * p.sb[(size_t)(col >> 7) * nk + kt];
-                const f32x4 part = mfma_fp8(bf, af, f32x4{0.f, 0.f, 0.f, 0.f});
-                acc[mi][j].x = __builtin_fmaf(part.x, s, acc[mi][j].x);
-                acc[mi][j].y = __builtin_fmaf(part.y, s, acc[mi][j].y);
-                acc[mi][j].z = __builtin_fmaf(part.z, s, acc[mi][j].z);
-                acc[mi][j].w = __builtin_fmaf(part.w, s, acc[mi][j].w);
-              } else {
-                acc[mi][j] = mfma_fp8(bf, af, acc[mi][j]);
-              }
-            }
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < NBW; ++j) {
-            i32x4 bl, bh;
-            if constexpr (KIND == KIND_INT4) {
-              bl = unpack_int4x16(b4lo[u][j]);
-              bh = unpack_int4x16(b4hi[u][j]);
-            } else {
-              bl = blo[u][j];
-              bh = bhi[u][j];
-            }
-#pragma unroll
-            for (int mi = 0; mi < MR; ++mi) {
-              acc[mi][j] = mfma_i8(bl, alo[u][mi], acc[mi][j]);
-              acc[mi][j] = mfma_i8(bh, ahi[u][mi], acc[mi][j]);
-            }
+        for (int j = 0; j < NBW; ++j) {
+          const i32x8 bf = i32x8{s.blo[j].x, s.blo[j].y, s.blo[j].z, s.blo[j].w,
+                                 s.bhi[j].x, s.bhi[j].y, s.bhi[j].z, s.bhi[j].w};
+          if constexpr (EPI == EPI_BLOCK) {
+            const int col = min((nb0 + j) * 16, N - 1);
+            const float sc = s_a * p.sb[(size_t)(col >> 7) * nk + kt];
+            const f32x4 part = mfma_fp8(bf, af, f32x4{0.f, 0.f, 0.f, 0.f});
+            acc[mi][j].x = __builtin_fmaf(part.x, sc, acc[mi][j].x);
+            acc[mi][j].y = __builtin_fmaf(part.y, sc, acc[mi][j].y);
+            acc[mi][j].z = __builtin_fmaf(part.z, sc, acc[mi][j].z);
+            acc[mi][j].w = __builtin_fmaf(part.w, sc, acc[mi][j].w);
+          } else {
+            acc[mi][j] = mfma_fp8(bf, af, acc[mi][j]);
           }
         }
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        i32x4 bl, bh;
+        if constexpr (KIND == KIND_INT4) {
+          bl = unpack_int4x16(s.b4lo[j]);
+          bh = unpack_int4x16(s.b4hi[j]);
+        } else {
+          bl = s.blo[j];
+          bh = s.bhi[j];
+        }
+#pragma unroll
+        for (int mi = 0; mi < MR; ++mi) {
+          acc[mi][j] = mfma_i8(bl, s.alo[mi], acc[mi][j]);
+          acc[mi][j] = mfma_i8(bh, s.ahi[mi], acc[mi][j]);
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int u = 0; u < UNROLL - 1; ++u)
+    if (wave + u * NW < nk) load(st[u], wave + u * NW);
+  for (int kt0 = wave; kt0 < nk; kt0 += NW * UNROLL) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int kt = kt0 + u * NW;
+      const int kl = kt + (UNROLL - 1) * NW;  // the tile whose loads go out now
+      if (kl < nk) load(st[(u + UNROLL - 1) % UNROLL], kl);
+      if (kt < nk) compute(st[u], kt);
     }
   }
 
