@@ -47,7 +47,11 @@ struct Shape {
   X(256, 256, 2, 4)    \
   X(256, 256, 4, 2)    \
   X(128, 128, 2, 2)    \
-  X(64, 128, 1, 4)
+  X(64, 128, 1, 4)     \
+  X(256, 128, 2, 4)    \
+  X(128, 256, 2, 4)    \
+  X(256, 64, 4, 1)     \
+  X(128, 64, 2, 2)
 
 #define DECODE_SHAPES(X) \
   X(1, 1, 8, 4)          \
@@ -57,7 +61,9 @@ struct Shape {
   X(2, 1, 8, 4)          \
   X(2, 2, 8, 3)          \
   X(4, 1, 8, 3)          \
-  X(4, 2, 8, 2)
+  X(4, 2, 8, 2)          \
+  X(8, 1, 8, 2)          \
+  X(8, 2, 8, 1)
 
 const Shape kShapes[] = {
 #define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64},

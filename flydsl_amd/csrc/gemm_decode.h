@@ -64,6 +64,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     i32x4 alo[MR], ahi[MR];
     i32x4 blo[NBW], bhi[NBW];
     i32x2 b4lo[NBW], b4hi[NBW];
+    float sa[MR], sb[NBW];  // blockscale: this K tile's A scale per row block, B scale per column block
   };
   Stage st[UNROLL];
   auto load = [&](Stage& s, int kt) {
@@ -84,6 +85,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       s.alo[mi] = *(const i32x4*)src;
       s.ahi[mi] = *(const i32x4*)(src + 64);
     }
+    // blockscale scales travel with the stage, so their latency hides behind the pipeline
+    if constexpr (EPI == EPI_BLOCK) {
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) s.sa[mi] = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) s.sb[j] = p.sb[(size_t)(min((nb0 + j) * 16, N - 1) >> 7) * nk + kt];
+    }
   };
   auto compute = [&](const Stage& s, int kt) {
     if constexpr (KIND == KIND_FP8) {
@@ -92,14 +100,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
         const i32x8 af = i32x8{s.alo[mi].x, s.alo[mi].y, s.alo[mi].z, s.alo[mi].w,
                                s.ahi[mi].x, s.ahi[mi].y, s.ahi[mi].z, s.ahi[mi].w};
         float s_a = 0.f;
-        if constexpr (EPI == EPI_BLOCK) s_a = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
+        if constexpr (EPI == EPI_BLOCK) s_a = s.sa[mi];
 #pragma unroll
         for (int j = 0; j < NBW; ++j) {
           const i32x8 bf = i32x8{s.blo[j].x, s.blo[j].y, s.blo[j].z, s.blo[j].w,
                                  s.bhi[j].x, s.bhi[j].y, s.bhi[j].z, s.bhi[j].w};
           if constexpr (EPI == EPI_BLOCK) {
-            const int col = min((nb0 + j) * 16, N - 1);
-            const float sc = s_a * p.sb[(size_t)(col >> 7) * nk + kt];
+            const float sc = s_a * s.sb[j];
             const f32x4 part = mfma_fp8(bf, af, f32x4{0.f, 0.f, 0.f, 0.f});
             acc[mi][j].x = __builtin_fmaf(part.x, sc, acc[mi][j].x);
             acc[mi][j].y = __builtin_fmaf(part.y, sc, acc[mi][j].y);

@@ -160,18 +160,27 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   AccT acc[MR][NR];
 
   // blockscale: the A scale of this lane's row in each MFMA row block and the B scale of
-  // each 16-column block, for one K tile
-  float sa_t[MR], sb_t[NR];
+  // each 16-column block, for one K tile.  They are loaded one step ahead (into sa_n/sb_n,
+  // together with that step's DMA), so the wait at the top of a step covers them too.
+  float sa_t[MR], sb_t[NR], sa_n[MR], sb_n[NR];
   auto load_scales = [&](int m0, int n0, int kt) {
     if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi)
-        sa_t[mi] = p.sa[(size_t)kt * M + min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
+        sa_n[mi] = p.sa[(size_t)kt * M + min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
 #pragma unroll
       for (int ni = 0; ni < NR; ++ni) {
         const int col = min(n0 + wn * C::TN + ni * 16, N - 1);
-        sb_t[ni] = p.sb[(size_t)(col >> 7) * nk + kt];
+        sb_n[ni] = p.sb[(size_t)(col >> 7) * nk + kt];
       }
+    }
+  };
+  auto take_scales = [&]() {
+    if constexpr (EPI == EPI_BLOCK) {
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) sa_t[mi] = sa_n[mi];
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni) sb_t[ni] = sb_n[ni];
     }
   };
 
@@ -305,6 +314,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   tile_coords(t, ntiles, nbm, bm, bn);
   int m0 = bm * BM, n0 = bn * BN;
   issue(lds0, m0, n0, 0);
+  load_scales(m0, n0, 0);
   int step = 0;
   for (; t < ntiles; t += G) {
     const int tn = t + G;
@@ -329,11 +339,14 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       __syncthreads();  // this step's tile has landed; every wave is done with the other stage
       uint8_t* cur = (step & 1) ? lds1 : lds0;
       uint8_t* nxt = (step & 1) ? lds0 : lds1;
-      load_scales(m0, n0, kt);
-      if (kt + 1 < nk)
+      take_scales();
+      if (kt + 1 < nk) {
         issue(nxt, m0, n0, kt + 1);
-      else if (tn < ntiles)
+        load_scales(m0, n0, kt + 1);
+      } else if (tn < ntiles) {
         issue(nxt, nm0, nn0, 0);
+        load_scales(nm0, nn0, 0);
+      }
       compute(cur);
     }
     epilogue(m0, n0);
