@@ -127,13 +127,24 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     }
     return best;
   }
-  // main family: largest tile that still gives every CU work (the blockscale epilogue's
-  // extra registers make the 256x256 tiles slower than 128x128 there)
-  for (int v = (epi == EPI_BLOCK ? 2 : 0); v < kFirstDecode; ++v) {
-    const long wg = (long)((M + kShapes[v].bm - 1) / kShapes[v].bm) * ((N + kShapes[v].bn - 1) / kShapes[v].bn);
-    if (wg >= 240) return v;
+  // main family: the first tile in a measured preference list that gives enough workgroups
+  // to occupy the chip (256 CUs).  The blockscale epilogue's per-K-tile rescale needs more
+  // registers, which makes the 8-wave 128x256 tile its best; elsewhere 256x256 wins when it
+  // fills the chip and the 4-wave 64x128 tile (two resident per CU) wins below that.
+  struct Pref {
+    int bm, bn, threads, min_wg;
+  };
+  static const Pref kRowcol[] = {{256, 256, 512, 240}, {128, 256, 512, 240}, {128, 128, 256, 480}, {64, 128, 256, 0}};
+  static const Pref kBlock[] = {{128, 256, 512, 200}, {128, 128, 256, 240}, {64, 128, 256, 0}};
+  const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
+  const int n = epi == EPI_BLOCK ? 3 : 4;
+  for (int i = 0; i < n; ++i) {
+    const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
+    if (wg < list[i].min_wg) continue;
+    for (int v = 0; v < kFirstDecode; ++v)
+      if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }
-  return kFirstDecode - 1;
+  return -1;
 }
 
 // Persistent grid for the large-M kernel: as many workgroups as can be resident at once

@@ -37,6 +37,16 @@ def test_variant_table():
     lib = _lib.load()
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 0, 0)].startswith("decode_m1")
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
+    # every shape gets a variant, and the five configurations get the tiles measured fastest
+    expect = {(128, 4096, 4096, 0, 0): "main_64x128_w1x4", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
+              (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_128x256_w2x4",
+              (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
+    for args, want in expect.items():
+        assert names[lib.flygemm_select_variant(*args)] == want, args
+    for m in (1, 17, 64, 65, 100, 1000, 5000):
+        for n in (16, 128, 2048, 30000):
+            for bs in (0, 1):
+                assert 0 <= lib.flygemm_select_variant(m, n, 1024, 0, bs) < len(names)
     assert lib.flygemm_variant_name(-1) is None and lib.flygemm_variant_name(len(names)) is None
 
 
