@@ -88,6 +88,47 @@ class Runner:
         return ms / steps, wall
 
 
+class QuantWorkload:
+    """The reference's per-token quant benchmark (tests/kernels/test_quant.py:277-297):
+    fp16 [M, N] uniform(-5, 5) with np.random.seed(42) -> int8 [M, N] + fp32 scales [M];
+    bytes = 2MN + MN + 4M."""
+    name, kind, note = "Q", "fp16->int8", "per-token quant (reference kernel semantics)"
+
+    def __init__(self, M=4096, N=8192):
+        self.M, self.N, self.K, self.seed = M, N, 0, 42
+        self.bytes = 2 * M * N + M * N + 4 * M
+        self.flops = 0
+
+
+class QuantRunner:
+    def __init__(self, w: QuantWorkload, dev, min_rotation_bytes=3 * LLC_BYTES):
+        import numpy as np
+
+        from flydsl_amd.kernels.quant import build_quant_module
+        self.w = w
+        np.random.seed(w.seed)
+        x = torch.from_numpy(np.random.uniform(-5.0, 5.0, size=(w.M, w.N)).astype(np.float16))
+        per_call = w.bytes
+        self.copies = max(1, min(8, -(-min_rotation_bytes // per_call)))
+        self.x = [x.to(dev) for _ in range(self.copies)]
+        self.out = [torch.empty(w.M, w.N, dtype=torch.int8, device=dev) for _ in range(self.copies)]
+        self.sc = torch.empty(w.M, dtype=torch.float32, device=dev)
+        self.fn, _ = build_quant_module(w.N)
+        self.variant = "quant_rows_recip_trunc"
+
+    def launch(self, i, stream):
+        j = i % self.copies
+        self.fn(self.x[j], self.out[j], self.sc, self.w.M, stream)
+
+    time = Runner.time
+
+
+def make_runner(name, dev, **kw):
+    if name == "Q":
+        return QuantRunner(QuantWorkload(), dev, **kw)
+    return Runner(workloads.WORKLOADS[name], dev, **kw)
+
+
 def roofline(w: workloads.Workload, ms_per_launch: float, bound: str, traffic=None):
     if bound == "hbm":
         achieved = w.bytes / (ms_per_launch * 1e-3) / 1e9
@@ -141,7 +182,7 @@ def traffic_from_profile(name: str):
 
 def launches_only(name: str, n: int):
     dev = torch.device("cuda:0")
-    r = Runner(workloads.WORKLOADS[name], dev, min_rotation_bytes=0)
+    r = make_runner(name, dev, min_rotation_bytes=0)
     stream = torch.cuda.current_stream()
     for i in range(n):
         r.launch(i, stream)
@@ -165,7 +206,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="C2")
-    ap.add_argument("--secondary", default="T", help="extra MFMA-bound workload ('' to skip)")
+    ap.add_argument("--secondary", default="T,Q", help="extra workloads, comma separated ('' to skip)")
     ap.add_argument("--all", action="store_true", help="also time every configuration")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--launches-only", default="", help="profiling: only launch this workload --n times")
@@ -209,22 +250,21 @@ def main():
     del r
     torch.cuda.empty_cache()
 
-    extra = []
-    if args.secondary:
-        extra.append(args.secondary)
+    extra = [n for n in args.secondary.split(",") if n]
     if args.all:
-        extra += [n for n in workloads.WORKLOADS if n not in extra and n != args.workload]
+        extra += [n for n in list(workloads.WORKLOADS) + ["Q"] if n not in extra and n != args.workload]
     sec = {}
     for name in extra:
-        w2 = workloads.WORKLOADS[name]
+        r2 = make_runner(name, dev)
+        w2 = r2.w
         log(f"[bench] preparing {name} {w2.kind} {w2.M}x{w2.N}x{w2.K}")
-        r2 = Runner(w2, dev)
         log(f"[bench] timing {name} variant={r2.variant}")
         ms2, _ = r2.time(max(5, args.steps // 2), max(2, args.warmup // 2))
-        b2 = "hbm" if name in ("C1", "C2") else "mfma"
-        sec[name] = {"ms": round(ms2, 5), "TFLOP/s": round(w2.flops / ms2 / 1e9, 1),
-                     "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
+        b2 = "hbm" if name in ("C1", "C2", "Q") else "mfma"
+        sec[name] = {"ms": round(ms2, 5), "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
+        if w2.flops:
+            sec[name]["TFLOP/s"] = round(w2.flops / ms2 / 1e9, 1)
         del r2
         torch.cuda.empty_cache()
     if sec:

@@ -16,6 +16,7 @@
 #include "../../include/flygemm.h"
 #include "gemm_decode.h"
 #include "gemm_main.h"
+#include "quant_rows.h"
 
 using namespace flygemm;
 
@@ -212,6 +213,28 @@ int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, 
   return 0;
 }
 
+// ---- per-row quantization ------------------------------------------------------------
+typedef void (*QuantFn)(QuantArgs);
+
+// registers-resident variant for rows of up to 1, 2, 4 or 8 slices, streaming beyond
+template <int IN, int OUT, int MODE>
+QuantFn quant_fn(int nslices) {
+  if (nslices <= 1) return quant_rows_kernel<IN, OUT, MODE, 1>;
+  if (nslices <= 2) return quant_rows_kernel<IN, OUT, MODE, 2>;
+  if (nslices <= 4) return quant_rows_kernel<IN, OUT, MODE, 4>;
+  if (nslices <= 8) return quant_rows_kernel<IN, OUT, MODE, 8>;
+  return quant_rows_kernel<IN, OUT, MODE, 0>;
+}
+
+template <int IN>
+QuantFn quant_fn_in(int out_dtype, int mode, int nslices) {
+  if (out_dtype == QOUT_FP8) return mode == QMODE_DIV_NEAREST ? quant_fn<IN, QOUT_FP8, QMODE_DIV_NEAREST>(nslices) : nullptr;
+  if (mode == QMODE_RECIP_TRUNC) return quant_fn<IN, QOUT_INT8, QMODE_RECIP_TRUNC>(nslices);
+  if (mode == QMODE_DIV_TRUNC) return quant_fn<IN, QOUT_INT8, QMODE_DIV_TRUNC>(nslices);
+  if (mode == QMODE_DIV_NEAREST) return quant_fn<IN, QOUT_INT8, QMODE_DIV_NEAREST>(nslices);
+  return nullptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -251,6 +274,36 @@ int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int
     return fail(hipErrorInvalidValue, "in_dtype %d not supported", in_dtype);
   GemmArgs args{acc, (const uint8_t*)a, (const uint8_t*)b, nullptr, nullptr, M, N, K};
   return launch(in_dtype, EPI_RAW, FLYGEMM_OUT_BF16, variant, args, (hipStream_t)stream);
+}
+
+int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int32_t N, int32_t in_dtype,
+                       int32_t out_dtype, int32_t mode, void* stream) {
+  if (M < 0 || N <= 0) return fail(hipErrorInvalidValue, "invalid sizes M=%d N=%d", M, N);
+  if (N % 8 != 0) return fail(hipErrorInvalidValue, "N=%d must be a multiple of 8 (16-byte row vectors)", N);
+  if (in_dtype < FLYGEMM_QIN_F16 || in_dtype > FLYGEMM_QIN_F32)
+    return fail(hipErrorInvalidValue, "quant in_dtype %d not supported", in_dtype);
+  if (out_dtype != FLYGEMM_QOUT_FP8 && out_dtype != FLYGEMM_QOUT_INT8)
+    return fail(hipErrorInvalidValue, "quant out_dtype %d not supported", out_dtype);
+  if (mode < FLYGEMM_QMODE_RECIP_TRUNC || mode > FLYGEMM_QMODE_DIV_NEAREST)
+    return fail(hipErrorInvalidValue, "quant mode %d not supported", mode);
+  if (out_dtype == FLYGEMM_QOUT_FP8 && mode != FLYGEMM_QMODE_DIV_NEAREST)
+    return fail(hipErrorInvalidValue, "fp8 output rounds to nearest: mode must be FLYGEMM_QMODE_DIV_NEAREST");
+  const int esz = in_dtype == FLYGEMM_QIN_F32 ? 4 : 2;
+  if ((long)M * N * esz >= (1L << 40)) return fail(hipErrorInvalidValue, "input too large (M=%d N=%d)", M, N);
+  if (M == 0) return 0;
+  if (!out || !scales || !in) return fail(hipErrorInvalidValue, "null pointer");
+  if (((uintptr_t)in & 15) || ((uintptr_t)out & 7) || ((uintptr_t)scales & 3))
+    return fail(hipErrorInvalidValue, "misaligned pointer (input needs 16-byte, output 8-byte alignment)");
+  const int nslices = (N + kQuantSlice - 1) / kQuantSlice;
+  QuantFn fn = in_dtype == FLYGEMM_QIN_F16    ? quant_fn_in<QIN_F16>(out_dtype, mode, nslices)
+               : in_dtype == FLYGEMM_QIN_BF16 ? quant_fn_in<QIN_BF16>(out_dtype, mode, nslices)
+                                              : quant_fn_in<QIN_F32>(out_dtype, mode, nslices);
+  if (!fn) return fail(hipErrorInvalidValue, "unsupported quant combination");
+  QuantArgs args{out, scales, in, M, N};
+  hipLaunchKernelGGL(fn, dim3(M), dim3(kQuantThreads), 0, (hipStream_t)stream, args);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(e, "launch of quant_rows failed: %s", hipGetErrorString(e));
+  return 0;
 }
 
 int32_t flygemm_num_variants(void) { return kNumShapes; }

@@ -1,0 +1,95 @@
+"""Device per-token quantization: the producer of a GEMM's A operand and ``scale_a``.
+
+Two interfaces over ``flygemm_quant_rows`` (``include/flygemm.h``):
+
+* ``build_quant_module(N)`` -> ``(launch_quant, config)`` -- the reference's quant kernel
+  builder (``tests/kernels/test_quant.py:81-265``): ``launch_quant(Input, Output, Scales, m_in,
+  stream=None)`` with fp16 ``Input[M, N]``, int8 ``Output[M, N]``, fp32 ``Scales[M]``;
+  ``Scales = amax / 127`` (0 -> 1) and ``Output = fptosi(Input * (1 / Scales))``.  ``config``
+  has the reference's keys.
+* ``per_token_quant(x, quant_dtype, rounding)`` -- the reference's ``pertoken_quant``
+  (``tests/utils.py:29-73``) on the device: NaN/inf scrubbing, ``scale = amax / dtypeMax``,
+  ``q = (x / scale).to(quant_dtype)``; returns ``(q, scale[M, 1])``.  int8 rounds half to
+  even by default (the benchmark workloads' rule) or truncates (``rounding="trunc"``, the
+  reference's ``.to(torch.int8)``); fp8 (``torch.float8_e4m3fn``) rounds to nearest even.
+
+Both fail loudly if the HIP library is missing; there is no host fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._launch import device_ptr, stream_handle
+
+BLOCK_THREADS = 256
+WARP_SIZE = 64
+VEC_WIDTH = 8
+
+_QIN = {torch.float16: _lib.QUANT_IN["fp16"], torch.bfloat16: _lib.QUANT_IN["bf16"],
+        torch.float32: _lib.QUANT_IN["fp32"]}
+
+
+def _launch(out_ptr, scale_ptr, in_ptr, M, N, in_code, out_code, mode, stream):
+    rc = _lib.load().flygemm_quant_rows(out_ptr, scale_ptr, in_ptr, int(M), int(N), in_code, out_code, mode,
+                                        stream_handle(stream))
+    _lib.check(rc, "flygemm_quant_rows")
+
+
+def build_quant_module(N: int):
+    """Quant launcher for hidden size ``N`` (reference ``test_quant.py:81``)."""
+    N = int(N)
+    if N <= 0 or N % VEC_WIDTH:
+        raise ValueError(f"N={N} must be a positive multiple of {VEC_WIDTH}")
+    tile_cols = BLOCK_THREADS * VEC_WIDTH
+
+    def launch_quant(Input, Output, Scales, m_in, stream=None):
+        M = int(m_in)
+        if M < 0:
+            raise ValueError(f"invalid M={M}")
+        i = device_ptr(Input, "Input", M * N, dtypes=(torch.float16,))
+        o = device_ptr(Output, "Output", M * N, elem_bytes=1)
+        s = device_ptr(Scales, "Scales", M, dtypes=(torch.float32,))
+        _launch(o, s, i, M, N, _lib.QUANT_IN["fp16"], _lib.QUANT_OUT["int8"], _lib.QUANT_MODE["recip_trunc"], stream)
+
+    config = {
+        "N": N,
+        "BLOCK_THREADS": BLOCK_THREADS,
+        "VEC_WIDTH": VEC_WIDTH,
+        "ELEMS_PER_BLOCK_ITER": tile_cols,
+        "ITERS": (N + tile_cols - 1) // tile_cols,
+    }
+    return launch_quant, config
+
+
+def per_token_quant(x: torch.Tensor, quant_dtype=torch.int8, rounding: str = "nearest", out=None, scale=None,
+                    stream=None):
+    """Per-row quantization of a 2-D fp16/bf16/fp32 GPU tensor; returns ``(q, scale[M, 1])``."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [M, N], got shape {tuple(x.shape)}")
+    if x.dtype not in _QIN:
+        raise TypeError(f"x dtype {x.dtype} not supported (fp16, bf16, fp32)")
+    if quant_dtype == torch.int8:
+        out_code = _lib.QUANT_OUT["int8"]
+        if rounding == "nearest":
+            mode = _lib.QUANT_MODE["div_nearest"]
+        elif rounding == "trunc":
+            mode = _lib.QUANT_MODE["div_trunc"]
+        else:
+            raise ValueError(f"rounding must be 'nearest' or 'trunc', got {rounding!r}")
+    elif quant_dtype == torch.float8_e4m3fn:
+        if rounding != "nearest":
+            raise ValueError("fp8 quantization rounds to nearest")
+        out_code, mode = _lib.QUANT_OUT["fp8"], _lib.QUANT_MODE["div_nearest"]
+    else:
+        raise TypeError(f"quant_dtype must be torch.int8 or torch.float8_e4m3fn, got {quant_dtype}")
+    M, N = x.shape
+    if out is None:
+        out = torch.empty(M, N, dtype=quant_dtype, device=x.device)
+    if scale is None:
+        scale = torch.empty(M, 1, dtype=torch.float32, device=x.device)
+    i = device_ptr(x, "x", M * N, dtypes=(x.dtype,))
+    o = device_ptr(out, "out", M * N, elem_bytes=1)
+    s = device_ptr(scale, "scale", M, dtypes=(torch.float32,))
+    _launch(o, s, i, M, N, _QIN[x.dtype], out_code, mode, stream)
+    return out, scale

@@ -62,6 +62,24 @@ int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_sca
 int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int32_t N, int32_t K,
                          int32_t in_dtype, int32_t variant, void* stream);
 
+/* Per-row (per-token) quantization of activations, the producer of A and scale_a:
+ *   scale[m] = max_n |in[m][n]| / qmax (qmax 127 int8, 448 fp8), 1 where that is 0;
+ *   out[m][n] = cast(in[m][n] / scale[m]), or cast(in[m][n] * (1 / scale[m])).
+ * mode FLYGEMM_QMODE_RECIP_TRUNC: the reference's device kernel
+ *   (tests/kernels/test_quant.py:81-265: fp16 in, int8 out, fptosi of the product with the
+ *   reciprocal); inputs must be finite.
+ * mode FLYGEMM_QMODE_DIV_TRUNC / _DIV_NEAREST: the reference's pertoken_quant
+ *   (tests/utils.py:29-73): NaN -> 0, +-inf -> +-qmax, then the quotient is cast, truncating
+ *   (int8, as torch's .to(int8)) or rounding half to even (int8 clamped to +-127; fp8
+ *   e4m3fn always uses _DIV_NEAREST, like torch's cast).
+ * in: [M][N] fp16/bf16/fp32 (16-byte aligned), out: [M][N] bytes (8-byte aligned),
+ * scales: fp32 [M].  N % 8 == 0.  Nothing is allocated; asynchronous on `stream`. */
+enum { FLYGEMM_QIN_F16 = 0, FLYGEMM_QIN_BF16 = 1, FLYGEMM_QIN_F32 = 2 };
+enum { FLYGEMM_QOUT_FP8 = 0, FLYGEMM_QOUT_INT8 = 1 };
+enum { FLYGEMM_QMODE_RECIP_TRUNC = 0, FLYGEMM_QMODE_DIV_TRUNC = 1, FLYGEMM_QMODE_DIV_NEAREST = 2 };
+int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int32_t N, int32_t in_dtype,
+                       int32_t out_dtype, int32_t mode, void* stream);
+
 /* Kernel variant table (replaces the reference's per-call tile kwargs,
  * kernels/preshuffle_gemm.py:39-53, with a static table). */
 int32_t flygemm_num_variants(void);

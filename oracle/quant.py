@@ -9,6 +9,11 @@ The reference's cast for int8 is ``.to(torch.int8)``, which truncates toward zer
 round-to-nearest for int8/int4, so ``quant_rows`` rounds half-to-even and clamps.
 fp8 uses the e4m3fn round-to-nearest-even cast, as the reference does.
 
+``quant_rows_recip`` restates the reference's device quant kernel
+(``tests/kernels/test_quant.py:81-265``): no NaN/inf scrubbing, ``scale = amax/127`` (0 -> 1,
+``:193-198``), then ``fptosi(x * (1/scale))`` -- a float32 reciprocal, a float32 product,
+truncation toward zero (``:208-238``).
+
 Pins (``tests/test_oracle.py``): invariants ``|q| <= qmax``, ``|q*scale - x| <=
 scale/2`` (int) or half an fp8 ulp (fp8), all-zero rows get scale 1, the row amax
 maps to exactly +-qmax; agreement with the product's torch quantizer; the block
@@ -31,20 +36,36 @@ def _row_scale(x32: np.ndarray, qmax: float) -> np.ndarray:
     return scale
 
 
-def _cast(y: np.ndarray, kind: str) -> np.ndarray:
+def _cast(y: np.ndarray, kind: str, rounding: str = "nearest") -> np.ndarray:
     if kind == "fp8":
         return e4m3fn_encode(y)
     qmax = QMAX[kind]
+    if rounding == "truncate":
+        return np.clip(np.trunc(y), -qmax, qmax).astype(np.int8)
     return np.clip(np.rint(y), -qmax, qmax).astype(np.int8)
 
 
-def quant_rows(x: np.ndarray, kind: str):
-    """Per-row quantization: returns (q, scale[rows]) with q uint8 codes (fp8) or int8."""
+def quant_rows(x: np.ndarray, kind: str, rounding: str = "nearest"):
+    """Per-row quantization: returns (q, scale[rows]) with q uint8 codes (fp8) or int8.
+    ``rounding`` ("nearest" or "truncate") applies to the integer kinds; fp8 always rounds
+    to nearest even."""
     qmax = QMAX[kind]
     x32 = np.nan_to_num(np.asarray(x, dtype=np.float32), nan=0.0, posinf=qmax, neginf=-qmax)
     scale = _row_scale(x32, qmax)
-    q = _cast((x32 / scale).astype(np.float32), kind)
+    q = _cast((x32 / scale).astype(np.float32), kind, rounding)
     return q, scale.reshape(-1)
+
+
+def quant_rows_recip(x: np.ndarray):
+    """The reference device kernel's int8 quantization: (q int8, scale[rows]) with
+    ``q = trunc(float32(x * float32(1 / scale)))`` and no scrubbing (finite inputs)."""
+    x32 = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x32).max(axis=-1, keepdims=True)
+    scale = (amax / np.float32(127.0)).astype(np.float32)
+    scale[scale == 0] = np.float32(1.0)
+    inv = (np.float32(1.0) / scale).astype(np.float32)
+    y = (x32 * inv).astype(np.float32)
+    return np.trunc(y).astype(np.int8), scale.reshape(-1)
 
 
 def quant_blocks(x: np.ndarray, block_rows: int, block_cols: int, kind: str = "fp8"):

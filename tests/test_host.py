@@ -70,6 +70,16 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc != 0 and b"invalid sizes" in lib.flygemm_last_error()
     # M == 0 is a no-op that succeeds without launching
     assert lib.flygemm_preshuffle(p, p, p, p, p, 0, 128, 256, 0, 0, -1, None) == 0
+    # per-row quantization
+    rc = lib.flygemm_quant_rows(p, p, p, 4, 12, 0, 1, 0, None)
+    assert rc != 0 and b"multiple of 8" in lib.flygemm_last_error()
+    rc = lib.flygemm_quant_rows(p, p, p, 4, 64, 0, 0, 1, None)
+    assert rc != 0 and b"fp8 output rounds to nearest" in lib.flygemm_last_error()
+    rc = lib.flygemm_quant_rows(p, p, p, 4, 64, 3, 1, 0, None)
+    assert rc != 0 and b"in_dtype" in lib.flygemm_last_error()
+    rc = lib.flygemm_quant_rows(ctypes.c_void_p(17), p, p, 4, 64, 0, 1, 0, None)
+    assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
+    assert lib.flygemm_quant_rows(p, p, p, 0, 64, 0, 1, 0, None) == 0
 
 
 @pytest.mark.parametrize("kw, exc", [

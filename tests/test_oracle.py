@@ -131,6 +131,113 @@ def test_reference_int8_cast_truncates():
     assert q_rn.tolist() == [[127, 2, 2, -2, -2, 0]]
 
 
+def _f32_round(v):
+    """Exact round-to-nearest-even of a rational to float32 (normal range), returned as a
+    Fraction: an implementation independent of numpy's float32 arithmetic."""
+    from fractions import Fraction
+    if v == 0:
+        return Fraction(0)
+    neg = v < 0
+    a = -v if neg else v
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    m = a / Fraction(2) ** (e - 23)          # in [2^23, 2^24)
+    fl = m.numerator // m.denominator
+    rem = m - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    r = Fraction(fl) * Fraction(2) ** (e - 23)
+    return -r if neg else r
+
+
+def _trunc(fr):
+    q = abs(fr.numerator) // fr.denominator
+    return -q if fr < 0 else q
+
+
+def test_quant_rows_recip_exact_rational():
+    """The reference device kernel's q = fptosi(x * f32(1 / f32(amax / 127))) recomputed with
+    exact rationals and explicit float32 rounding, on the reference test's own data
+    distribution (np.random.seed(42), uniform(-5, 5) in fp16; test_quant.py:306-307)."""
+    from fractions import Fraction
+    np.random.seed(42)
+    x = np.random.uniform(-5.0, 5.0, size=(3, 700)).astype(np.float16)
+    q, s = oq.quant_rows_recip(x)
+    for r in range(x.shape[0]):
+        amax = max(abs(Fraction(float(v))) for v in x[r])
+        scale = _f32_round(amax / 127)
+        assert Fraction(float(s[r])) == scale
+        inv = _f32_round(1 / scale)
+        want = [_trunc(_f32_round(Fraction(float(v)) * inv)) for v in x[r]]
+        assert q[r].tolist() == want
+
+
+def test_quant_rows_recip_vs_division_known_answers():
+    """Values where truncating x * (1/s) and x / s give different integers: the device-kernel
+    oracle must follow the reciprocal, the pertoken_quant oracle the quotient."""
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    found = 0
+    for _ in range(400):
+        row = rng.uniform(-5, 5, 64).astype(np.float32)
+        row[0] = np.float32(rng.uniform(3, 5))  # amax position
+        amax = max(abs(Fraction(float(v))) for v in row)
+        scale = _f32_round(amax / 127)
+        inv = _f32_round(1 / scale)
+        for k, v in enumerate(row):
+            fv = Fraction(float(v))
+            a, b = _trunc(_f32_round(fv * inv)), _trunc(_f32_round(fv / scale))
+            if a != b:
+                found += 1
+                q_r, _ = oq.quant_rows_recip(row[None, :])
+                q_d, _ = oq.quant_rows(row[None, :], "int8", rounding="truncate")
+                assert q_r[0, k] == a and q_d[0, k] == b
+        if found >= 3:
+            break
+    assert found >= 3
+
+
+def test_quant_rows_recip_reference_criterion_and_invariants():
+    """The reference test's own acceptance (|q - (x/scale).astype(int8)| <= 1, scales equal to
+    amax/127; test_quant.py:309-316, 339-349) plus truncation invariants."""
+    np.random.seed(42)
+    x = np.random.uniform(-5.0, 5.0, size=(64, 8192)).astype(np.float16)
+    xf = x.astype(np.float32)
+    q, s = oq.quant_rows_recip(x)
+    amax = np.max(np.abs(xf), axis=1)
+    ref_scale = amax / 127.0
+    ref_scale[ref_scale == 0] = 1.0
+    assert np.max(np.abs(s - ref_scale)) == 0.0
+    ref_q = (xf / ref_scale[:, None]).astype(np.int8)
+    assert np.max(np.abs(q.astype(np.int32) - ref_q.astype(np.int32))) <= 1
+    y = xf / s[:, None]
+    assert np.all(np.abs(q) <= 127)
+    assert np.all(np.abs(q.astype(np.float64)) <= np.abs(y) * (1 + 1e-6))   # toward zero
+    assert np.all(np.abs(y) - np.abs(q) < 1 + 1e-4)
+    assert np.all((q == 0) | (np.sign(q) == np.sign(xf)))
+    z, sz = oq.quant_rows_recip(np.zeros((2, 16), np.float16))
+    assert np.all(sz == 1.0) and np.all(z == 0)
+
+
+def test_quant_rows_truncate_matches_torch_cast():
+    """pertoken_quant's int8 cast is torch's .to(int8) of the float32 quotient (tests/utils.py:71)."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(50, 300, generator=g) * 3
+    x[4] = 0
+    x[5, 7] = float("inf")
+    x[6, 9] = float("nan")
+    q, s = oq.quant_rows(x.numpy(), "int8", rounding="truncate")
+    xs = torch.nan_to_num(x, nan=0.0, posinf=127.0, neginf=-127.0)
+    st = torch.maximum(xs.amax(-1, keepdim=True), -xs.amin(-1, keepdim=True)) / 127.0
+    st[st == 0] = 1
+    qt = (xs / st).to(torch.int8)
+    assert np.array_equal(s, st.view(-1).numpy())
+    assert np.array_equal(q, qt.numpy())
+
+
 def test_quant_blocks_reduces_to_rows_and_matches_product():
     from flydsl_amd import quant as pq
     rng = np.random.default_rng(3)
