@@ -34,12 +34,20 @@ from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
 
 METRIC = "FP8 GEMM TFLOP/s + % MFMA peak (large M); achieved HBM GB/s (small M)"
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = {"fp8": 5000.0, "fp8_block": 5000.0, "int8": 5000.0, "int4": 5000.0}
+MFMA_PEAK_TFLOPS = {"fp8": 5000.0, "fp8_block": 5000.0, "int8": 5000.0, "int4": 5000.0, "bf16": 2500.0,
+                    "fp16": 2500.0}
 LLC_BYTES = 256 << 20
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def _dev_flat(t, dev):
+    """Flat device operand: 1-byte types viewed as int8 (as the reference harness passes fp8),
+    2-byte types unchanged."""
+    t = t.to(dev)
+    return (t.view(torch.int8) if t.element_size() == 1 else t).view(-1)
 
 
 class Runner:
@@ -51,8 +59,8 @@ class Runner:
         per_call = ops["a"].numel() + ops["b_dev"].numel()
         copies = max(1, min(8, -(-min_rotation_bytes // per_call)))
         self.copies = copies
-        self.a = [ops["a"].to(dev).view(torch.int8).view(-1) for _ in range(copies)]
-        self.b = [ops["b_dev"].to(dev).view(torch.int8).view(-1) for _ in range(copies)]
+        self.a = [_dev_flat(ops["a"], dev) for _ in range(copies)]
+        self.b = [_dev_flat(ops["b_dev"], dev) for _ in range(copies)]
         sa = ops["sa_t"] if w.kind == "fp8_block" else ops["sa"]
         self.sa = sa.to(dev).contiguous().view(-1)
         self.sb = ops["sb"].to(dev).contiguous().view(-1)

@@ -10,7 +10,7 @@ import os
 
 from .build import OUT as LIB_PATH
 
-FLYGEMM_IN = {"fp8": 0, "int8": 1, "int4": 2}
+FLYGEMM_IN = {"fp8": 0, "int8": 1, "int4": 2, "bf16": 3, "fp16": 4}
 FLYGEMM_OUT = {"bf16": 0, "fp16": 1}
 QUANT_IN = {"fp16": 0, "bf16": 1, "fp32": 2}
 QUANT_OUT = {"fp8": 0, "int8": 1}

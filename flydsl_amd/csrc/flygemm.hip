@@ -102,12 +102,16 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
     if (kind == KIND_FP8) return bf16 ? KernelRow<KIND_FP8, EPI_ROWCOL, true>::get() : KernelRow<KIND_FP8, EPI_ROWCOL, false>::get();
     if (kind == KIND_INT8) return bf16 ? KernelRow<KIND_INT8, EPI_ROWCOL, true>::get() : KernelRow<KIND_INT8, EPI_ROWCOL, false>::get();
     if (kind == KIND_INT4) return bf16 ? KernelRow<KIND_INT4, EPI_ROWCOL, true>::get() : KernelRow<KIND_INT4, EPI_ROWCOL, false>::get();
+    if (kind == KIND_BF16) return bf16 ? KernelRow<KIND_BF16, EPI_ROWCOL, true>::get() : KernelRow<KIND_BF16, EPI_ROWCOL, false>::get();
+    if (kind == KIND_F16) return bf16 ? KernelRow<KIND_F16, EPI_ROWCOL, true>::get() : KernelRow<KIND_F16, EPI_ROWCOL, false>::get();
   } else if (epi == EPI_BLOCK) {
     if (kind == KIND_FP8) return bf16 ? KernelRow<KIND_FP8, EPI_BLOCK, true>::get() : KernelRow<KIND_FP8, EPI_BLOCK, false>::get();
   } else if (epi == EPI_RAW) {
     if (kind == KIND_FP8) return KernelRow<KIND_FP8, EPI_RAW, true>::get();
     if (kind == KIND_INT8) return KernelRow<KIND_INT8, EPI_RAW, true>::get();
     if (kind == KIND_INT4) return KernelRow<KIND_INT4, EPI_RAW, true>::get();
+    if (kind == KIND_BF16) return KernelRow<KIND_BF16, EPI_RAW, true>::get();
+    if (kind == KIND_F16) return KernelRow<KIND_F16, EPI_RAW, true>::get();
   }
   return nullptr;
 }
@@ -235,6 +239,19 @@ QuantFn quant_fn_in(int out_dtype, int mode, int nslices) {
   return nullptr;
 }
 
+// K in bytes for the kernels: 16-bit inputs have two bytes per element and need K % 64 == 0
+// (one 128-byte K tile); returns -1 after setting the error for a bad K.
+int k_bytes(int in_dtype, int K) {
+  if (in_dtype == FLYGEMM_IN_BF16 || in_dtype == FLYGEMM_IN_FP16) {
+    if (K <= 0 || K % 64 != 0) {
+      fail(hipErrorInvalidValue, "K=%d must be a multiple of 64 for 16-bit inputs (128-byte K tile)", K);
+      return -1;
+    }
+    return 2 * K;
+  }
+  return K;
+}
+
 }  // namespace
 
 extern "C" {
@@ -242,14 +259,18 @@ extern "C" {
 int flygemm_preshuffle(void* c, const void* a, const void* b, const float* scale_a, const float* scale_b,
                        int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t out_dtype,
                        int32_t variant, void* stream) {
-  int rc = check_common(c, a, b, M, N, K, variant);
-  if (rc) return rc;
-  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_INT4)
+  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_FP16)
     return fail(hipErrorInvalidValue, "in_dtype %d not supported", in_dtype);
+  const int kb = k_bytes(in_dtype, K);
+  if (kb < 0) return hipErrorInvalidValue;
+  int rc = check_common(c, a, b, M, N, kb, variant);
+  if (rc) return rc;
   if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16)
     return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
-  if (M > 0 && (!scale_a || !scale_b)) return fail(hipErrorInvalidValue, "null scale pointer");
-  GemmArgs args{c, (const uint8_t*)a, (const uint8_t*)b, scale_a, scale_b, M, N, K};
+  const bool scaled = in_dtype <= FLYGEMM_IN_INT4;
+  if (M > 0 && scaled && (!scale_a || !scale_b)) return fail(hipErrorInvalidValue, "null scale pointer");
+  GemmArgs args{c, (const uint8_t*)a, (const uint8_t*)b, scaled ? scale_a : nullptr, scaled ? scale_b : nullptr,
+                M, N, kb};
   return launch(in_dtype, EPI_ROWCOL, out_dtype, variant, args, (hipStream_t)stream);
 }
 
@@ -268,11 +289,13 @@ int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_sca
 
 int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int32_t N, int32_t K,
                          int32_t in_dtype, int32_t variant, void* stream) {
-  int rc = check_common(acc, a, b, M, N, K, variant);
-  if (rc) return rc;
-  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_INT4)
+  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_FP16)
     return fail(hipErrorInvalidValue, "in_dtype %d not supported", in_dtype);
-  GemmArgs args{acc, (const uint8_t*)a, (const uint8_t*)b, nullptr, nullptr, M, N, K};
+  const int kb = k_bytes(in_dtype, K);
+  if (kb < 0) return hipErrorInvalidValue;
+  int rc = check_common(acc, a, b, M, N, kb, variant);
+  if (rc) return rc;
+  GemmArgs args{acc, (const uint8_t*)a, (const uint8_t*)b, nullptr, nullptr, M, N, kb};
   return launch(in_dtype, EPI_RAW, FLYGEMM_OUT_BF16, variant, args, (hipStream_t)stream);
 }
 

@@ -24,7 +24,16 @@ typedef int   i32x4 __attribute__((ext_vector_type(4)));
 typedef int   i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2 };
+enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIND_F16 = 4 };
+
+// 16-bit inputs (bf16 / fp16) run through the same kernels in bytes: K counts bytes (two per
+// element), the preshuffled B layout is the 1-byte layout applied to each row's bytes
+// (reference tests/utils.py:76-96 with 8 elements per 16-byte chunk), and one
+// v_mfma_f32_16x16x32_{bf16,f16} consumes the same 64 bytes of K per row and 16 bytes per
+// lane as the int8 16x16x64 instruction.  They are not scaled (kernels/preshuffle_gemm.py:
+// 804-806, 874-877).
+constexpr bool kind_is_16bit(int k) { return k == KIND_BF16 || k == KIND_F16; }
+constexpr bool kind_float_acc(int k) { return k == KIND_FP8 || kind_is_16bit(k); }
 enum Epi : int {
   EPI_ROWCOL = 0,    // out = (acc * sa[m]) * sb[n]            (per-token / per-channel)
   EPI_BLOCK = 1,     // acc += mfma_block * (sa[kb][m] * sb[n/128][kb]) per 128-K block
@@ -43,6 +52,20 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const 
 
 __device__ __forceinline__ i32x4 mfma_i8(const i32x4& a, const i32x4& b, const i32x4& c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// One 64-byte-deep MFMA step of the int8 / bf16 / fp16 kinds on 16-byte operand fragments.
+template <int KIND, typename AccT>
+__device__ __forceinline__ AccT mfma_k64(const i32x4& b, const i32x4& a, const AccT& c) {
+  if constexpr (KIND == KIND_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b), __builtin_bit_cast(bf16x8, a), c, 0, 0, 0);
+  else if constexpr (KIND == KIND_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+  else
+    return mfma_i8(b, a, c);
 }
 
 // 4 packed int4 bytes (8 nibbles, little-endian) -> 8 sign-extended int8 in two dwords:
@@ -108,7 +131,7 @@ __device__ __forceinline__ i32x2 pack_out4(const float (&v)[4]) {
 
 struct GemmArgs {
   void* c;            // output [M][N] bf16/fp16, or int32/fp32 for EPI_RAW
-  const uint8_t* a;   // [M][K]
+  const uint8_t* a;   // [M][K] (16-bit kinds: K counts bytes)
   const uint8_t* b;   // preshuffled B
   const float* sa;    // EPI_ROWCOL: [M]; EPI_BLOCK: [K/128][M]
   const float* sb;    // EPI_ROWCOL: [N]; EPI_BLOCK: [ceil(N/128)][K/128]

@@ -37,7 +37,9 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   constexpr int B_BLK = (KIND == KIND_INT4) ? 1024 : 2048;
   constexpr size_t B_PER_K = B_BLK / KT;  // bytes of one 16-col block per K element (16 or 8)
 
-  typedef typename std::conditional<KIND == KIND_FP8 || EPI == EPI_BLOCK, f32x4, i32x4>::type AccT;
+  typedef typename std::conditional<kind_float_acc(KIND) || EPI == EPI_BLOCK, f32x4, i32x4>::type AccT;
+  // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be null)
+  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_is_16bit(KIND);
   AccT acc[MR][NBW];
 #pragma unroll
   for (int i = 0; i < MR; ++i)
@@ -130,8 +132,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
         }
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) {
-          acc[mi][j] = mfma_i8(bl, s.alo[mi], acc[mi][j]);
-          acc[mi][j] = mfma_i8(bh, s.ahi[mi], acc[mi][j]);
+          acc[mi][j] = mfma_k64<KIND>(bl, s.alo[mi], acc[mi][j]);
+          acc[mi][j] = mfma_k64<KIND>(bh, s.ahi[mi], acc[mi][j]);
         }
       }
     }
@@ -159,14 +161,14 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     for (int j = 0; j < NBW; ++j) red[wave][mi * NBW + j][lane] = acc[mi][j];
   __syncthreads();
 
-  typedef typename std::conditional<KIND == KIND_FP8 || EPI == EPI_BLOCK, float, int>::type AccE;
+  typedef typename std::conditional<kind_float_acc(KIND) || EPI == EPI_BLOCK, float, int>::type AccE;
 #pragma unroll
   for (int j = 0; j < NBW; ++j) {
     if (j % NW != wave) continue;
     const int col = (nb0 + j) * 16 + lq * 4;
     if (col >= N) continue;
     f32x4 sb4 = f32x4{1.f, 1.f, 1.f, 1.f};
-    if constexpr (EPI == EPI_ROWCOL) sb4 = *(const f32x4*)(p.sb + col);
+    if constexpr (kScaled) sb4 = *(const f32x4*)(p.sb + col);
 #pragma unroll
     for (int mi = 0; mi < MR; ++mi) {
       AccT s = red[0][mi * NBW + j][lane];
@@ -178,12 +180,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       if constexpr (EPI == EPI_RAW) {
         *(AccT*)((AccE*)p.c + idx) = s;
       } else {
-        const float s_a = (EPI == EPI_ROWCOL) ? p.sa[row] : 1.f;
+        float s_a = 1.f;
+        if constexpr (kScaled) s_a = p.sa[row];
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           v[r] = (float)s[r];
-          if constexpr (EPI == EPI_ROWCOL) v[r] = (v[r] * s_a) * sb4[r];
+          if constexpr (kScaled) v[r] = (v[r] * s_a) * sb4[r];
         }
         *(i32x2*)((typename OutT<OUT_BF16>::type*)p.c + idx) = pack_out4<OUT_BF16>(v);
       }

@@ -156,8 +156,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     }
   };
 
-  typedef typename std::conditional<KIND == KIND_FP8, f32x4, i32x4>::type AccT;
+  typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
   AccT acc[MR][NR];
+  // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be null)
+  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_is_16bit(KIND);
 
   // blockscale: the A scale of this lane's row in each MFMA row block and the B scale of
   // each 16-column block, for one K tile.  They are loaded one step ahead (into sa_n/sb_n,
@@ -254,8 +256,8 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         if (mi + 1 < MR) load_a(sA, mi + 1, alo, ahi);
 #pragma unroll
         for (int ni = 0; ni < NR; ++ni) {
-          acc[mi][ni] = mfma_i8(bl[ni], lo, acc[mi][ni]);
-          acc[mi][ni] = mfma_i8(bh[ni], hi, acc[mi][ni]);
+          acc[mi][ni] = mfma_k64<KIND>(bl[ni], lo, acc[mi][ni]);
+          acc[mi][ni] = mfma_k64<KIND>(bh[ni], hi, acc[mi][ni]);
         }
       }
     }
@@ -272,7 +274,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   auto epilogue = [&](int m0, int n0) {
     float sa_e[MR];
     f32x4 sb_e[NR];
-    if constexpr (EPI == EPI_ROWCOL) {
+    if constexpr (kScaled) {
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) sa_e[mi] = p.sa[min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
 #pragma unroll
@@ -292,11 +294,8 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
           float v[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if constexpr (KIND == KIND_FP8)
-              v[r] = acc[mi][ni][r];
-            else
-              v[r] = (float)acc[mi][ni][r];
-            if constexpr (EPI == EPI_ROWCOL) v[r] = (v[r] * sa_e[mi]) * sb_e[ni][r];
+            v[r] = (float)acc[mi][ni][r];
+            if constexpr (kScaled) v[r] = (v[r] * sa_e[mi]) * sb_e[ni][r];
           }
           __builtin_amdgcn_raw_buffer_store_b64(pack_out4<OUT_BF16>(v), rsrc_c, off, 0, 0);
         }

@@ -9,7 +9,10 @@ checks and launcher signature (reference ``kernels/preshuffle_gemm.py:39-202`` a
     launch(c, a, b_preshuffled, scale_a, scale_b, M, N, stream)
 
 computes ``c[m, n] = out_dtype((acc[m, n] * scale_a[m]) * scale_b[n])`` with
-``acc = sum_k a[m, k] * b[n, k]`` (fp32 for fp8, exact int32 for int8/int4).  Behind the
+``acc = sum_k a[m, k] * b[n, k]`` (fp32 for fp8, exact int32 for int8/int4); bf16/fp16 inputs
+are not scaled, ``c = out_dtype(acc)`` with fp32 ``acc``, and their scale arguments may be
+empty tensors, as the reference's harness passes them (``tests/kernels/
+test_preshuffle_gemm.py:183-188``).  Behind the
 launcher there is no JIT: a ctypes call into the hand-written gfx950 kernels of
 ``flydsl_amd/csrc`` (``flygemm_preshuffle`` in ``include/flygemm.h``).
 
@@ -19,10 +22,10 @@ Differences from the reference, all on purpose:
   as hints only: the kernel variant comes from the library's MI355X table, keyed on the
   run-time M, N, K.  ``variant=`` forces one (tests, tuning).
 * Any ``N % 16 == 0`` is computed in full (the reference's grid silently skips a tail
-  when ``N % tile_n != 0``); K must be a multiple of 128.
+  when ``N % tile_n != 0``); K must be a multiple of 128 (64 for bf16/fp16).
 * GPU errors raise ``RuntimeError`` (the reference prints them).
-* ``in_dtype`` "fp16"/"bf16"/"fp4" are accepted by the checks but not built for MI355X
-  yet: the launcher raises ``NotImplementedError``.
+* ``in_dtype`` "fp4" is accepted by the checks but not built for MI355X yet: the launcher
+  raises ``NotImplementedError``.
 """
 from __future__ import annotations
 
@@ -35,6 +38,7 @@ from ._launch import device_ptr, stream_handle
 
 _IN_DTYPES = ("fp8", "int8", "int4", "fp16", "bf16", "fp4")
 _OUT_TORCH = {"bf16": torch.bfloat16, "fp16": torch.float16}
+_IN_TORCH16 = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
 class PreshuffleGemm:
@@ -62,14 +66,21 @@ class PreshuffleGemm:
             raise ValueError(f"N={N} must be a multiple of 16 (preshuffle block)")
         if K % self.tile_k:
             raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
-        if K % 128:
-            raise ValueError(f"K={K} must be a multiple of 128 on MI355X")
-        b_elems = N * K // 2 if self.in_dtype == "int4" else N * K
+        is16 = self.in_dtype in ("bf16", "fp16")
+        if K % (64 if is16 else 128):
+            raise ValueError(f"K={K} must be a multiple of {64 if is16 else 128} on MI355X")
         c = device_ptr(arg_c, "arg_c", M * N, dtypes=(_OUT_TORCH[self.out_dtype],))
-        a = device_ptr(arg_a, "arg_a", M * K, elem_bytes=1)
-        b = device_ptr(arg_b, "arg_b", b_elems, elem_bytes=1)
-        sa = device_ptr(arg_scale_a, "arg_scale_a", M, dtypes=(torch.float32,))
-        sb = device_ptr(arg_scale_b, "arg_scale_b", N, dtypes=(torch.float32,))
+        if is16:
+            t = _IN_TORCH16[self.in_dtype]
+            a = device_ptr(arg_a, "arg_a", M * K, dtypes=(t,))
+            b = device_ptr(arg_b, "arg_b", N * K, dtypes=(t,))
+            sa = sb = 0  # not scaled; the reference passes empty tensors here
+        else:
+            b_elems = N * K // 2 if self.in_dtype == "int4" else N * K
+            a = device_ptr(arg_a, "arg_a", M * K, elem_bytes=1)
+            b = device_ptr(arg_b, "arg_b", b_elems, elem_bytes=1)
+            sa = device_ptr(arg_scale_a, "arg_scale_a", M, dtypes=(torch.float32,))
+            sb = device_ptr(arg_scale_b, "arg_scale_b", N, dtypes=(torch.float32,))
         lib = _lib.load()
         rc = lib.flygemm_preshuffle(c, a, b, sa, sb, M, N, K, _lib.FLYGEMM_IN[self.in_dtype],
                                     _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
@@ -150,15 +161,16 @@ def compile_preshuffle_gemm_w4(*, M: int = 0, N: int = 0, K: int, tile_m: int, t
 
 
 def accumulators(acc, a, b, M, N, K, in_dtype, variant=-1, stream=None):
-    """Raw accumulators of ``sum_k a[m,k] b[n,k]`` (int32 for int8/int4, fp32 for fp8), no
-    scaling: the value the kernels hold before the epilogue."""
+    """Raw accumulators of ``sum_k a[m,k] b[n,k]`` (int32 for int8/int4, fp32 for fp8, bf16
+    and fp16), no scaling: the value the kernels hold before the epilogue."""
     if in_dtype not in _lib.FLYGEMM_IN:
         raise ValueError(f"in_dtype must be one of {tuple(_lib.FLYGEMM_IN)}, got {in_dtype!r}")
     b_elems = N * K // 2 if in_dtype == "int4" else N * K
-    want = torch.float32 if in_dtype == "fp8" else torch.int32
+    want = torch.int32 if in_dtype in ("int8", "int4") else torch.float32
+    eb = 2 if in_dtype in ("bf16", "fp16") else 1
     p_acc = device_ptr(acc, "acc", M * N, dtypes=(want,))
-    p_a = device_ptr(a, "a", M * K, elem_bytes=1)
-    p_b = device_ptr(b, "b", b_elems, elem_bytes=1)
+    p_a = device_ptr(a, "a", M * K, elem_bytes=eb)
+    p_b = device_ptr(b, "b", b_elems, elem_bytes=eb)
     lib = _lib.load()
     rc = lib.flygemm_accumulators(p_acc, p_a, p_b, int(M), int(N), int(K), _lib.FLYGEMM_IN[in_dtype],
                                   int(variant), stream_handle(stream))

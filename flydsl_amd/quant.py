@@ -58,17 +58,22 @@ def blockscale_quant(x: torch.Tensor, block_rows: int, block_cols: int = 128, dt
 
 
 def shuffle_weight(x: torch.Tensor, layout=(16, 16)) -> torch.Tensor:
-    """Preshuffle a [N, K] 1-byte weight; returns a tensor of the same shape and dtype."""
+    """Preshuffle a [N, K] weight of 1- or 2-byte elements; returns a tensor of the same shape
+    and dtype.  Each 16-column block is laid out as 16-byte K chunks, column-interleaved
+    (reference ``tests/utils.py:76-96``: 16 elements per chunk for 1-byte types, 8 for
+    2-byte ones) -- the same permutation of each row's bytes in both cases."""
     if tuple(layout) != (16, 16):
         raise ValueError(f"only layout=(16, 16) is supported, got {layout!r}")
-    if x.element_size() != 1:
-        raise ValueError(f"shuffle_weight expects 1-byte elements, got {x.dtype}")
+    es = x.element_size()
+    if es not in (1, 2):
+        raise ValueError(f"shuffle_weight expects 1- or 2-byte elements, got {x.dtype}")
     N, K = x.shape[-2], x.shape[-1]
     if N % 16 or K % 32:
         raise ValueError(f"B shape [{N}, {K}] must have N % 16 == 0 and K % 32 == 0")
-    u = x.contiguous().view(torch.uint8)
-    t = u.view(-1, N // 16, 16, K // 32, 2, 16).permute(0, 1, 3, 4, 2, 5).contiguous()
-    return t.view(x.shape).view(x.dtype)
+    kb = K * es
+    u = x.contiguous().view(torch.uint8).reshape(-1, N, kb)
+    t = u.view(-1, N // 16, 16, kb // 32, 2, 16).permute(0, 1, 3, 4, 2, 5).contiguous()
+    return t.view(torch.uint8).reshape(x.shape[:-1] + (kb,)).view(x.dtype).reshape(x.shape)
 
 
 def pack_int4(x_shuffled: torch.Tensor) -> torch.Tensor:

@@ -17,7 +17,7 @@ from . import quant
 @dataclass(frozen=True)
 class Workload:
     name: str
-    kind: str          # "fp8" | "int8" | "int4" | "fp8_block"
+    kind: str          # "fp8" | "int8" | "int4" | "fp8_block" | "bf16" | "fp16"
     M: int
     N: int
     K: int
@@ -34,6 +34,8 @@ class Workload:
         """Algorithmic bytes: A + B + C(bf16) + fp32 scales (reference test_preshuffle_gemm.py:254,
         test_blockscale_preshuffle_gemm.py:222)."""
         M, N, K = self.M, self.N, self.K
+        if self.kind in ("bf16", "fp16"):
+            return 2 * (M * K + N * K + M * N)   # no scales
         b = N * K // 2 if self.kind == "int4" else N * K
         base = M * K + b + 2 * M * N
         if self.kind == "fp8_block":
@@ -48,6 +50,7 @@ WORKLOADS = {
     "C4": Workload("C4", "fp8_block", 1024, 7168, 7168, 3, note="FP8 1x128/128x128 blockscale"),
     "C5": Workload("C5", "int4", 256, 14336, 4096, 4, b_std=0.02, note="W4A8"),
     "T": Workload("T", "fp8", 8192, 8192, 8192, 5, note="FP8 8192^3, MFMA-bound target"),
+    "T16": Workload("T16", "bf16", 8192, 8192, 8192, 6, note="BF16 8192^3 (in_dtype='bf16', unscaled)"),
 }
 
 
@@ -61,7 +64,8 @@ def make_operands(w: Workload) -> dict:
     Keys: ``a`` (A quantized, [M, K]), ``b`` (B quantized, unshuffled [N, K], int8 values for
     int4), ``b_dev`` (the B buffer the kernel reads: shuffled, int4 packed), ``sa``, ``sb``
     (fp32 scales; blockscale: ``sa`` is [M, K/128] and ``sa_t`` its [K/128, M] transpose,
-    ``sb`` is [N/128, K/128]).
+    ``sb`` is [N/128, K/128]; bf16/fp16: A and B are the inputs cast to that type and the
+    scales are empty).
     """
     g = torch.Generator().manual_seed(w.seed)
     a32 = torch.randn(w.M, w.K, generator=g, dtype=torch.float32)
@@ -83,6 +87,10 @@ def make_operands(w: Workload) -> dict:
         b, sb = quant.blockscale_quant(b32p, 128, 128)
         b = b[: w.N].contiguous()
         out["sa_t"] = sa.t().contiguous()
+    elif w.kind in ("bf16", "fp16"):
+        dt = torch.bfloat16 if w.kind == "bf16" else torch.float16
+        a, b = a32.to(dt), b32.to(dt)
+        sa = sb = torch.empty(0, dtype=torch.float32)
     else:
         raise ValueError(f"unknown kind {w.kind!r}")
     del a32, b32

@@ -14,8 +14,10 @@
  *    reference's `shuffle_weight(b, layout=(16, 16))` (tests/utils.py:76-96): element
  *    (n, k) at byte (n/16)*16*K + (k/16)*256 + (n%16)*16 + (k%16).  INT4 B is that buffer
  *    packed two values per byte as in tests/kernels/test_preshuffle_gemm.py:165-174.
- *  - Requirements: N % 16 == 0, K % 128 == 0, M >= 0 (M == 0 is a no-op), every operand
- *    below 2^31 elements.  Violations return nonzero without launching.
+ *    bf16/fp16 B uses the same rule on each row's bytes (8 elements per 16-byte chunk), which
+ *    is what shuffle_weight produces for 2-byte elements.
+ *  - Requirements: N % 16 == 0, K % 128 == 0 (K % 64 == 0 for bf16/fp16), M >= 0 (M == 0 is
+ *    a no-op), every operand below 2^31 bytes.  Violations return nonzero without launching.
  *  - Return value: 0 on success, otherwise a hipError_t code; flygemm_last_error() gives
  *    the message of the calling thread's last failure.
  *  - `variant`: -1 picks the kernel from the built-in table; 0..flygemm_num_variants()-1
@@ -33,12 +35,15 @@ extern "C" {
 enum {
   FLYGEMM_IN_FP8 = 0,  /* OCP e4m3fn (torch.float8_e4m3fn) */
   FLYGEMM_IN_INT8 = 1, /* int8 A and B */
-  FLYGEMM_IN_INT4 = 2  /* int8 A, packed signed int4 B */
+  FLYGEMM_IN_INT4 = 2, /* int8 A, packed signed int4 B */
+  FLYGEMM_IN_BF16 = 3, /* bf16 A and B, no scaling (scale pointers ignored) */
+  FLYGEMM_IN_FP16 = 4  /* fp16 A and B, no scaling (scale pointers ignored) */
 };
 enum { FLYGEMM_OUT_BF16 = 0, FLYGEMM_OUT_FP16 = 1 };
 
 /* C[M][N] = out_dtype((acc[m][n] * scale_a[m]) * scale_b[n]),
- * acc = sum_k A[m][k] * B[n][k] in fp32 (fp8) or int32 (int8/int4).
+ * acc = sum_k A[m][k] * B[n][k] in fp32 (fp8, bf16, fp16) or int32 (int8/int4);
+ * bf16/fp16 inputs are not scaled: C = out_dtype(acc) (reference preshuffle_gemm.py:804-806).
  * scale_a: fp32 [M] per token; scale_b: fp32 [N] per output channel.
  * Replaces the launcher returned by compile_preshuffle_gemm_a8
  * (reference kernels/preshuffle_gemm.py:39-57, launch_gemm :1268-1301; epilogue :863-883). */
@@ -56,7 +61,7 @@ int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_sca
                        int32_t M, int32_t N, int32_t K, int32_t scale_block_k, int32_t out_dtype,
                        int32_t variant, void* stream);
 
-/* Raw accumulators, no scaling: int32 [M][N] for int8/int4, fp32 [M][N] for fp8.
+/* Raw accumulators, no scaling: int32 [M][N] for int8/int4, fp32 [M][N] for fp8/bf16/fp16.
  * Exposes the value the reference's kernels hold before their epilogue
  * (kernels/preshuffle_gemm.py:643-797) so integer paths can be checked bit-exactly. */
 int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int32_t N, int32_t K,

@@ -1,7 +1,9 @@
 """Dequantize-then-matmul oracles and the fused epilogue (test infrastructure only).
 
 * ``run_torch``            restates ``tests/kernels/test_preshuffle_gemm.py:55-65``:
-                           ``mm(a.float() * sa[:, None], (b.float() * sb[:, None]).T)``.
+                           ``mm(a.float() * sa[:, None], (b.float() * sb[:, None]).T)``;
+                           for bf16/fp16 inputs (bit patterns, uint16) there are no scales
+                           (``:146-151``): ``mm(a.float(), b.float().T)``.
 * ``run_torch_blockscale`` restates ``tests/kernels/test_blockscale_preshuffle_gemm.py:86-109``:
                            A scales expanded over 1x128 blocks, B scales over 128x128 blocks
                            (``w_scale.view(-1,1).repeat(...).permute(0,2,1,3)``), then
@@ -25,10 +27,14 @@ from __future__ import annotations
 
 import numpy as np
 
-from .numerics import bf16_rne, e4m3fn_decode
+from .numerics import bf16_rne, bf16_to_f32, e4m3fn_decode, f16_to_f32
 
 
-def dequant_rows(q: np.ndarray, scale: np.ndarray, kind: str, dtype=np.float32) -> np.ndarray:
+def dequant_rows(q: np.ndarray, scale, kind: str, dtype=np.float32) -> np.ndarray:
+    if kind == "bf16":
+        return bf16_to_f32(q).astype(dtype)
+    if kind == "fp16":
+        return f16_to_f32(q).astype(dtype)
     v = e4m3fn_decode(q) if kind == "fp8" else np.asarray(q).view(np.int8).astype(np.float32)
     out = (v * np.asarray(scale, dtype=np.float32).reshape(-1, 1)).astype(np.float32)
     return out.astype(dtype)

@@ -20,10 +20,17 @@ import numpy as np
 
 
 def shuffle_weight(b: np.ndarray) -> np.ndarray:
-    """[N, K] 1-byte elements -> same-size array in preshuffle order (returned flat)."""
+    """[N, K] 1- or 2-byte elements -> the preshuffled bytes (returned flat, uint8 for 2-byte
+    input).  For 2-byte elements the reference groups 8 elements per 16-byte chunk
+    (``tests/utils.py:83-90``), which is the 1-byte rule applied to each row's 2K bytes."""
+    b = np.ascontiguousarray(b)
     N, K = b.shape
     assert N % 16 == 0 and K % 32 == 0
-    t = np.ascontiguousarray(b).reshape(N // 16, 16, K // 32, 2, 16).transpose(0, 2, 3, 1, 4)
+    if b.dtype.itemsize == 2:
+        b = b.view(np.uint8).reshape(N, 2 * K)
+        K = 2 * K
+    assert b.dtype.itemsize == 1
+    t = b.reshape(N // 16, 16, K // 32, 2, 16).transpose(0, 2, 3, 1, 4)
     return np.ascontiguousarray(t).reshape(-1)
 
 

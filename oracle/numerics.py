@@ -83,5 +83,10 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
     return (np.asarray(bits).view(np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """IEEE binary16 bit patterns (uint16) -> float32 (exact)."""
+    return np.asarray(bits).view(np.uint16).view(np.float16).astype(np.float32)
+
+
 def round_half_even(x: np.ndarray) -> np.ndarray:
     return np.rint(x)

@@ -18,19 +18,31 @@ def u8(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.uint8).numpy() if t.dtype != torch.uint8 else t.numpy()
 
 
+def dev_flat(t: torch.Tensor, device) -> torch.Tensor:
+    """Flat device view the launchers take: 1-byte types as int8 (fp8 is passed as int8, as
+    in the reference harness), 2-byte types unchanged."""
+    t = t.to(device)
+    return (t.view(torch.int8) if t.element_size() == 1 else t).view(-1)
+
+
+def bits16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
 def launch(ops, device, variant=-1, out_dtype="bf16", stream=None):
     """Run the drop-in launcher for ``ops`` (from ``flydsl_amd.workloads.make_operands``)."""
     w = ops["workload"]
     M, N, K = w.M, w.N, w.K
-    a = ops["a"].to(device).view(torch.int8).view(-1)
-    b = ops["b_dev"].to(device).view(torch.int8).view(-1)
+    a = dev_flat(ops["a"], device)
+    b = dev_flat(ops["b_dev"], device)
     c = torch.empty(M, N, dtype=OUT_TORCH[out_dtype], device=device)
     if w.kind == "fp8_block":
         fn = compile_blockscale_preshuffle_gemm(M=M, N=N, K=K, tile_m=64, tile_n=64, tile_k=128,
                                                 out_dtype=out_dtype, variant=variant)
         fn(c.view(-1), a, b, ops["sa_t"].to(device).view(-1), ops["sb"].to(device).view(-1), M, N, stream)
     else:
-        fn = compile_preshuffle_gemm_a8(K=K, tile_m=64, tile_n=128, tile_k=128, in_dtype=w.kind,
+        tk = 64 if w.kind in ("bf16", "fp16") else 128  # 128 bytes of K either way
+        fn = compile_preshuffle_gemm_a8(K=K, tile_m=64, tile_n=128, tile_k=tk, in_dtype=w.kind,
                                         out_dtype=out_dtype, variant=variant)
         fn(c.view(-1), a, b, ops["sa"].to(device).view(-1), ops["sb"].to(device).view(-1), M, N, stream)
     return c
@@ -39,15 +51,20 @@ def launch(ops, device, variant=-1, out_dtype="bf16", stream=None):
 def raw_acc(ops, device, variant=-1):
     w = ops["workload"]
     kind = "fp8" if w.kind == "fp8_block" else w.kind
-    acc = torch.empty(w.M, w.N, dtype=torch.float32 if kind == "fp8" else torch.int32, device=device)
-    accumulators(acc, ops["a"].to(device).view(torch.int8), ops["b_dev"].to(device).view(torch.int8),
-                 w.M, w.N, w.K, kind, variant=variant)
+    acc = torch.empty(w.M, w.N, dtype=torch.int32 if kind in ("int8", "int4") else torch.float32, device=device)
+    accumulators(acc, dev_flat(ops["a"], device), dev_flat(ops["b_dev"], device), w.M, w.N, w.K, kind,
+                 variant=variant)
     return acc
 
 
 def reference(ops, rows=None):
     """Oracle output: float64 [M, N] (fp8 paths) or exact int32 accumulators (int paths)."""
     w = ops["workload"]
+    if w.kind in ("bf16", "fp16"):
+        a = bits16(ops["a"])
+        if rows is not None:
+            a = a[rows]
+        return og.run_torch(a, bits16(ops["b"]), None, None, w.kind, "f64")
     a = u8(ops["a"])
     b = u8(ops["b"])
     if rows is not None:

@@ -80,6 +80,10 @@ def test_abi_rejects_bad_arguments_before_launch():
     rc = lib.flygemm_quant_rows(ctypes.c_void_p(17), p, p, 4, 64, 0, 1, 0, None)
     assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
     assert lib.flygemm_quant_rows(p, p, p, 0, 64, 0, 1, 0, None) == 0
+    # 16-bit inputs: K counts elements and must be a multiple of 64; scales are not needed
+    rc = lib.flygemm_preshuffle(p, p, p, None, None, 16, 128, 96, 3, 0, -1, None)
+    assert rc != 0 and b"multiple of 64" in lib.flygemm_last_error()
+    assert lib.flygemm_preshuffle(p, p, p, None, None, 0, 128, 192, 4, 0, -1, None) == 0
 
 
 @pytest.mark.parametrize("kw, exc", [
@@ -101,9 +105,14 @@ def test_compile_validation_matches_reference(kw, exc):
 def test_w4_entry_and_unbuilt_dtypes():
     with pytest.raises(NotImplementedError):
         compile_preshuffle_gemm_w4(K=256, tile_m=64, tile_n=128, tile_k=128, a_dtype="fp8")
-    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="bf16")
+    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp4")
     with pytest.raises(NotImplementedError):
         fn(None, None, None, None, None, 16, 128, None)
+    # bf16 is built: host tensors are rejected by the argument checks, before any launch
+    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="bf16")
+    x = torch.empty(16 * 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        fn(torch.empty(16 * 128, dtype=torch.bfloat16), x, x, None, None, 16, 128, None)
 
 
 def test_launcher_rejects_host_tensors_and_bad_shapes():

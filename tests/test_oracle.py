@@ -272,6 +272,48 @@ def test_shuffle_matches_product():
     assert np.array_equal(got, ol.shuffle_weight(b))
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_shuffle_2byte_bruteforce(dt):
+    """2-byte elements: the reference groups 8 elements per 16-byte chunk
+    (tests/utils.py:83-90: view(-1, N/16, 16, K/32, 4, 8).permute(0, 1, 3, 4, 2, 5)); element
+    (n, k) lands at [n//16][k//32][(k//8)%4][n%16][k%8] -- checked element by element."""
+    N, K = 32, 96
+    x = (torch.randn(N, K) * 5).to(dt)
+    bits = x.view(torch.int16).numpy().view(np.uint16)
+    got = ol.shuffle_weight(bits).view(np.uint16)
+    want = np.empty(N * K, dtype=np.uint16)
+    for n in range(N):
+        for k in range(K):
+            idx = (((n // 16) * (K // 32) + k // 32) * 4 + (k // 8) % 4) * 128 + (n % 16) * 8 + k % 8
+            want[idx] = bits[n, k]
+    assert np.array_equal(got, want)
+    from flydsl_amd import quant as pq
+    assert np.array_equal(pq.shuffle_weight(x).contiguous().view(torch.int16).numpy().view(np.uint16).reshape(-1), got)
+
+
+@pytest.mark.parametrize("kind,dt", [("bf16", torch.bfloat16), ("fp16", torch.float16)])
+def test_run_torch_16bit_matches_torch_and_loop(kind, dt):
+    g = torch.Generator().manual_seed(4)
+    a = (torch.randn(9, 64, generator=g) * 3).to(dt)
+    b = (torch.randn(20, 64, generator=g) * 3).to(dt)
+    ab = a.view(torch.int16).numpy().view(np.uint16)
+    bb = b.view(torch.int16).numpy().view(np.uint16)
+    ref32 = og.run_torch(ab, bb, None, None, kind)
+    # float32 BLAS (numpy vs torch) differs only by accumulation rounding: bound by K ulps of sum|a||b|
+    mag = (a.float().abs() @ b.float().abs().T).numpy()
+    assert np.all(np.abs(ref32 - (a.float() @ b.float().T).numpy()) <= 64 * 2.0 ** -23 * mag)
+    ref64 = og.run_torch(ab, bb, None, None, kind, "f64")
+    af, bf = a.double().numpy(), b.double().numpy()
+    loop = np.array([[sum(af[m, k] * bf[n, k] for k in range(64)) for n in range(20)] for m in range(9)])
+    assert np.allclose(ref64, loop, rtol=1e-12, atol=1e-12)
+    # the decode itself: every 16-bit pattern that is finite
+    allbits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    t = torch.from_numpy(allbits.view(np.int16).copy()).view(dt).float().numpy()
+    d = on.bf16_to_f32(allbits) if kind == "bf16" else on.f16_to_f32(allbits)
+    fin = np.isfinite(t)
+    assert np.array_equal(np.isfinite(d), fin) and np.array_equal(t[fin].view(np.uint32), d[fin].view(np.uint32))
+
+
 def test_int4_pack_unpack_exhaustive():
     from flydsl_amd import quant as pq
     vals = np.arange(-8, 8, dtype=np.int8)
