@@ -208,6 +208,55 @@ def copy_bytes(nbytes: int, n: int = 5):
     log(f"[bench] {n} copies of {nbytes} bytes done")
 
 
+def vs_library(n: int = 50):
+    """Context for the roofline fractions: the same shapes through ROCm's own GEMM library
+    (hipBLASLt via torch._scaled_mm / torch._int_mm / torch.mm), operands resident and reused,
+    per-tensor and per-row scales.  Prints one JSON line; nothing here is the product path."""
+    dev = torch.device("cuda:0")
+
+    def timeit(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name in ("T", "C1", "C2", "C4"):
+        w = workloads.WORKLOADS[name]
+        a = torch.randn(w.M, w.K, device=dev, generator=g).to(torch.float8_e4m3fn)
+        b = torch.randn(w.N, w.K, device=dev, generator=g).to(torch.float8_e4m3fn)
+        for mode in ("tensor", "rowwise"):
+            sa = torch.ones((), device=dev) if mode == "tensor" else torch.ones(w.M, 1, device=dev)
+            sb = torch.ones((), device=dev) if mode == "tensor" else torch.ones(1, w.N, device=dev)
+            try:
+                ms = timeit(lambda: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16))
+                res[f"{name}_fp8_{mode}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(w.flops / ms / 1e9, 1)}
+            except Exception as e:  # a scaling mode the library lacks
+                res[f"{name}_fp8_{mode}"] = {"error": f"{type(e).__name__}: {str(e)[:120]}"}
+        del a, b
+    for name, dt in (("C3", torch.int8), ("T16", torch.bfloat16)):
+        w = workloads.WORKLOADS[name]
+        if dt == torch.int8:
+            a = torch.randint(-127, 127, (w.M, w.K), device=dev, dtype=dt, generator=g)
+            b = torch.randint(-127, 127, (w.N, w.K), device=dev, dtype=dt, generator=g)
+            fn = lambda: torch._int_mm(a, b.t())
+        else:
+            a = torch.randn(w.M, w.K, device=dev, dtype=dt, generator=g)
+            b = torch.randn(w.N, w.K, device=dev, dtype=dt, generator=g)
+            fn = lambda: torch.mm(a, b.t())
+        ms = timeit(fn)
+        res[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(w.flops / ms / 1e9, 1)}
+        del a, b
+    print(json.dumps({"library": "hipBLASLt (torch)", "results": res}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,6 +269,7 @@ def main():
     ap.add_argument("--launches-only", default="", help="profiling: only launch this workload --n times")
     ap.add_argument("--n", type=int, default=20)
     ap.add_argument("--copy-bytes", type=int, default=0, help="profiling: copy this many bytes on the GPU")
+    ap.add_argument("--vs-library", action="store_true", help="time the same shapes through hipBLASLt (context)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no "
@@ -235,6 +285,9 @@ def main():
         return
     if args.copy_bytes:
         copy_bytes(args.copy_bytes)
+        return
+    if args.vs_library:
+        vs_library()
         return
 
     w = workloads.WORKLOADS[args.workload]
