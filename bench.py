@@ -35,7 +35,7 @@ from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
 METRIC = "FP8 GEMM TFLOP/s + % MFMA peak (large M); achieved HBM GB/s (small M)"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"fp8": 5000.0, "fp8_block": 5000.0, "int8": 5000.0, "int4": 5000.0, "bf16": 2500.0,
-                    "fp16": 2500.0}
+                    "fp16": 2500.0, "mxfp4": 10100.0}
 LLC_BYTES = 256 << 20
 
 
@@ -70,9 +70,10 @@ class Runner:
                                                          out_dtype="bf16")
         else:
             self.fn = compile_preshuffle_gemm_a8(M=w.M, N=w.N, K=w.K, tile_m=128, tile_n=128, tile_k=128,
-                                                 in_dtype=w.kind, out_dtype="bf16")
+                                                 in_dtype="fp4" if w.kind == "mxfp4" else w.kind, out_dtype="bf16")
         self.variant = _lib.variants()[_lib.load().flygemm_select_variant(
-            w.M, w.N, w.K, _lib.FLYGEMM_IN.get(w.kind, 0), int(w.kind == "fp8_block"))]
+            w.M, w.N, w.K, _lib.FLYGEMM_IN.get("fp4" if w.kind == "mxfp4" else w.kind, 0),
+            int(w.kind == "fp8_block"))]
         del ops
 
     def launch(self, i, stream):

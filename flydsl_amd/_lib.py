@@ -10,8 +10,8 @@ import os
 
 from .build import OUT as LIB_PATH
 
-FLYGEMM_IN = {"fp8": 0, "int8": 1, "int4": 2, "bf16": 3, "fp16": 4}
-FLYGEMM_OUT = {"bf16": 0, "fp16": 1}
+FLYGEMM_IN = {"fp8": 0, "int8": 1, "int4": 2, "bf16": 3, "fp16": 4, "fp4": 5}
+FLYGEMM_OUT = {"bf16": 0, "fp16": 1, "fp32": 2}
 QUANT_IN = {"fp16": 0, "bf16": 1, "fp32": 2}
 QUANT_OUT = {"fp8": 0, "int8": 1}
 QUANT_MODE = {"recip_trunc": 0, "div_trunc": 1, "div_nearest": 2}
@@ -25,6 +25,7 @@ SIGNATURES = [
     ("flygemm_blockscale", ctypes.c_int, [_P, _P, _P, _F, _F, _I, _I, _I, _I, _I, _I, _P]),
     ("flygemm_accumulators", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     ("flygemm_quant_rows", ctypes.c_int, [_P, _F, _P, _I, _I, _I, _I, _I, _P]),
+    ("flygemm_mxfp4", ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     ("flygemm_num_variants", ctypes.c_int32, []),
     ("flygemm_variant_name", ctypes.c_char_p, [_I]),
     ("flygemm_select_variant", ctypes.c_int32, [_I, _I, _I, _I, _I]),

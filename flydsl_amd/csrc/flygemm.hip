@@ -104,6 +104,7 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
     if (kind == KIND_INT4) return bf16 ? KernelRow<KIND_INT4, EPI_ROWCOL, true>::get() : KernelRow<KIND_INT4, EPI_ROWCOL, false>::get();
     if (kind == KIND_BF16) return bf16 ? KernelRow<KIND_BF16, EPI_ROWCOL, true>::get() : KernelRow<KIND_BF16, EPI_ROWCOL, false>::get();
     if (kind == KIND_F16) return bf16 ? KernelRow<KIND_F16, EPI_ROWCOL, true>::get() : KernelRow<KIND_F16, EPI_ROWCOL, false>::get();
+    if (kind == KIND_FP4) return bf16 ? KernelRow<KIND_FP4, EPI_ROWCOL, true>::get() : KernelRow<KIND_FP4, EPI_ROWCOL, false>::get();
   } else if (epi == EPI_BLOCK) {
     if (kind == KIND_FP8) return bf16 ? KernelRow<KIND_FP8, EPI_BLOCK, true>::get() : KernelRow<KIND_FP8, EPI_BLOCK, false>::get();
   } else if (epi == EPI_RAW) {
@@ -112,13 +113,13 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
     if (kind == KIND_INT4) return KernelRow<KIND_INT4, EPI_RAW, true>::get();
     if (kind == KIND_BF16) return KernelRow<KIND_BF16, EPI_RAW, true>::get();
     if (kind == KIND_F16) return KernelRow<KIND_F16, EPI_RAW, true>::get();
+    if (kind == KIND_FP4) return KernelRow<KIND_FP4, EPI_RAW, true>::get();
   }
   return nullptr;
 }
 
 int select_variant(int M, int N, int K, int kind, int epi) {
   (void)K;
-  (void)kind;
   if (M <= 64) {
     // decode family: fewest rows that cover M, then the most column blocks per workgroup
     // that still leaves about one workgroup per CU
@@ -128,6 +129,7 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     for (int v = kFirstDecode; v < kNumShapes; ++v) {
       if (kShapes[v].bm != rows) continue;
       const int nbw = kShapes[v].bn / 16;
+      if (kind == KIND_FP4 && nbw > 4) continue;  // MXFP4's scale words push 7 blocks past the register file
       if (best < 0 || (nblk / nbw >= 240 && nbw > kShapes[best].bn / 16)) best = v;
     }
     return best;
@@ -327,6 +329,21 @@ int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int3
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of quant_rows failed: %s", hipGetErrorString(e));
   return 0;
+}
+
+int flygemm_mxfp4(void* c, const void* a, const void* b, const void* scale_a, const void* scale_b, int32_t M,
+                  int32_t N, int32_t K, int32_t out_dtype, int32_t variant, void* stream) {
+  if (K <= 0 || K % 256 != 0)
+    return fail(hipErrorInvalidValue, "K=%d must be a multiple of 256 (8 scale blocks of 32 per K tile)", K);
+  if (N % 32 != 0) return fail(hipErrorInvalidValue, "N=%d must be a multiple of 32 (scale groups)", N);
+  int rc = check_common(c, a, b, M, N, K / 2, variant);
+  if (rc) return rc;
+  if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16 && out_dtype != FLYGEMM_OUT_F32)
+    return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
+  if (M > 0 && (!scale_a || !scale_b)) return fail(hipErrorInvalidValue, "null scale pointer");
+  GemmArgs args{c, (const uint8_t*)a, (const uint8_t*)b, (const float*)scale_a, (const float*)scale_b, M, N, K / 2};
+  if (out_dtype == FLYGEMM_OUT_F32) return launch(KIND_FP4, EPI_RAW, FLYGEMM_OUT_BF16, variant, args, (hipStream_t)stream);
+  return launch(KIND_FP4, EPI_ROWCOL, out_dtype, variant, args, (hipStream_t)stream);
 }
 
 int32_t flygemm_num_variants(void) { return kNumShapes; }

@@ -24,7 +24,7 @@ typedef int   i32x4 __attribute__((ext_vector_type(4)));
 typedef int   i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIND_F16 = 4 };
+enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIND_F16 = 4, KIND_FP4 = 5 };
 
 // 16-bit inputs (bf16 / fp16) run through the same kernels in bytes: K counts bytes (two per
 // element), the preshuffled B layout is the 1-byte layout applied to each row's bytes
@@ -33,7 +33,18 @@ enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIN
 // lane as the int8 16x16x64 instruction.  They are not scaled (kernels/preshuffle_gemm.py:
 // 804-806, 874-877).
 constexpr bool kind_is_16bit(int k) { return k == KIND_BF16 || k == KIND_F16; }
-constexpr bool kind_float_acc(int k) { return k == KIND_FP8 || kind_is_16bit(k); }
+constexpr bool kind_float_acc(int k) { return k == KIND_FP8 || kind_is_16bit(k) || k == KIND_FP4; }
+// kinds whose epilogue applies no per-token / per-channel scale (MXFP4 scales live inside the MFMA)
+constexpr bool kind_unscaled(int k) { return kind_is_16bit(k) || k == KIND_FP4; }
+
+// MXFP4 (KIND_FP4): A packed e2m1 [M][K/2] bytes, B the preshuffled packed bytes (the 1-byte
+// layout on rows of K/2 bytes), one E8M0 scale per 32 elements of K.  K here counts bytes, so a
+// 128-byte K tile holds 256 elements = 8 scale blocks, consumed by two 16x16x128 MFMAs (h = 0,
+// 1).  In MFMA h, lane group g = lane/16 supplies the 32 elements of scale block 4h + g, i.e.
+// 16-byte chunk 4h + g of the tile, and its scale.  Scales arrive in the reference's shuffled
+// order (tests/kernels/utils/fp4_utils.py:624-653): for 32 rows (or columns) r1 and K tile kt,
+// lane l reads the 32-bit word (r1 * ktiles + kt) * 64 + l, whose byte 2h + p is the scale of
+// 16-row block p (0/1) of the 32 for MFMA h -- the byte the MFMA's op_sel picks.
 enum Epi : int {
   EPI_ROWCOL = 0,    // out = (acc * sa[m]) * sb[n]            (per-token / per-channel)
   EPI_BLOCK = 1,     // acc += mfma_block * (sa[kb][m] * sb[n/128][kb]) per 128-K block
@@ -66,6 +77,17 @@ __device__ __forceinline__ AccT mfma_k64(const i32x4& b, const i32x4& a, const A
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
   else
     return mfma_i8(b, a, c);
+}
+
+// v_mfma_scale_f32_16x16x128_f8f6f4 with both operands e2m1 (format 4); an fp4 operand is
+// 16 bytes per lane, passed in the low half of the 8-dword operand.  H (0/1) is the MFMA's half
+// of the 128-byte K tile; op_sel 2H picks byte 2H of each scale word, so callers pass the word
+// shifted right by 8 bits for an odd 16-row (16-column) block, whose scale is byte 2H + 1.
+template <int H>
+__device__ __forceinline__ f32x4 mfma_fp4(const i32x4& b, const i32x4& a, const f32x4& c, uint32_t sb, uint32_t sa) {
+  const i32x8 b8 = i32x8{b.x, b.y, b.z, b.w, 0, 0, 0, 0};
+  const i32x8 a8 = i32x8{a.x, a.y, a.z, a.w, 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b8, a8, c, 4, 4, 2 * H, (int)sb, 2 * H, (int)sa);
 }
 
 // 4 packed int4 bytes (8 nibbles, little-endian) -> 8 sign-extended int8 in two dwords:

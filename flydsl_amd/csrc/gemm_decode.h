@@ -38,8 +38,10 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   constexpr size_t B_PER_K = B_BLK / KT;  // bytes of one 16-col block per K element (16 or 8)
 
   typedef typename std::conditional<kind_float_acc(KIND) || EPI == EPI_BLOCK, f32x4, i32x4>::type AccT;
-  // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be null)
-  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_is_16bit(KIND);
+  // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be
+  // null, nor to MXFP4, whose block scales are applied by the MFMA)
+  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_unscaled(KIND);
+  constexpr int MQ = (MR + 1) / 2;
   AccT acc[MR][NBW];
 #pragma unroll
   for (int i = 0; i < MR; ++i)
@@ -67,6 +69,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     i32x4 blo[NBW], bhi[NBW];
     i32x2 b4lo[NBW], b4hi[NBW];
     float sa[MR], sb[NBW];  // blockscale: this K tile's A scale per row block, B scale per column block
+    uint32_t fa[MQ], fb[NBW];  // MXFP4: scale words, already shifted to the block's byte pair
   };
   Stage st[UNROLL];
   auto load = [&](Stage& s, int kt) {
@@ -87,7 +90,18 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       s.alo[mi] = *(const i32x4*)src;
       s.ahi[mi] = *(const i32x4*)(src + 64);
     }
-    // blockscale scales travel with the stage, so their latency hides behind the pipeline
+    // blockscale / MXFP4 scales travel with the stage, so their latency hides behind the pipeline
+    if constexpr (KIND == KIND_FP4) {
+      const uint32_t* wa = (const uint32_t*)p.sa;
+      const uint32_t* wb = (const uint32_t*)p.sb;
+#pragma unroll
+      for (int q = 0; q < MQ; ++q) s.fa[q] = wa[((size_t)min(q, (M + 31) / 32 - 1) * nk + kt) * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const int nb = min(nb0 + j, nblk_max);
+        s.fb[j] = wb[((size_t)(nb >> 1) * nk + kt) * 64 + lane] >> (8 * (nb & 1));
+      }
+    }
     if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) s.sa[mi] = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
@@ -132,8 +146,14 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
         }
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) {
-          acc[mi][j] = mfma_k64<KIND>(bl, s.alo[mi], acc[mi][j]);
-          acc[mi][j] = mfma_k64<KIND>(bh, s.ahi[mi], acc[mi][j]);
+          if constexpr (KIND == KIND_FP4) {
+            const uint32_t saw = s.fa[mi >> 1] >> (8 * (mi & 1));
+            acc[mi][j] = mfma_fp4<0>(bl, s.alo[mi], acc[mi][j], s.fb[j], saw);
+            acc[mi][j] = mfma_fp4<1>(bh, s.ahi[mi], acc[mi][j], s.fb[j], saw);
+          } else {
+            acc[mi][j] = mfma_k64<KIND>(bl, s.alo[mi], acc[mi][j]);
+            acc[mi][j] = mfma_k64<KIND>(bh, s.ahi[mi], acc[mi][j]);
+          }
         }
       }
     }

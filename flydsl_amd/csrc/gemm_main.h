@@ -19,6 +19,14 @@
 //   B: the preshuffled bytes copied verbatim: per 16-column block a 2 KB run
 //      [chunk 0..7][col 0..15][16 B] (INT4: 1 KB [chunk][col][8 B]); lanes that read one
 //      chunk read 256 (128) contiguous bytes.
+//   Scales of the K tile, when the kernel has per-K-tile scales (blockscale, MXFP4), after B:
+//      they travel with the tile through the same DMA and barrier, so no separate vector
+//      memory load has to be waited for inside a step (such a wait would also drain the
+//      next step's DMA, which vector memory counters track in issue order).
+//      Blockscale: A's BM fp32 scales of the tile (x_scale_t[kt][m0..], 4-byte DMA, since
+//      those rows need not be 16-byte aligned), then w_scale[n/128][kt] of each 128-column
+//      block.  MXFP4: the 256-byte lane-word block of every 32-row group of A, then of every
+//      32-column group of B (16-byte DMA).
 #pragma once
 #include "gemm_common.h"
 
@@ -67,46 +75,84 @@ __device__ __forceinline__ void tile_coords(int t, int ntiles, int nbm, int& bm,
   bn = r / gsz;
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
+// Raw buffer descriptor over [base, base + bytes) as four SGPR words: base, stride 0,
+// num_records = bytes, dword3 0x00020000 (32-bit data format, the gfx9 setting for untyped raw
+// buffer access).  Loads past num_records return zero; stores past it are dropped.
+typedef int sgpr4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sgpr4 buf_desc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return sgpr4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xFFFF), (int)bytes, 0x00020000};
+}
 
-// Raw buffer resource over [base, base + bytes); dword3 0x00020000 = 32-bit data format,
-// the gfx9 setting for untyped raw buffer access.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, bytes, 0x00020000);
 }
 
-// One wave-wide LDS-DMA load: lane l reads 16 bytes at voffset(l) + soffset of the buffer
-// and the wave writes them to lds_wave_base + 16*l.  Lanes whose voffset lies outside the
-// buffer write zeros.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_wave_base, uint32_t voffset,
-                                      uint32_t soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_wave_base, 16, voffset, soffset, 0, 0);
+// LDS-DMA loads (gfx950 buffer_load ... lds): lane l reads 16 (4) bytes at voffset(l) + soffset
+// of the buffer and the wave writes them to LDS base + 16*l (4*l); lanes past the buffer write
+// zeros.  They are issued as inline assembly on purpose: the compiler then does not treat them
+// as LDS writes that a later LDS read of the *other* stage might alias (it cannot tell the two
+// stages apart and would wait for every outstanding load, including the DMA just issued).  The
+// kernels wait for them explicitly (vector memory counter) before the barrier that publishes a
+// stage.  M0 carries the LDS base; nothing else in these kernels uses M0.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+__device__ __forceinline__ void dma16(sgpr4 desc, uint8_t* lds_wave_base, uint32_t voffset, uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               ::"s"(lds_addr(lds_wave_base)), "v"(voffset), "s"(desc), "s"(soffset)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(sgpr4 desc, uint8_t* lds_wave_base, uint32_t voffset, uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               ::"s"(lds_addr(lds_wave_base)), "v"(voffset), "s"(desc), "s"(soffset)
+               : "memory", "m0");
 }
 
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Waits go through __builtin_amdgcn_s_waitcnt rather than inline assembly: the compiler's
+// own wait insertion accounts for them.  It does not see waits written as inline assembly, and
+// would then assume a step's LDS-DMA still pending when that stage is read and wait for every
+// outstanding load -- including the next step's DMA, issued just before.
+// gfx9 encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+template <int VM, int LGKM = 15>
+__device__ __forceinline__ void waitcnt() {
+  static_assert(VM >= 0 && VM <= 63 && LGKM >= 0 && LGKM <= 15, "counter range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (LGKM << 8));
+}
 
-// Wait until at most N (capped at 63, the counter's range) vector memory operations of this
-// wave are outstanding.  Values without a case here fall back to waiting for all of them.
+__device__ __forceinline__ void wait_dma() { waitcnt<0>(); }
+
+// Wait until at most N vector memory operations of this wave are outstanding.
 template <int N>
 __device__ __forceinline__ void wait_vmem_leaving() {
-  if constexpr (N >= 63)
-    asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
-  else if constexpr (N == 32)
-    asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-  else if constexpr (N == 16)
-    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if constexpr (N == 8)
-    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  waitcnt<(N < 63 ? N : 63)>();
+}
+
+// Workgroup barrier without a memory fence (__syncthreads() adds one that waits for every
+// outstanding vector memory operation): this wave's LDS reads have completed, and the empty
+// "memory" assembly keeps the compiler from moving LDS or buffer accesses across it.
+__device__ __forceinline__ void workgroup_barrier() {
+  waitcnt<63, 0>();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) {
   using C = MainCfg<BM, BN, WM, WN, KIND>;
   constexpr int MR = C::MR, NR = C::NR, NW = C::NW;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds0[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds1[C::STAGE];
+  // per-K-tile scale regions of a stage, in whole DMA instructions: 1 KB (16-byte lanes) for
+  // MXFP4, 256 bytes (4-byte lanes) for blockscale
+  constexpr int SC_INSTR = KIND == KIND_FP4 ? 1024 : 256;
+  constexpr int SA_BYTES = KIND == KIND_FP4 ? (BM / 32 * 256 + 1023) / 1024 * 1024
+                                            : (EPI == EPI_BLOCK ? (BM * 4 + 255) / 256 * 256 : 0);
+  constexpr int SB_BYTES = KIND == KIND_FP4 ? (BN / 32 * 256 + 1023) / 1024 * 1024 : (EPI == EPI_BLOCK ? 256 : 0);
+  constexpr int SA_DMA = SA_BYTES / SC_INSTR, SB_DMA = SB_BYTES / SC_INSTR;
+  static_assert(EPI != EPI_BLOCK || BN / 128 <= 64, "one w_scale per lane");
+  constexpr int STAGE = C::STAGE + SA_BYTES + SB_BYTES;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
 
   const int M = p.M, N = p.N, K = p.K;
   const int nbm = (M + BM - 1) / BM;
@@ -139,10 +185,17 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   constexpr int PARTS = C::B_BLK / 1024;
   const uint32_t vb = (uint32_t)lane * 16u;
   const int b_bytes = (KIND == KIND_INT4) ? (N / 2) * K : N * K;
-  const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(p.b, b_bytes);
+  const sgpr4 rsrc_b = buf_desc(p.b, (uint32_t)b_bytes);
+
+  // scale arrays: MXFP4 [round_up(M, 32) / 32][K tiles][64 lanes] words of A and
+  // [N / 32][K tiles][64] of B; blockscale x_scale_t [K tiles][M] and w_scale [ceil(N/128)][K tiles]
+  const int sa_bytes = KIND == KIND_FP4 ? (M + 31) / 32 * nk * 256 : nk * M * 4;
+  const int sb_bytes = KIND == KIND_FP4 ? N / 32 * nk * 256 : (N + 127) / 128 * nk * 4;
+  const sgpr4 rsrc_sa = buf_desc(p.sa, (SA_DMA + SB_DMA > 0) ? (uint32_t)sa_bytes : 0u);
+  const sgpr4 rsrc_sb = buf_desc(p.sb, (SA_DMA + SB_DMA > 0) ? (uint32_t)sb_bytes : 0u);
 
   auto issue = [&](uint8_t* s, int m0, int n0, int kt) {
-    const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(p.a + (size_t)kt * KT, M * K - kt * KT);
+    const sgpr4 rsrc_a = buf_desc(p.a + (size_t)kt * KT, (uint32_t)(M * K - kt * KT));
     const uint32_t mo = (uint32_t)m0 * (uint32_t)K;
 #pragma unroll
     for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, va0[j] + mo, 0);
@@ -154,37 +207,44 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
                           (uint32_t)kt * C::B_BLK;
       dma16(rsrc_b, s + C::A_BYTES + q * 1024, vb, __builtin_amdgcn_readfirstlane(so));
     }
+    // this K tile's scales: scale instruction q = wave, wave + NW, ... (q < SA_DMA: A region,
+    // then B region); indices past the arrays are clamped
+    if constexpr (SA_DMA + SB_DMA > 0) {
+      uint8_t* sc = s + C::STAGE;
+#pragma unroll
+      for (int j = 0; j < (SA_DMA + SB_DMA + NW - 1) / NW; ++j) {
+        const int q = wave + j * NW;
+        if (q < SA_DMA) {
+          if constexpr (KIND == KIND_FP4) {
+            const uint32_t b = (uint32_t)q * 1024u + (uint32_t)lane * 16u;  // byte in the region
+            const int r1 = min(m0 / 32 + (int)(b >> 8), (M + 31) / 32 - 1);
+            dma16(rsrc_sa, sc + q * 1024, ((uint32_t)r1 * (uint32_t)nk * 64u) * 4u + (b & 255u), (uint32_t)kt * 256u);
+          } else {
+            // x_scale_t[kt][m0 + 64q + lane]; rows past M read the next values or zeros
+            dma4(rsrc_sa, sc + q * 256, ((uint32_t)kt * (uint32_t)M + (uint32_t)(m0 + q * 64 + lane)) * 4u, 0);
+          }
+        } else if (q < SA_DMA + SB_DMA) {
+          const int qb = q - SA_DMA;
+          if constexpr (KIND == KIND_FP4) {
+            const uint32_t b = (uint32_t)qb * 1024u + (uint32_t)lane * 16u;
+            const int c1 = min(n0 / 32 + (int)(b >> 8), N / 32 - 1);
+            dma16(rsrc_sb, sc + SA_BYTES + qb * 1024, ((uint32_t)c1 * (uint32_t)nk * 64u) * 4u + (b & 255u),
+                  (uint32_t)kt * 256u);
+          } else {
+            // lane l: w_scale[n0/128 + l][kt]
+            const int nb = min(n0 / 128 + lane, (N - 1) / 128);
+            dma4(rsrc_sb, sc + SA_BYTES, ((uint32_t)nb * (uint32_t)nk + (uint32_t)kt) * 4u, 0);
+          }
+        }
+      }
+    }
   };
 
   typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
   AccT acc[MR][NR];
-  // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be null)
-  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_is_16bit(KIND);
-
-  // blockscale: the A scale of this lane's row in each MFMA row block and the B scale of
-  // each 16-column block, for one K tile.  They are loaded one step ahead (into sa_n/sb_n,
-  // together with that step's DMA), so the wait at the top of a step covers them too.
-  float sa_t[MR], sb_t[NR], sa_n[MR], sb_n[NR];
-  auto load_scales = [&](int m0, int n0, int kt) {
-    if constexpr (EPI == EPI_BLOCK) {
-#pragma unroll
-      for (int mi = 0; mi < MR; ++mi)
-        sa_n[mi] = p.sa[(size_t)kt * M + min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
-#pragma unroll
-      for (int ni = 0; ni < NR; ++ni) {
-        const int col = min(n0 + wn * C::TN + ni * 16, N - 1);
-        sb_n[ni] = p.sb[(size_t)(col >> 7) * nk + kt];
-      }
-    }
-  };
-  auto take_scales = [&]() {
-    if constexpr (EPI == EPI_BLOCK) {
-#pragma unroll
-      for (int mi = 0; mi < MR; ++mi) sa_t[mi] = sa_n[mi];
-#pragma unroll
-      for (int ni = 0; ni < NR; ++ni) sb_t[ni] = sb_n[ni];
-    }
-  };
+  // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be
+  // null, nor to MXFP4, whose block scales are applied by the MFMA)
+  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_unscaled(KIND);
 
   // A fragment of MFMA row mi: lane holds 16-byte chunks lq and lq+4 of its row
   auto load_a = [&](const uint8_t* sA, int mi, i32x4& lo, i32x4& hi) {
@@ -199,6 +259,24 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   // each accumulator tile holds C transposed (see the epilogue).
   auto compute = [&](const uint8_t* sA) {
     const uint8_t* sB = sA + C::A_BYTES;
+    const uint8_t* sS = sA + C::STAGE;  // this K tile's scales
+    // blockscale: this lane's row scale per row block, the column-block scale per tile column;
+    // MXFP4: this lane's scale word per 32-row / 32-column group
+    constexpr int MQ = (MR + 1) / 2, NQ = (NR + 1) / 2;
+    float sa_t[MR], sb_t[NR];
+    uint32_t fa_t[MQ], fb_t[NQ];
+    if constexpr (EPI == EPI_BLOCK) {
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) sa_t[mi] = *(const float*)(sS + (wm * C::TM + mi * 16 + l16) * 4);
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni) sb_t[ni] = *(const float*)(sS + SA_BYTES + ((wn * C::TN + ni * 16) / 128) * 4);
+    }
+    if constexpr (KIND == KIND_FP4) {
+#pragma unroll
+      for (int q = 0; q < MQ; ++q) fa_t[q] = *(const uint32_t*)(sS + (wm * C::TM / 32 + q) * 256 + lane * 4);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) fb_t[q] = *(const uint32_t*)(sS + SA_BYTES + (wn * C::TN / 32 + q) * 256 + lane * 4);
+    }
     i32x4 alo, ahi;
     load_a(sA, 0, alo, ahi);
     if constexpr (KIND == KIND_FP8) {
@@ -254,11 +332,29 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       for (int mi = 0; mi < MR; ++mi) {
         const i32x4 lo = alo, hi = ahi;
         if (mi + 1 < MR) load_a(sA, mi + 1, alo, ahi);
+#if FLY_SCHED
+        __builtin_amdgcn_sched_barrier(0);
+#endif
+        // the two 64-byte halves of the K tile go out as two passes over the row's tiles, so
+        // the two MFMAs that accumulate into one tile are NR instructions apart
 #pragma unroll
-        for (int ni = 0; ni < NR; ++ni) {
-          acc[mi][ni] = mfma_k64<KIND>(bl[ni], lo, acc[mi][ni]);
-          acc[mi][ni] = mfma_k64<KIND>(bh[ni], hi, acc[mi][ni]);
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int ni = 0; ni < NR; ++ni) {
+            const i32x4& bq = h ? bh[ni] : bl[ni];
+            const i32x4& aq = h ? hi : lo;
+            if constexpr (KIND == KIND_FP4) {
+              // chunks lq / lq+4 are the 32-element scale blocks of MFMA halves 0 / 1
+              const uint32_t sbw = fb_t[ni >> 1] >> (8 * (ni & 1)), saw = fa_t[mi >> 1] >> (8 * (mi & 1));
+              acc[mi][ni] = h ? mfma_fp4<1>(bq, aq, acc[mi][ni], sbw, saw) : mfma_fp4<0>(bq, aq, acc[mi][ni], sbw, saw);
+            } else {
+              acc[mi][ni] = mfma_k64<KIND>(bq, aq, acc[mi][ni]);
+            }
+          }
         }
+#if FLY_SCHED
+        __builtin_amdgcn_sched_barrier(0);
+#endif
       }
     }
   };
@@ -313,7 +409,6 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   tile_coords(t, ntiles, nbm, bm, bn);
   int m0 = bm * BM, n0 = bn * BN;
   issue(lds0, m0, n0, 0);
-  load_scales(m0, n0, 0);
   int step = 0;
   for (; t < ntiles; t += G) {
     const int tn = t + G;
@@ -335,17 +430,17 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         wait_vmem_leaving<MR * NR>();
       else
         wait_dma();
-      __syncthreads();  // this step's tile has landed; every wave is done with the other stage
+      // this step's tile has landed; every wave is done with the other stage.  A bare
+      // s_barrier: __syncthreads() would add a fence that waits for every outstanding vector
+      // memory operation, i.e. also for the previous tile's epilogue stores kept in flight above.
+      // The waits this barrier needs are this wave's DMAs (just above) and its LDS reads.
+      workgroup_barrier();
       uint8_t* cur = (step & 1) ? lds1 : lds0;
       uint8_t* nxt = (step & 1) ? lds0 : lds1;
-      take_scales();
-      if (kt + 1 < nk) {
+      if (kt + 1 < nk)
         issue(nxt, m0, n0, kt + 1);
-        load_scales(m0, n0, kt + 1);
-      } else if (tn < ntiles) {
+      else if (tn < ntiles)
         issue(nxt, nm0, nn0, 0);
-        load_scales(nm0, nn0, 0);
-      }
       compute(cur);
     }
     epilogue(m0, n0);

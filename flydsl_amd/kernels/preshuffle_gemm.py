@@ -24,8 +24,8 @@ Differences from the reference, all on purpose:
 * Any ``N % 16 == 0`` is computed in full (the reference's grid silently skips a tail
   when ``N % tile_n != 0``); K must be a multiple of 128 (64 for bf16/fp16).
 * GPU errors raise ``RuntimeError`` (the reference prints them).
-* ``in_dtype`` "fp4" is accepted by the checks but not built for MI355X yet: the launcher
-  raises ``NotImplementedError``.
+* ``in_dtype="fp4"`` (MXFP4, what ``compile_preshuffle_gemm_w4`` builds) takes packed e2m1
+  bytes and shuffled E8M0 scale bytes (``flydsl_amd.fp4``); N % 32 == 0 and K % 256 == 0.
 """
 from __future__ import annotations
 
@@ -56,6 +56,8 @@ class PreshuffleGemm:
         self.hints = hints
 
     def __call__(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):
+        if self.in_dtype == "fp4":
+            return self._call_fp4(arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream)
         if self.in_dtype not in _lib.FLYGEMM_IN:
             raise NotImplementedError(f"in_dtype={self.in_dtype!r} has no MI355X kernel in this build")
         M, N, K = int(M), int(N), self.K
@@ -85,6 +87,32 @@ class PreshuffleGemm:
         rc = lib.flygemm_preshuffle(c, a, b, sa, sb, M, N, K, _lib.FLYGEMM_IN[self.in_dtype],
                                     _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
         _lib.check(rc, "flygemm_preshuffle")
+
+
+def _fp4_call(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):
+    """MXFP4: packed e2m1 A [M, K/2] and preshuffled B [N, K/2] bytes, shuffled E8M0 scales
+    [round_up(M, 32), K/32] and [N, K/32] bytes (``flydsl_amd.fp4``; reference harness
+    ``tests/kernels/test_preshuffle_gemm.py:315-358``)."""
+    M, N, K = int(M), int(N), self.K
+    h_stream = stream_handle(stream)
+    if M < 0 or N <= 0:
+        raise ValueError(f"invalid M={M}, N={N}")
+    if N % 32:
+        raise ValueError(f"N={N} must be a multiple of 32 for MXFP4 (scale groups)")
+    if K % 256:
+        raise ValueError(f"K={K} must be a multiple of 256 for MXFP4")
+    if K % self.tile_k:
+        raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
+    c = device_ptr(arg_c, "arg_c", M * N, dtypes=(_OUT_TORCH[self.out_dtype],))
+    a = device_ptr(arg_a, "arg_a", M * K // 2, elem_bytes=1)
+    b = device_ptr(arg_b, "arg_b", N * K // 2, elem_bytes=1)
+    sa = device_ptr(arg_scale_a, "arg_scale_a", (M + 31) // 32 * 32 * (K // 32), elem_bytes=1)
+    sb = device_ptr(arg_scale_b, "arg_scale_b", N * (K // 32), elem_bytes=1)
+    rc = _lib.load().flygemm_mxfp4(c, a, b, sa, sb, M, N, K, _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
+    _lib.check(rc, "flygemm_mxfp4")
+
+
+PreshuffleGemm._call_fp4 = _fp4_call
 
 
 def compile_preshuffle_gemm_a8(
@@ -149,8 +177,9 @@ def compile_preshuffle_gemm_w4(*, M: int = 0, N: int = 0, K: int, tile_m: int, t
                                a_dtype: str = "fp4", b_dtype: str = "fp4", out_dtype: str = "bf16",
                                lds_stage: int = 2, use_cshuffle_epilog: bool = False,
                                waves_per_eu: Optional[int] = None, use_async_copy: bool = False):
-    """MXFP4 entry (reference ``kernels/preshuffle_gemm.py:1306-1337``): same checks, no MI355X
-    kernel in this build yet."""
+    """MXFP4 entry (reference ``kernels/preshuffle_gemm.py:1306-1337``): fp4 A and B with 1x32
+    E8M0 block scales, applied inside the gfx950 scaled MFMA.  fp8 A is rejected as the
+    reference rejects it."""
     if a_dtype == "fp8":
         raise NotImplementedError("fp8-A not yet supported with MXFP4 kernel (op_sel_a overflow)")
     return compile_preshuffle_gemm_a8(
@@ -163,8 +192,9 @@ def compile_preshuffle_gemm_w4(*, M: int = 0, N: int = 0, K: int, tile_m: int, t
 def accumulators(acc, a, b, M, N, K, in_dtype, variant=-1, stream=None):
     """Raw accumulators of ``sum_k a[m,k] b[n,k]`` (int32 for int8/int4, fp32 for fp8, bf16
     and fp16), no scaling: the value the kernels hold before the epilogue."""
-    if in_dtype not in _lib.FLYGEMM_IN:
-        raise ValueError(f"in_dtype must be one of {tuple(_lib.FLYGEMM_IN)}, got {in_dtype!r}")
+    if in_dtype not in _lib.FLYGEMM_IN or in_dtype == "fp4":
+        raise ValueError(f"in_dtype must be one of fp8, int8, int4, bf16, fp16 (MXFP4 accumulators: the fp4 "
+                         f"launcher with out_dtype fp32 through flygemm_mxfp4), got {in_dtype!r}")
     b_elems = N * K // 2 if in_dtype == "int4" else N * K
     want = torch.int32 if in_dtype in ("int8", "int4") else torch.float32
     eb = 2 if in_dtype in ("bf16", "fp16") else 1

@@ -11,13 +11,13 @@ from dataclasses import dataclass
 
 import torch
 
-from . import quant
+from . import fp4, quant
 
 
 @dataclass(frozen=True)
 class Workload:
     name: str
-    kind: str          # "fp8" | "int8" | "int4" | "fp8_block" | "bf16" | "fp16"
+    kind: str          # "fp8" | "int8" | "int4" | "fp8_block" | "bf16" | "fp16" | "mxfp4"
     M: int
     N: int
     K: int
@@ -36,6 +36,8 @@ class Workload:
         M, N, K = self.M, self.N, self.K
         if self.kind in ("bf16", "fp16"):
             return 2 * (M * K + N * K + M * N)   # no scales
+        if self.kind == "mxfp4":   # reference test_preshuffle_gemm.py:371-374
+            return M * K // 2 + N * K // 2 + 2 * M * N + (M + N) * (K // 32)
         b = N * K // 2 if self.kind == "int4" else N * K
         base = M * K + b + 2 * M * N
         if self.kind == "fp8_block":
@@ -51,6 +53,7 @@ WORKLOADS = {
     "C5": Workload("C5", "int4", 256, 14336, 4096, 4, b_std=0.02, note="W4A8"),
     "T": Workload("T", "fp8", 8192, 8192, 8192, 5, note="FP8 8192^3, MFMA-bound target"),
     "T16": Workload("T16", "bf16", 8192, 8192, 8192, 6, note="BF16 8192^3 (in_dtype='bf16', unscaled)"),
+    "F4": Workload("F4", "mxfp4", 8192, 8192, 8192, 7, note="MXFP4 8192^3 (1x32 E8M0 block scales)"),
 }
 
 
@@ -87,6 +90,18 @@ def make_operands(w: Workload) -> dict:
         b, sb = quant.blockscale_quant(b32p, 128, 128)
         b = b[: w.N].contiguous()
         out["sa_t"] = sa.t().contiguous()
+    elif w.kind == "mxfp4":
+        # as the reference harness prepares them (test_preshuffle_gemm.py:304-336): A quantized
+        # on rows padded to a multiple of 32, both scale arrays shuffled for the MFMA lanes
+        m32 = (w.M + 31) // 32 * 32
+        a_pad = torch.zeros(m32, w.K)
+        a_pad[: w.M] = a32
+        a_q, sa_raw, _ = fp4.per_1x32_f4_quant(a_pad)
+        b_q, sb_raw, _ = fp4.per_1x32_f4_quant(b32)
+        del a32, b32, a_pad
+        out.update(a=a_q[: w.M].contiguous(), b=b_q, b_dev=fp4.shuffle_weight_w4(b_q),
+                   sa=fp4.shuffle_scale_w4(sa_raw), sb=fp4.shuffle_scale_w4(sb_raw), sa_raw=sa_raw, sb_raw=sb_raw)
+        return out
     elif w.kind in ("bf16", "fp16"):
         dt = torch.bfloat16 if w.kind == "bf16" else torch.float16
         a, b = a32.to(dt), b32.to(dt)

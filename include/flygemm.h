@@ -37,9 +37,10 @@ enum {
   FLYGEMM_IN_INT8 = 1, /* int8 A and B */
   FLYGEMM_IN_INT4 = 2, /* int8 A, packed signed int4 B */
   FLYGEMM_IN_BF16 = 3, /* bf16 A and B, no scaling (scale pointers ignored) */
-  FLYGEMM_IN_FP16 = 4  /* fp16 A and B, no scaling (scale pointers ignored) */
+  FLYGEMM_IN_FP16 = 4, /* fp16 A and B, no scaling (scale pointers ignored) */
+  FLYGEMM_IN_FP4 = 5   /* MXFP4: flygemm_mxfp4 only (and flygemm_select_variant) */
 };
-enum { FLYGEMM_OUT_BF16 = 0, FLYGEMM_OUT_FP16 = 1 };
+enum { FLYGEMM_OUT_BF16 = 0, FLYGEMM_OUT_FP16 = 1, FLYGEMM_OUT_F32 = 2 /* flygemm_mxfp4 only */ };
 
 /* C[M][N] = out_dtype((acc[m][n] * scale_a[m]) * scale_b[n]),
  * acc = sum_k A[m][k] * B[n][k] in fp32 (fp8, bf16, fp16) or int32 (int8/int4);
@@ -66,6 +67,18 @@ int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_sca
  * (kernels/preshuffle_gemm.py:643-797) so integer paths can be checked bit-exactly. */
 int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int32_t N, int32_t K,
                          int32_t in_dtype, int32_t variant, void* stream);
+
+/* MXFP4 GEMM: C[m][n] = out_dtype(sum_k a[m][k] * sa[m][k/32] * b[n][k] * sb[n][k/32]),
+ * fp32 accumulation; a, b OCP e2m1 (two per byte, element 2j in the low nibble), sa, sb E8M0.
+ * a: row-major [M][K/2] bytes.  b: [N][K/2] bytes after the reference's
+ * shuffle_weight_w4(b, 16, False, False) (tests/kernels/utils/fp4_utils.py:578-621), which
+ * is the 1-byte preshuffle rule on rows of K/2 bytes.  scale_a / scale_b: E8M0 bytes
+ * [round_up(M, 32)][K/32] / [N][K/32] after shuffle_scale_w4(s, 1, False) (:624-653).
+ * K % 256 == 0, N % 32 == 0.  out_dtype bf16, fp16 or fp32.  Replaces the launcher of
+ * compile_preshuffle_gemm_w4 (reference kernels/preshuffle_gemm.py:1306-1337, MFMA use
+ * :692-732; harness tests/kernels/test_preshuffle_gemm.py:261-379). */
+int flygemm_mxfp4(void* c, const void* a, const void* b, const void* scale_a, const void* scale_b, int32_t M,
+                  int32_t N, int32_t K, int32_t out_dtype, int32_t variant, void* stream);
 
 /* Per-row (per-token) quantization of activations, the producer of A and scale_a:
  *   scale[m] = max_n |in[m][n]| / qmax (qmax 127 int8, 448 fp8), 1 where that is 0;

@@ -43,6 +43,8 @@ def test_variant_table():
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
+    # MXFP4 decode keeps to at most 4 column blocks per workgroup
+    assert names[lib.flygemm_select_variant(16, 28672, 8192, 5, 0)] == "decode_m1_nb4_w8_u3"
     for m in (1, 17, 64, 65, 100, 1000, 5000):
         for n in (16, 128, 2048, 30000):
             for bs in (0, 1):
@@ -84,6 +86,14 @@ def test_abi_rejects_bad_arguments_before_launch():
     rc = lib.flygemm_preshuffle(p, p, p, None, None, 16, 128, 96, 3, 0, -1, None)
     assert rc != 0 and b"multiple of 64" in lib.flygemm_last_error()
     assert lib.flygemm_preshuffle(p, p, p, None, None, 0, 128, 192, 4, 0, -1, None) == 0
+    # MXFP4
+    rc = lib.flygemm_mxfp4(p, p, p, p, p, 16, 128, 384, 0, -1, None)
+    assert rc != 0 and b"multiple of 256" in lib.flygemm_last_error()
+    rc = lib.flygemm_mxfp4(p, p, p, p, p, 16, 48, 512, 0, -1, None)
+    assert rc != 0 and b"multiple of 32" in lib.flygemm_last_error()
+    rc = lib.flygemm_mxfp4(p, p, p, None, p, 16, 128, 512, 0, -1, None)
+    assert rc != 0 and b"null scale" in lib.flygemm_last_error()
+    assert lib.flygemm_mxfp4(p, p, p, p, p, 0, 128, 512, 2, -1, None) == 0
 
 
 @pytest.mark.parametrize("kw, exc", [
@@ -105,9 +115,17 @@ def test_compile_validation_matches_reference(kw, exc):
 def test_w4_entry_and_unbuilt_dtypes():
     with pytest.raises(NotImplementedError):
         compile_preshuffle_gemm_w4(K=256, tile_m=64, tile_n=128, tile_k=128, a_dtype="fp8")
-    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp4")
-    with pytest.raises(NotImplementedError):
-        fn(None, None, None, None, None, 16, 128, None)
+    fn = compile_preshuffle_gemm_w4(K=256, tile_m=64, tile_n=128, tile_k=128)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        fn(torch.empty(16 * 128, dtype=torch.bfloat16), torch.empty(16 * 128, dtype=torch.uint8),
+           torch.empty(128 * 128, dtype=torch.uint8), torch.empty(32 * 8, dtype=torch.uint8),
+           torch.empty(128 * 8, dtype=torch.uint8), 16, 128, None)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        fn(None, None, None, None, None, 16, 112, None)
+    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp16")
+    with pytest.raises(ValueError, match="GPU tensor"):
+        fn(torch.empty(16 * 128, dtype=torch.float16), torch.empty(16 * 256, dtype=torch.float16),
+           torch.empty(128 * 256, dtype=torch.float16), None, None, 16, 128, None)
     # bf16 is built: host tensors are rejected by the argument checks, before any launch
     fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="bf16")
     x = torch.empty(16 * 256, dtype=torch.bfloat16)

@@ -438,3 +438,135 @@ def test_bar_rejects_planted_mistakes():
     good = og.run_torch_blockscale(qx, qw, sx, sw, "f64")
     wrong = og.run_torch_blockscale(qx, qw, sx.T.reshape(sx.shape), sw, "f64")
     assert not og.within_bar(wrong, good)[0]
+
+
+# ---------------------------------------------------------------- MXFP4
+from oracle import mxfp4 as om  # noqa: E402
+
+_OCP_E2M1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]   # OCP MX spec v1.0, FP4 E2M1 magnitudes
+
+
+def test_e2m1_decode_matches_spec_table():
+    codes = np.arange(16, dtype=np.uint8)
+    want = np.array(_OCP_E2M1 + [-v for v in _OCP_E2M1], dtype=np.float32)
+    got = om.e2m1_decode(codes)
+    assert np.array_equal(got, want) and np.signbit(got[8])
+    from flydsl_amd import fp4
+    packed = torch.tensor([0x10, 0x32, 0x54, 0x76, 0x98, 0xBA, 0xDC, 0xFE], dtype=torch.uint8)
+    assert np.array_equal(fp4.mxfp4_to_f32(packed).numpy(), want)
+    assert np.array_equal(om.unpack(packed.numpy()).reshape(-1), np.arange(16))
+
+
+def _nearest_e2m1_bruteforce(y):
+    """Exhaustive nearest grid value, ties to the even code, saturating at 6."""
+    out = []
+    for v in y.astype(np.float64):
+        a = min(abs(v), 6.0)
+        d = [abs(a - g) for g in _OCP_E2M1]
+        best = min(d)
+        cands = [i for i, x in enumerate(d) if x == best]
+        code = [c for c in cands if c % 2 == 0][0] if len(cands) > 1 else cands[0]
+        out.append(code | (8 if np.signbit(v) else 0))
+    return np.array(out, dtype=np.uint8)
+
+
+def test_e2m1_encode_nearest_even_and_saturating():
+    rng = np.random.default_rng(21)
+    grid = np.array(_OCP_E2M1)
+    mids = (grid[1:] + grid[:-1]) / 2
+    y = np.concatenate([rng.uniform(-8, 8, 3000), mids, -mids, grid, -grid, [6.5, 7.0, 100.0, -9.0, 0.1, -0.2]]).astype(np.float32)
+    assert np.array_equal(om.e2m1_encode(y), _nearest_e2m1_bruteforce(y))
+    assert np.array_equal(om.e2m1_encode(om.e2m1_decode(np.arange(16))), np.arange(16, dtype=np.uint8))
+    from flydsl_amd import fp4
+    assert np.array_equal(fp4.e2m1_encode(torch.from_numpy(y)).numpy(), om.e2m1_encode(y))
+
+
+def test_e8m0_encode_closed_form_and_edges():
+    import math
+    rng = np.random.default_rng(22)
+    x = np.concatenate([np.exp2(rng.uniform(-120, 120, 4000)), [1.0, 1.5, 1.4999999, 2.9999, 3.0, 0.75]]).astype(np.float32)
+    want = []
+    for v in x.astype(np.float64):
+        m, e = math.frexp(v)          # v = m * 2**e, m in [0.5, 1)
+        sig, ex = 2 * m, e - 1        # v = sig * 2**ex, sig in [1, 2)
+        want.append(ex + 127 + (1 if sig >= 1.5 else 0))
+    assert np.array_equal(om.e8m0_encode(x).astype(np.int64), np.array(want))
+    edge = np.array([0x00000000, 0x00400000, 0x00400001, 0x00200000, 0x7F800000, 0x7FC00000, 0x7F400000],
+                    dtype=np.uint32).view(np.float32)
+    # 0 -> 0; subnormal with only bit 22 -> 0; bit 22 + lower bit -> 1; bit 21 only -> 0;
+    # inf/NaN -> 0xFF; largest finite binade with significand >= 1.5 -> 0xFF
+    assert om.e8m0_encode(edge).tolist() == [0, 0, 1, 0, 0xFF, 0xFF, 0xFF]
+    from flydsl_amd import fp4
+    assert np.array_equal(fp4.e8m0_from_f32(torch.from_numpy(np.concatenate([x, edge]))).numpy(),
+                          om.e8m0_encode(np.concatenate([x, edge])))
+    d = om.e8m0_decode(np.array([0, 1, 127, 128, 254, 255], dtype=np.uint8))
+    assert d[0] == 2.0 ** -127 and d[1] == 2.0 ** -126 and d[2] == 1.0 and d[3] == 2.0 and d[4] == 2.0 ** 127
+    assert np.isnan(d[5])
+    assert np.array_equal(fp4.e8m0_to_f32(torch.tensor([0, 1, 127, 128, 254], dtype=torch.uint8)).numpy(), d[:5])
+
+
+def test_quant_1x32_error_bound_and_product_equality():
+    from flydsl_amd import fp4
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(40, 512, generator=g) * 3
+    x[2] = 0.0
+    x[3, :32] = 1e-3
+    q, s = om.quant_1x32(x.numpy())
+    deq = om.dequant(q, s)
+    sc = np.repeat(om.e8m0_decode(s).astype(np.float64), 32, axis=1)
+    y = np.abs(x.numpy() / sc)
+    step = np.where(y < 2, 0.5, np.where(y < 4, 1.0, 2.0))
+    sat = y > 6
+    err = np.abs(deq - x.numpy())
+    assert np.all(err[~sat] <= step[~sat] / 2 * sc[~sat] * (1 + 1e-6))
+    assert np.all(deq[2] == 0)
+    # the block amax lands in [4/1.5, 6] after scaling (the scale rounds amax/4 to a power of two)
+    blk = y.reshape(-1, 32).max(axis=1)
+    nz = blk > 0
+    assert np.all(blk[nz] >= 4 / 1.5 * (1 - 1e-6)) and np.all(blk[nz] <= 6 * 1.5)
+    qt, st, _ = fp4.per_1x32_f4_quant(x)
+    assert np.array_equal(qt.numpy(), q) and np.array_equal(st.numpy(), s)
+
+
+def test_mxfp4_shuffles_elementwise():
+    from flydsl_amd import fp4
+    rng = np.random.default_rng(24)
+    N, K = 64, 512
+    b = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    got = om.shuffle_weight_w4(b)
+    kb = K // 2
+    want = np.empty(N * kb, dtype=np.uint8)
+    for n in range(N):
+        for k in range(kb):   # reference view (N0, NLane, K0, KLane, KPack) -> (N0, K0, KLane, NLane, KPack)
+            n0, nl, k0, kl, kp = n // 16, n % 16, k // 64, (k // 16) % 4, k % 16
+            want[(((n0 * (kb // 64) + k0) * 4 + kl) * 16 + nl) * 16 + kp] = b[n, k]
+    assert np.array_equal(got, want)
+    assert np.array_equal(fp4.shuffle_weight_w4(torch.from_numpy(b)).numpy().reshape(-1), got)
+    R, ks = 64, K // 32 * 2     # K = 1024 -> 32 scale blocks per row
+    s = rng.integers(0, 256, (R, ks), dtype=np.uint8)
+    gs = om.shuffle_scale_w4(s)
+    ws = np.empty(R * ks, dtype=np.uint8)
+    for r in range(R):
+        for k in range(ks):   # (r1, rp, rl) x (k1, kp, kl) -> [r1][k1][kl][rl][kp][rp]
+            r1, rp, rl = r // 32, (r // 16) % 2, r % 16
+            k1, kp, kl = k // 8, (k // 4) % 2, k % 4
+            ws[((((r1 * (ks // 8) + k1) * 4 + kl) * 16 + rl) * 2 + kp) * 2 + rp] = s[r, k]
+    assert np.array_equal(gs, ws)
+    assert np.array_equal(fp4.shuffle_scale_w4(torch.from_numpy(s)).numpy().reshape(-1), gs)
+
+
+def test_run_torch_w4_bruteforce():
+    rng = np.random.default_rng(25)
+    a = rng.integers(0, 256, (3, 32), dtype=np.uint8)     # K = 64
+    b = rng.integers(0, 256, (5, 32), dtype=np.uint8)
+    sa = rng.integers(120, 135, (32, 2), dtype=np.uint8)  # padded rows like the reference
+    sb = rng.integers(120, 135, (5, 2), dtype=np.uint8)
+    ref = om.run_torch_w4(a, b, sa, sb, "f64")
+    dec = lambda p: [v for byte in p for v in (_OCP_E2M1 + [-x for x in _OCP_E2M1])[byte & 15:(byte & 15) + 1] +
+                     (_OCP_E2M1 + [-x for x in _OCP_E2M1])[byte >> 4:(byte >> 4) + 1]]
+    for m in range(3):
+        for n in range(5):
+            av, bv = dec(a[m]), dec(b[n])
+            tot = sum(av[k] * 2.0 ** (int(sa[m, k // 32]) - 127) * bv[k] * 2.0 ** (int(sb[n, k // 32]) - 127)
+                      for k in range(64))
+            assert abs(ref[m, n] - tot) <= 1e-9 * max(1.0, abs(tot))
