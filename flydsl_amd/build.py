@@ -10,7 +10,7 @@ import subprocess
 import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-SRC = os.path.join(PKG_DIR, "csrc", "flygemm.hip")
+SOURCES = [os.path.join(PKG_DIR, "csrc", f) for f in ("flygemm.hip", "moe.hip")]
 OUT = os.path.join(PKG_DIR, "_flygemm.so")
 ARCH = "gfx950"
 
@@ -37,14 +37,32 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> str:
+    """Compile each source to an object in parallel, then link the shared library."""
+    objs, procs = [], []
+    for src in SOURCES:
+        obj = os.path.splitext(OUT)[0] + "_" + os.path.splitext(os.path.basename(src))[0] + ".o"
+        cmd = [hipcc(), *[f for f in HIPCC_FLAGS if f != "-shared"], "-c", "-o", obj, src]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        objs.append(obj)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    errors = []
+    for src, proc in procs:
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            errors.append(f"hipcc failed on {os.path.basename(src)} ({proc.returncode}):\n{err[-8000:]}")
+    if errors:
+        raise RuntimeError("\n".join(errors))
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, SRC]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
+        raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-8000:]}")
     os.replace(tmp, OUT)
+    for obj in objs:
+        os.remove(obj)
     return OUT
 
 

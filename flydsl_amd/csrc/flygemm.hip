@@ -14,6 +14,7 @@
 #include <utility>
 
 #include "../../include/flygemm.h"
+#include "abi_error.h"
 #include "gemm_decode.h"
 #include "gemm_main.h"
 #include "quant_rows.h"
@@ -21,16 +22,19 @@
 using namespace flygemm;
 
 namespace {
-
 thread_local char g_err[512] = "";
+}  // namespace
 
-int fail(int code, const char* fmt, ...) {
+// the one error slot of the library, shared by every translation unit (abi_error.h)
+int flygemm::fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
   return code;
 }
+
+namespace {
 
 typedef void (*KernelFn)(GemmArgs);
 

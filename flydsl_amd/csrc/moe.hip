@@ -1,0 +1,134 @@
+// C-ABI of the MoE 2-stage GEMM (declarations: include/flygemm.h).  Host-side validation,
+// tile dispatch and launch; the kernels are in moe.h.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/flygemm.h"
+#include "abi_error.h"
+#include "moe.h"
+
+using namespace flygemm;
+
+namespace {
+
+typedef void (*MoeFn)(MoeArgs);
+
+template <int STAGE, int KIND, int OUT>
+MoeFn moe_tile(int tm, int tn) {
+#define T(M_, N_) \
+  if (tm == M_ && tn == N_) return moe_gemm_kernel<STAGE, KIND, M_, N_, OUT>;
+  T(16, 64) T(16, 128) T(16, 256) T(32, 64) T(32, 128) T(32, 256) T(64, 64) T(64, 128) T(64, 256)
+#undef T
+  return nullptr;
+}
+
+template <int STAGE, int OUT>
+MoeFn moe_kind(int kind, int tm, int tn) {
+  switch (kind) {
+    case KIND_FP8: return moe_tile<STAGE, KIND_FP8, OUT>(tm, tn);
+    case KIND_INT8: return moe_tile<STAGE, KIND_INT8, OUT>(tm, tn);
+    case KIND_BF16: return moe_tile<STAGE, KIND_BF16, OUT>(tm, tn);
+    case KIND_F16: return moe_tile<STAGE, KIND_F16, OUT>(tm, tn);
+    default: return nullptr;
+  }
+}
+
+// Column tile when the caller leaves it open (tile_n <= 0): the widest of 256/128/64 that
+// divides N and still gives every sorted block at least two column tiles.
+int pick_tile_n(int N) {
+  for (int tn : {256, 128})
+    if (N % tn == 0 && N / tn >= 2) return tn;
+  return 64;
+}
+
+int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
+               const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
+               const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
+               int tile_n, int in_dtype, int out_dtype, int doweight, hipStream_t stream) {
+  const char* what = stage == 1 ? "moe_gemm1" : "moe_gemm2";
+  if (tokens < 0 || N <= 0 || K <= 0 || blocks < 0 || experts <= 0)
+    return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d N=%d K=%d blocks=%d experts=%d", what, tokens, N, K,
+                blocks, experts);
+  if (topk < 1 || topk > 255) return fail(hipErrorInvalidValue, "%s: topk=%d must be in [1, 255]", what, topk);
+  if (tokens >= (1 << 24)) return fail(hipErrorInvalidValue, "%s: tokens=%d must be below 2^24", what, tokens);
+  if (tile_m != 16 && tile_m != 32 && tile_m != 64)
+    return fail(hipErrorInvalidValue, "%s: tile_m=%d must be 16, 32 or 64", what, tile_m);
+  if (tile_n <= 0) tile_n = pick_tile_n(N);
+  if (tile_n != 64 && tile_n != 128 && tile_n != 256)
+    return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
+  if (N % tile_n != 0) return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
+  int kind;
+  switch (in_dtype) {
+    case FLYGEMM_IN_FP8: kind = KIND_FP8; break;
+    case FLYGEMM_IN_INT8: kind = KIND_INT8; break;
+    case FLYGEMM_IN_BF16: kind = KIND_BF16; break;
+    case FLYGEMM_IN_FP16: kind = KIND_F16; break;
+    default: return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
+  }
+  const bool is16 = kind_is_16bit(kind);
+  const long kb = is16 ? 2L * K : (long)K;
+  if (kb % 128 != 0)
+    return fail(hipErrorInvalidValue, "%s: K=%d must be a multiple of %d (128-byte K tile)", what, K, is16 ? 64 : 128);
+  const long a_rows = stage == 1 ? tokens : (long)tokens * topk;
+  const long w_rows = stage == 1 ? 2L * N : (long)N;
+  if (a_rows * kb >= (1L << 31) || w_rows * kb >= (1L << 31))
+    return fail(hipErrorInvalidValue, "%s: activation or per-expert weight above 2^31 bytes", what);
+  int mout;
+  if (out_dtype == FLYGEMM_OUT_FP16) mout = MOE_OUT_F16;
+  else if (out_dtype == FLYGEMM_OUT_BF16) mout = MOE_OUT_BF16;
+  else if (out_dtype == FLYGEMM_OUT_F32 && stage == 2) mout = MOE_OUT_F32;
+  else return fail(hipErrorInvalidValue, "%s: out_dtype %d not supported", what, out_dtype);
+  if (tokens == 0 || blocks == 0) return 0;
+  if (!out || !a || !w || !sorted_ids || !expert_ids || !num_valid)
+    return fail(hipErrorInvalidValue, "%s: null tensor pointer", what);
+  if (!is16 && (!sa || !sw)) return fail(hipErrorInvalidValue, "%s: null scale pointer", what);
+  if (doweight && !sorted_w) return fail(hipErrorInvalidValue, "%s: null sorted_weights with doweight", what);
+
+  MoeFn fn = nullptr;
+  if (stage == 1)
+    fn = mout == MOE_OUT_BF16 ? moe_kind<1, MOE_OUT_BF16>(kind, tile_m, tile_n) : moe_kind<1, MOE_OUT_F16>(kind, tile_m, tile_n);
+  else if (mout == MOE_OUT_F32)
+    fn = moe_kind<2, MOE_OUT_F32>(kind, tile_m, tile_n);
+  else
+    fn = mout == MOE_OUT_BF16 ? moe_kind<2, MOE_OUT_BF16>(kind, tile_m, tile_n) : moe_kind<2, MOE_OUT_F16>(kind, tile_m, tile_n);
+  if (!fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d", what, tile_m, tile_n);
+
+  MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
+               sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
+               doweight ? 1 : 0};
+  // grid (N / tile_n, blocks) in the reference; here flattened with the column tile fastest, so
+  // the column tiles of one sorted block are dispatched together and share its gathered rows
+  const long ntn = N / tile_n;
+  const long g = ntn * blocks;
+  if (g >= (1L << 31)) return fail(hipErrorInvalidValue, "%s: grid too large", what);
+  hipLaunchKernelGGL(fn, dim3((unsigned)g), dim3(256), 0, stream, args);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(e, "launch of %s failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scale_x, const float* scale_w,
+                      const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
+                      const int32_t* num_valid_ids, int32_t tokens, int32_t inter_dim, int32_t model_dim,
+                      int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream) {
+  return moe_launch(1, out, x, w, scale_x, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights, num_valid_ids,
+                    tokens, inter_dim, model_dim, size_expert_ids, experts, topk, tile_m, tile_n, in_dtype, out_dtype,
+                    doweight_stage1, (hipStream_t)stream);
+}
+
+int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* scale_a2, const float* scale_w,
+                      const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
+                      const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
+                      int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, void* stream) {
+  return moe_launch(2, out, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
+                    num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
+                    in_dtype, out_dtype, doweight_stage2, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+"""MI355X MoE 2-stage GEMM: the drop-in for the reference's ``kernels/moe_gemm_2stage.py``.
+
+``compile_moe_gemm1`` / ``compile_moe_gemm2`` keep the reference's names, keyword arguments,
+argument checks and launcher signatures (reference ``kernels/moe_gemm_2stage.py:93-1264`` and
+``:1267-2481``; harness ``tests/kernels/test_moe_gemm.py:299-1170``)::
+
+    s1 = compile_moe_gemm1(model_dim=D, inter_dim=I, experts=E, topk=k, tile_m=32, tile_n=128,
+                           tile_k=128, doweight_stage1=False, in_dtype="fp8", out_dtype="f16")
+    s1(out1, x, w1, scale_x, scale_w1, sorted_token_ids, sorted_expert_ids, sorted_weights,
+       num_valid_ids, tokens, I, D, blocks, stream)
+    s2 = compile_moe_gemm2(..., doweight_stage2=True, out_dtype="f16")
+    s2(out2, a2, w2, scale_a2, scale_w2, sorted_token_ids, sorted_expert_ids, sorted_weights,
+       num_valid_ids, tokens, D, I, blocks, stream)
+
+Stage 1 writes ``out1[t, s, :] = silu(gate) * up`` for every route (token t, slot s) of the
+sorted metadata; stage 2 adds ``a2[t, s] @ W2[e]^T`` (scaled, optionally weighted) into
+``out2[t]`` with device atomics, so ``out2`` must be zeroed first, as in the reference harness.
+The metadata is what ``flydsl_amd.moe.moe_sorting`` (or the reference's ``moe_sorting``)
+produces with ``block_size == tile_m``.
+
+Behind the launchers: ``flygemm_moe_gemm1`` / ``flygemm_moe_gemm2`` of ``include/flygemm.h``,
+hand-written gfx950 kernels; no JIT and no host fallback.
+
+Built: ``in_dtype`` fp8, int8 (per-token x scale, per-row weight scale), fp16, bf16 (unscaled);
+``group_size=-1``; ``tile_m`` 16/32/64; ``tile_n`` 64/128/256.  ``int8smooth``, ``int4``,
+``int4_bf16`` and group-wise scales raise ``NotImplementedError``.  ``tile_k`` is validated as the
+reference validates it and otherwise a hint (the kernels' K tile is 128 bytes).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from ._launch import device_ptr, stream_handle
+
+_ALL_IN = ("fp8", "fp16", "bf16", "int8", "int8smooth", "int4", "int4_bf16")
+_BUILT_IN = {"fp8": "fp8", "int8": "int8", "bf16": "bf16", "fp16": "fp16"}
+_T16 = {"bf16": torch.bfloat16, "fp16": torch.float16}
+_OUT = {"f16": ("fp16", torch.float16), "bf16": ("bf16", torch.bfloat16), "f32": ("fp32", torch.float32)}
+# stage 2 spellings the reference accepts (moe_gemm_2stage.py:1315-1316)
+_OUT_ALIAS = {"fp16": "f16", "half": "f16", "bfloat16": "bf16", "fp32": "f32", "float": "f32"}
+
+
+def _check_common(in_dtype, group_size, tile_m, tile_n, tile_k):
+    if in_dtype not in _ALL_IN:
+        raise ValueError(f"in_dtype must be one of {_ALL_IN}, got {in_dtype!r}")
+    elem = 2 if in_dtype in ("fp16", "bf16", "int4_bf16") else 1
+    if (int(tile_k) * elem) % 64:
+        raise ValueError(f"tile_k_bytes must be divisible by 64, got tile_k={tile_k} (elem_bytes={elem})")
+    if (int(tile_m) * int(tile_k) * elem) % 256:
+        raise ValueError(f"tile_m*tile_k*elem_bytes must be divisible by 256: tile_m={tile_m}, tile_k={tile_k}")
+    if in_dtype not in _BUILT_IN:
+        raise NotImplementedError(f"in_dtype={in_dtype!r} has no MI355X MoE kernel in this build")
+    if int(group_size) > 0:
+        raise NotImplementedError("group-wise weight scales (group_size > 0) are not built")
+    if int(tile_m) not in (16, 32, 64):
+        raise ValueError(f"tile_m={tile_m}: the MI355X kernels take routing blocks of 16, 32 or 64 rows")
+    if int(tile_n) not in (64, 128, 256):
+        raise ValueError(f"tile_n={tile_n} must be 64, 128 or 256")
+    return elem
+
+
+class _MoeStage:
+    def __init__(self, stage, *, model_dim, inter_dim, experts, topk, tile_m, tile_n, tile_k, doweight, in_dtype,
+                 out_dtype, elem):
+        self.stage = stage
+        self.model_dim, self.inter_dim = int(model_dim), int(inter_dim)
+        self.experts, self.topk = int(experts), int(topk)
+        self.tile_m, self.tile_n, self.tile_k = int(tile_m), int(tile_n), int(tile_k)
+        self.doweight = bool(doweight)
+        self.in_dtype, self.out_dtype = in_dtype, out_dtype
+        self.elem = elem
+
+    def __call__(self, arg_out, arg_x, arg_w, arg_scale_x, arg_scale_w, arg_sorted_token_ids, arg_expert_ids,
+                 arg_sorted_weights, arg_num_valid_ids, tokens, n_in, k_in, size_expert_ids, stream=None):
+        tokens, N, K, blocks = int(tokens), int(n_in), int(k_in), int(size_expert_ids)
+        h_stream = stream_handle(stream)
+        if tokens < 0 or blocks < 0:
+            raise ValueError(f"invalid tokens={tokens} / size_expert_ids={blocks}")
+        want_n, want_k = (self.inter_dim, self.model_dim) if self.stage == 1 else (self.model_dim, self.inter_dim)
+        if N != want_n or K != want_k:
+            raise ValueError(f"stage {self.stage} was compiled for N={want_n}, K={want_k}; got N={N}, K={K}")
+        if N % self.tile_n:
+            raise ValueError(f"N={N} must be divisible by tile_n={self.tile_n}")
+        if K % self.tile_k:
+            raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
+        E, topk = self.experts, self.topk
+        a_rows = tokens if self.stage == 1 else tokens * topk
+        w_rows = E * 2 * N if self.stage == 1 else E * N
+        out_name, out_t = _OUT[self.out_dtype]
+        out_elems = tokens * topk * N if self.stage == 1 else tokens * N
+        o = device_ptr(arg_out, "arg_out", out_elems, dtypes=(out_t,))
+        if self.in_dtype in _T16:
+            x = device_ptr(arg_x, "arg_x", a_rows * K, dtypes=(_T16[self.in_dtype],))
+            w = device_ptr(arg_w, "arg_w", w_rows * K, dtypes=(_T16[self.in_dtype],))
+            sx = sw = 0  # unscaled; the reference passes empty tensors
+        else:
+            x = device_ptr(arg_x, "arg_x", a_rows * K, elem_bytes=1)
+            w = device_ptr(arg_w, "arg_w", w_rows * K, elem_bytes=1)
+            sx = device_ptr(arg_scale_x, "arg_scale_x", a_rows, dtypes=(torch.float32,))
+            sw = device_ptr(arg_scale_w, "arg_scale_w", w_rows, dtypes=(torch.float32,))
+        # moe_sorting allocates tokens*topk + E*tile_m - topk entries, which need not fill the
+        # last block; the kernels read entries only below num_valid_ids[0]
+        n_sorted = min(blocks * self.tile_m, max(tokens * topk + E * self.tile_m - topk, 0))
+        ids = device_ptr(arg_sorted_token_ids, "arg_sorted_token_ids", n_sorted, dtypes=(torch.int32,))
+        eids = device_ptr(arg_expert_ids, "arg_expert_ids", blocks, dtypes=(torch.int32,))
+        sws = (device_ptr(arg_sorted_weights, "arg_sorted_weights", n_sorted, dtypes=(torch.float32,))
+               if self.doweight else 0)
+        nv = device_ptr(arg_num_valid_ids, "arg_num_valid_ids", 1, dtypes=(torch.int32,))
+        lib = _lib.load()
+        fn = lib.flygemm_moe_gemm1 if self.stage == 1 else lib.flygemm_moe_gemm2
+        rc = fn(o, x, w, sx, sw, ids, eids, sws, nv, tokens, N, K, blocks, E, topk, self.tile_m, self.tile_n,
+                _lib.FLYGEMM_IN[_BUILT_IN[self.in_dtype]], _lib.FLYGEMM_OUT[out_name], int(self.doweight), h_stream)
+        _lib.check(rc, f"flygemm_moe_gemm{self.stage}")
+
+
+def compile_moe_gemm1(*, model_dim: int, inter_dim: int, experts: int, topk: int, tile_m: int, tile_n: int,
+                      tile_k: int, doweight_stage1: bool, in_dtype: str = "fp8", group_size: int = -1,
+                      out_dtype: str = "f16", use_cshuffle_epilog=None):
+    """Stage 1 (gate/up GEMM + silu(gate) * up); validates like reference ``moe_gemm_2stage.py:126-200``."""
+    elem = _check_common(in_dtype, group_size, tile_m, tile_n, tile_k)
+    if out_dtype not in ("f16", "bf16"):
+        raise ValueError(f"out_dtype must be 'f16' or 'bf16', got {out_dtype!r}")
+    if int(inter_dim) % int(tile_n) or int(model_dim) % int(tile_k):
+        raise ValueError(f"inter_dim={inter_dim} % tile_n={tile_n} and model_dim={model_dim} % tile_k={tile_k} must be 0")
+    return _MoeStage(1, model_dim=model_dim, inter_dim=inter_dim, experts=experts, topk=topk, tile_m=tile_m,
+                     tile_n=tile_n, tile_k=tile_k, doweight=doweight_stage1, in_dtype=in_dtype, out_dtype=out_dtype,
+                     elem=elem)
+
+
+def compile_moe_gemm2(*, model_dim: int, inter_dim: int, experts: int, topk: int, tile_m: int, tile_n: int,
+                      tile_k: int, doweight_stage2: bool, in_dtype: str = "fp8", group_size: int = -1,
+                      out_dtype: str = "f16", use_cshuffle_epilog=None, accumulate: bool = True):
+    """Stage 2 (down GEMM accumulated over the top-k slots); validates like reference
+    ``moe_gemm_2stage.py:1300-1430``.  ``accumulate=False`` (the reduce mode) is not built."""
+    elem = _check_common(in_dtype, group_size, tile_m, tile_n, tile_k)
+    out_dtype = _OUT_ALIAS.get(str(out_dtype).strip().lower(), out_dtype)
+    if out_dtype not in ("f16", "bf16", "f32"):
+        raise ValueError(f"out_dtype must be 'f16', 'bf16', or 'f32', got {out_dtype!r}")
+    if not accumulate:
+        if out_dtype == "f32":
+            raise ValueError("compile_moe_gemm2(accumulate=False) only supports out_dtype in {'f16','bf16'}")
+        raise NotImplementedError("accumulate=False (per-slot output + reduce) is not built")
+    if int(model_dim) % int(tile_n) or int(inter_dim) % int(tile_k):
+        raise ValueError(f"model_dim={model_dim} % tile_n={tile_n} and inter_dim={inter_dim} % tile_k={tile_k} must be 0")
+    return _MoeStage(2, model_dim=model_dim, inter_dim=inter_dim, experts=experts, topk=topk, tile_m=tile_m,
+                     tile_n=tile_n, tile_k=tile_k, doweight=doweight_stage2, in_dtype=in_dtype, out_dtype=out_dtype,
+                     elem=elem)

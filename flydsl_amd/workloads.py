@@ -113,3 +113,105 @@ def make_operands(w: Workload) -> dict:
     out["b_dev"] = quant.pack_int4(b_shuf) if w.kind == "int4" else b_shuf
     out.update(a=a.contiguous(), b=b.contiguous(), sa=sa.contiguous(), sb=sb.contiguous())
     return out
+
+
+# ---- MoE 2-stage ------------------------------------------------------------------------
+@dataclass(frozen=True)
+class MoeWorkload:
+    """One MoE layer: ``tokens`` routed to ``topk`` of ``experts`` experts, each expert a gate/up
+    projection [2*inter_dim, model_dim] (stage 1) and a down projection [model_dim, inter_dim]
+    (stage 2).  Shapes follow the reference's tests (``tests/kernels/test_moe_gemm.py:1173-1182,
+    1477-1489``)."""
+    name: str
+    tokens: int
+    model_dim: int
+    inter_dim: int
+    experts: int
+    topk: int
+    tile_m: int
+    tile_n1: int
+    tile_n2: int
+    kind: str = "fp8"     # "fp8" | "int8" | "bf16" | "fp16"
+    seed: int = 0
+    note: str = ""
+
+    @property
+    def routes(self) -> int:
+        return self.tokens * self.topk
+
+    @property
+    def flops1(self) -> int:
+        return 2 * self.routes * 2 * self.inter_dim * self.model_dim
+
+    @property
+    def flops2(self) -> int:
+        return 2 * self.routes * self.model_dim * self.inter_dim
+
+
+MOE_WORKLOADS = {
+    "MS": MoeWorkload("MS", 64, 256, 128, 4, 2, 16, 64, 64, note="reference test shape S"),
+    "MM": MoeWorkload("MM", 129, 1024, 256, 8, 2, 32, 128, 128, note="reference test shape M"),
+    "ML": MoeWorkload("ML", 333, 4096, 2048, 17, 9, 64, 128, 256, note="reference test shape L"),
+    "DSP": MoeWorkload("DSP", 8192, 7168, 256, 128, 8, 64, 256, 256, seed=1, note="DS-TP8-prefill-S"),
+    "DSD": MoeWorkload("DSD", 8, 7168, 256, 256, 8, 32, 256, 256, seed=2, note="DS-TP8-decode-bs8"),
+}
+
+
+def moe_custom(tokens, model_dim, inter_dim, experts, topk, tile_m, tile_n1, tile_n2, kind="fp8", seed=0):
+    return MoeWorkload("custom", tokens, model_dim, inter_dim, experts, topk, tile_m, tile_n1, tile_n2, kind, seed)
+
+
+_MOE_T16 = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def _moe_quant(x: torch.Tensor, kind: str):
+    """-> (q, scale [rows] fp32 or None) with rows over the last dimension."""
+    if kind in _MOE_T16:
+        return x.to(_MOE_T16[kind]), None
+    q, s = quant.pertoken_quant(x.reshape(-1, x.shape[-1]), quant.FP8 if kind == "fp8" else torch.int8)
+    return q.reshape(x.shape), s.reshape(-1)
+
+
+def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
+    """Synthetic operands drawn as the reference's 2-stage test draws them
+    (``test_moe_gemm.py:1236-1262``: x ~ 0.2 N(0,1), W1 ~ 0.2 N(0,1), W2 ~ 0.2/sqrt(I) N(0,1),
+    routing = softmax over the top-k of uniform scores), generated on ``device`` from
+    ``torch.Generator(device).manual_seed(seed)``, quantized per row and preshuffled; routing
+    metadata from ``flydsl_amd.moe.moe_sorting`` with ``block_size = tile_m``.
+
+    The stage-2 input ``a2`` [tokens*topk, inter_dim] is drawn directly (0.2 N(0,1), quantized
+    per row) so stage 2 can be measured and tested on its own."""
+    from .moe import moe_sorting
+
+    g = torch.Generator(device=device).manual_seed(w.seed)
+    T, D, I, E, k, s = w.tokens, w.model_dim, w.inter_dim, w.experts, w.topk, 0.2
+    x = torch.randn(T, D, generator=g, device=device) * s
+    w1 = torch.randn(E * 2 * I, D, generator=g, device=device) * s
+    w2 = torch.randn(E * D, I, generator=g, device=device) * (s / I ** 0.5)
+    score = torch.rand(T, E, generator=g, device=device)
+    vals, topk_ids = torch.topk(score, k=k, dim=1)
+    topk_w = torch.softmax(vals, dim=1).float()
+    xq, sx = _moe_quant(x, w.kind)
+    w1q, sw1 = _moe_quant(w1, w.kind)
+    w2q, sw2 = _moe_quant(w2, w.kind)
+    del w1, w2
+    sid, sw, eid, post = moe_sorting(topk_ids.to(torch.int32), topk_w, E, w.tile_m)
+    out = dict(workload=w, x=xq, sx=sx, w1=w1q, sw1=sw1, w1_shuf=quant.shuffle_weight(w1q), w2=w2q, sw2=sw2,
+               w2_shuf=quant.shuffle_weight(w2q), topk_ids=topk_ids.to(torch.int32), topk_weights=topk_w,
+               sorted_ids=sid, sorted_weights=sw, sorted_expert_ids=eid, num_valid_ids=post[:1].contiguous(),
+               blocks=int(eid.numel()))
+    if with_stage2_input:
+        a2 = torch.randn(T * k, I, generator=g, device=device) * s
+        out["a2"], out["sa2"] = _moe_quant(a2, w.kind)
+    return out
+
+
+def moe_bytes(w: MoeWorkload, stage: int, active_experts: int) -> int:
+    """Algorithmic HBM bytes of one stage: each active expert's weights and every activation,
+    scale and output element once (index/weight metadata included)."""
+    eb = 2 if w.kind in _MOE_T16 else 1
+    T, D, I, k = w.tokens, w.model_dim, w.inter_dim, w.topk
+    meta = 4 * (T * k + w.experts * w.tile_m) * 2
+    if stage == 1:
+        return active_experts * 2 * I * D * eb + T * D * eb + T * k * I * 2 + (T + active_experts * 2 * I) * 4 + meta
+    return active_experts * D * I * eb + T * k * I * eb + T * D * 2 + (T * k + active_experts * D) * 4 + meta

@@ -98,6 +98,43 @@ enum { FLYGEMM_QMODE_RECIP_TRUNC = 0, FLYGEMM_QMODE_DIV_TRUNC = 1, FLYGEMM_QMODE
 int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int32_t N, int32_t in_dtype,
                        int32_t out_dtype, int32_t mode, void* stream);
 
+/* MoE 2-stage GEMM over routing metadata sorted by expert (the reference's moe_sorting,
+ * tests/kernels/test_moe_gemm.py:97-162):
+ *   sorted_token_ids int32 [>= num_valid_ids[0]]: (slot << 24) | token, each expert's run
+ *     padded to a multiple of tile_m with entries whose token is >= tokens;
+ *   sorted_expert_ids int32 [size_expert_ids]: the expert of each tile_m-row block (-1: none);
+ *   sorted_weights fp32, aligned with sorted_token_ids (read only when doweight != 0);
+ *   num_valid_ids int32 [1]: padded row count; blocks at or past it do nothing.
+ * in_dtype FLYGEMM_IN_FP8 / _INT8 (per-token scale_x, per-row scale_w) or _BF16 / _FP16
+ * (unscaled; scale pointers ignored).  Weights preshuffled as B everywhere here.
+ * tile_m (16, 32, 64) is the routing block size the metadata was built with; tile_n (64, 128,
+ * 256, or 0 to choose) must divide the output width.  K % 128 == 0 (K % 64 for 16-bit).
+ *
+ * Stage 1: out [tokens][topk][inter_dim] (fp16 or bf16) =
+ *   silu((x[t].W1[e*2I+n]) * sx[t] * sw[e*2I+n]) * ((x[t].W1[e*2I+I+n]) * sx[t] * sw[e*2I+I+n])
+ *   (* sorted_weights if doweight_stage1); x [tokens][model_dim], W1 [experts*2*inter_dim]
+ *   [model_dim], scale_x [tokens], scale_w [experts*2*inter_dim].  Rows no route writes are
+ *   left untouched.  Replaces the launcher of compile_moe_gemm1
+ *   (reference kernels/moe_gemm_2stage.py:93-1264; oracle tests/kernels/test_ref.py:7-75). */
+int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scale_x, const float* scale_w,
+                      const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
+                      const int32_t* num_valid_ids, int32_t tokens, int32_t inter_dim, int32_t model_dim,
+                      int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream);
+
+/* Stage 2: out [tokens][model_dim] += sum over routes (a2[t*topk+s].W2[e*D+n]) * sa[t*topk+s]
+ *   * sw[e*D+n] (* sorted_weights if doweight_stage2), accumulated with device atomics (the
+ *   caller zeroes `out` first; the order of the additions is unspecified).  a2 [tokens*topk]
+ *   [inter_dim], W2 [experts*model_dim][inter_dim], scale_a2 [tokens*topk], scale_w
+ *   [experts*model_dim].  out_dtype fp16, bf16 or fp32.  Replaces the launcher of
+ *   compile_moe_gemm2 with accumulate=True (reference kernels/moe_gemm_2stage.py:1267-2481;
+ *   oracle tests/kernels/test_ref.py:78-141). */
+int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* scale_a2, const float* scale_w,
+                      const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
+                      const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
+                      int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, void* stream);
+
 /* Kernel variant table (replaces the reference's per-call tile kwargs,
  * kernels/preshuffle_gemm.py:39-53, with a static table). */
 int32_t flygemm_num_variants(void);

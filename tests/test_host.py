@@ -177,3 +177,64 @@ def test_small_operands_roundtrip_through_oracle():
     a32 = torch.randn(32, 256, generator=g)
     q, s = oq.quant_rows(a32.numpy(), "int8")
     assert np.array_equal(ops["a"].numpy(), q)
+
+
+def test_moe_abi_rejects_bad_arguments_before_launch():
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+
+    def s1(**kw):
+        a = dict(tokens=64, inter=128, model=256, blocks=12, experts=4, topk=2, tile_m=16, tile_n=64, in_dtype=0,
+                 out_dtype=1, doweight=0)
+        a.update(kw)
+        return lib.flygemm_moe_gemm1(p, p, p, p, p, p, p, p, p, a["tokens"], a["inter"], a["model"], a["blocks"],
+                                     a["experts"], a["topk"], a["tile_m"], a["tile_n"], a["in_dtype"], a["out_dtype"],
+                                     a["doweight"], None)
+
+    def err():
+        return lib.flygemm_last_error()
+
+    assert s1(tile_m=48) != 0 and b"tile_m" in err()
+    assert s1(tile_n=96) != 0 and b"tile_n" in err()
+    assert s1(inter=192, tile_n=128) != 0 and b"multiple of tile_n" in err()
+    assert s1(model=200) != 0 and b"128-byte K tile" in err()
+    assert s1(in_dtype=3, model=96) != 0 and b"multiple of 64" in err()
+    assert s1(in_dtype=2) != 0 and b"in_dtype" in err()
+    assert s1(out_dtype=2) != 0 and b"out_dtype" in err()       # stage 1 has no fp32 output
+    assert s1(topk=0) != 0 and b"topk" in err()
+    assert s1(tokens=1 << 24) != 0 and b"2^24" in err()
+    assert s1(tokens=0) == 0 and s1(blocks=0) == 0                # nothing to do
+    rc = lib.flygemm_moe_gemm2(p, p, p, None, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, None)
+    assert rc != 0 and b"null scale" in err()
+    rc = lib.flygemm_moe_gemm2(p, p, p, None, None, p, p, None, p, 64, 256, 128, 12, 4, 2, 16, 64, 3, 2, 1, None)
+    assert rc != 0 and b"sorted_weights" in err()
+    # a per-expert weight slab above 2^31 bytes is refused
+    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 8, 65536, 65536, 12, 4, 2, 16, 256, 0, 2, 0, None)
+    assert rc != 0 and b"2^31" in err()
+
+
+def test_moe_launchers_validate_like_reference():
+    from flydsl_amd.kernels.moe_gemm_2stage import compile_moe_gemm1, compile_moe_gemm2
+    kw = dict(model_dim=256, inter_dim=128, experts=4, topk=2, tile_m=16, tile_n=64, tile_k=128)
+    with pytest.raises(ValueError):
+        compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype="fp32")
+    with pytest.raises(ValueError):
+        compile_moe_gemm1(**kw, doweight_stage1=False, out_dtype="f32")
+    with pytest.raises(ValueError):
+        compile_moe_gemm1(**{**kw, "tile_k": 32}, doweight_stage1=False)       # 32 bytes per K tile
+    with pytest.raises(NotImplementedError):
+        compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype="int4_bf16")
+    with pytest.raises(NotImplementedError):
+        compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype="bf16", group_size=32)
+    with pytest.raises(ValueError):
+        compile_moe_gemm2(**kw, doweight_stage2=True, out_dtype="f32", accumulate=False)
+    with pytest.raises(NotImplementedError):
+        compile_moe_gemm2(**kw, doweight_stage2=True, accumulate=False)
+    fn = compile_moe_gemm2(**kw, doweight_stage2=True, out_dtype="float")
+    assert fn.out_dtype == "f32"
+    c = torch.empty(64 * 256, dtype=torch.float32)
+    b = torch.empty(4 * 256 * 128, dtype=torch.int8)
+    s = torch.empty(4 * 256, dtype=torch.float32)
+    i = torch.empty(200, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        fn(c, b, b, s, s, i, i, s, i, 64, 256, 128, 12)

@@ -570,3 +570,141 @@ def test_run_torch_w4_bruteforce():
             tot = sum(av[k] * 2.0 ** (int(sa[m, k // 32]) - 127) * bv[k] * 2.0 ** (int(sb[n, k // 32]) - 127)
                       for k in range(64))
             assert abs(ref[m, n] - tot) <= 1e-9 * max(1.0, abs(tot))
+
+
+# ---- MoE 2-stage ------------------------------------------------------------------------
+from oracle import moe as omoe  # noqa: E402
+from flydsl_amd.moe import moe_sorting as product_moe_sorting  # noqa: E402
+
+
+def test_moe_sorting_hand_worked_example():
+    """topk_ids [[0,2],[2,1],[0,1]], 3 experts, blocks of 2, worked out by hand from the
+    reference's loop (test_moe_gemm.py:131-155): expert 0 takes (t0,s0),(t2,s0); expert 1
+    (t1,s1),(t2,s1); expert 2 (t0,s1),(t1,s0); buffers sized 3*2 + 3*2 - 2 = 10 entries, 5 blocks."""
+    ids = np.array([[0, 2], [2, 1], [0, 1]])
+    w = np.array([[.6, .4], [.7, .3], [.5, .5]], np.float32)
+    pad = (2 << 24) | 3
+    want_ids = [0, 2, (1 << 24) | 1, (1 << 24) | 2, (1 << 24) | 0, 1, pad, pad, pad, pad]
+    want_w = [.6, .5, .3, .5, .4, .7, 0, 0, 0, 0]
+    for sid, sw, eid, post in (omoe.moe_sorting(ids, w, 3, 2),
+                               [t.numpy() for t in product_moe_sorting(torch.tensor(ids), torch.tensor(w), 3, 2)]):
+        assert list(sid) == want_ids
+        assert np.allclose(sw, want_w)
+        assert list(eid) == [0, 1, 2, -1, -1]
+        assert list(post) == [6, 3]
+    # an expert mask drops expert 1's routes and renumbers expert 2 as 1
+    sid, sw, eid, post = omoe.moe_sorting(ids, w, 3, 2, expert_mask=np.array([1, 0, 1]))
+    assert list(sid[:4]) == [0, 2, (1 << 24) | 0, 1] and list(eid[:3]) == [0, 1, -1] and list(post) == [4, 3]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_moe_sorting_invariants_and_product(seed):
+    g = np.random.default_rng(seed)
+    T, E = int(g.integers(1, 80)), int(g.integers(1, 12))
+    k, bs = int(g.integers(1, min(E, 4) + 1)), int(g.choice([1, 4, 16, 32, 64]))
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)])
+    w = g.random((T, k)).astype(np.float32)
+    mask = (g.random(E) > 0.3).astype(np.int32) if seed % 3 == 0 else None
+    sid, sw, eid, post = omoe.moe_sorting(ids, w, E, bs, mask)
+    kept = np.ones(E, bool) if mask is None else mask.astype(bool)
+    local = np.cumsum(kept) - 1
+    routes = {(t, s) for t in range(T) for s in range(k) if kept[ids[t, s]]}
+    seen = set()
+    n_valid = int(post[0])
+    assert n_valid % bs == 0 and post[1] == T
+    assert n_valid == sum(-(-int((ids == e).sum()) // bs) * bs for e in range(E) if kept[e])
+    for b in range(len(eid)):
+        rows = sid[b * bs:(b + 1) * bs] if (b + 1) * bs <= len(sid) else sid[b * bs:]
+        if b * bs >= n_valid:
+            assert eid[b] == -1
+            continue
+        for i, v in enumerate(rows):
+            t, s = int(v) & 0xFFFFFF, int(v) >> 24
+            if t == T:
+                assert s == k          # padding entry
+                continue
+            assert local[ids[t, s]] == eid[b] and (t, s) not in seen
+            assert sw[b * bs + i] == w[t, s]
+            seen.add((t, s))
+    assert seen == routes
+    assert all(int(v) == ((k << 24) | T) for v in sid[n_valid:])
+    prod = product_moe_sorting(torch.tensor(ids), torch.tensor(w), E, bs, None if mask is None else torch.tensor(mask))
+    for a, b in zip((sid, sw, eid, post), prod):
+        assert np.array_equal(a, b.numpy())
+
+
+def test_silu_closed_forms():
+    x = np.array([0.0, 1.0, -1.0, 2.5, -30.0, 30.0, 1e-3])
+    y = omoe.silu(x)
+    assert y[0] == 0.0
+    assert abs(y[1] - 1.0 / (1.0 + np.exp(-1.0))) < 1e-15              # sigmoid(1) = 0.7310585786...
+    assert abs(y[1] - 0.7310585786300049) < 1e-15
+    assert np.allclose(omoe.silu(x) - omoe.silu(-x), x, rtol=0, atol=1e-12)   # x*s(x) + x*s(-x)... = x
+    assert abs(y[4]) < 1e-11 and abs(y[5] - 30.0) < 1e-11
+
+
+def _moe_case(seed, T=6, D=64, I=32, E=4, k=2, kind="fp8"):
+    g = np.random.default_rng(seed)
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)])
+    w = g.random((T, k)).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    x = g.standard_normal((T, D)).astype(np.float32)
+    w1 = (g.standard_normal((E * 2 * I, D)) * 0.2).astype(np.float32)
+    xq, sx = oq.quant_rows(x, kind)
+    w1q, sw1 = oq.quant_rows(w1, kind)
+    return ids, w, xq, sx.reshape(-1), w1q, sw1.reshape(-1)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+@pytest.mark.parametrize("doweight", [False, True])
+def test_moe_gemm1_route_and_sorted_forms_agree(kind, doweight):
+    T, D, I, E, k, bs = 7, 64, 32, 5, 3, 4
+    ids, w, xq, sx, w1q, sw1 = _moe_case(3, T, D, I, E, k, kind)
+    ref = omoe.gemm1(xq, w1q, sx, sw1, ids, w, I, doweight, kind)
+    sid, sw, eid, post = omoe.moe_sorting(ids, w, E, bs)
+    alt = omoe.gemm1_sorted(xq, w1q, sx, sw1, sid, sw, eid, post[0], bs, T, k, I, doweight, kind)
+    assert np.allclose(ref, alt, rtol=1e-12, atol=1e-12)
+    # a subset of tokens leaves the other rows at zero and the chosen ones unchanged
+    sub = omoe.gemm1(xq, w1q, sx, sw1, ids, w, I, doweight, kind, tokens_subset=[1, 4])
+    assert np.allclose(sub[[1, 4]], ref[[1, 4]], rtol=1e-12, atol=1e-12) and not sub[[0, 2, 3, 5, 6]].any()
+
+
+def test_moe_gemm1_gate_up_order():
+    """Zeroing the up rows zeroes the output; zeroing the gate rows gives silu(0) * up = 0 as
+    well, but a huge positive gate turns silu(gate) * up into gate * up: the two halves are told
+    apart by which one scales linearly."""
+    T, D, I, E, k = 3, 64, 16, 2, 1
+    ids, w, xq, sx, w1q, sw1 = _moe_case(5, T, D, I, E, k, "int8")
+    sw_up0 = sw1.copy().reshape(E, 2, I)
+    sw_up0[:, 1] = 0
+    assert not omoe.gemm1(xq, w1q, sx, sw_up0.reshape(-1), ids, w, I, False, "int8").any()
+    base = omoe.gemm1(xq, w1q, sx, sw1, ids, w, I, False, "int8")
+    sw_up2 = sw1.copy().reshape(E, 2, I)
+    sw_up2[:, 1] *= 2
+    assert np.allclose(omoe.gemm1(xq, w1q, sx, sw_up2.reshape(-1), ids, w, I, False, "int8"), 2 * base, rtol=1e-12)
+
+
+def test_moe_gemm2_equal_experts_is_one_dense_matmul():
+    """Every expert holding the same W2, every slot of a token holding the same a2 row and
+    routing weights summing to one: the weighted sum over slots is a2 @ W2^T."""
+    T, I, D, E, k = 5, 64, 48, 3, 3
+    g = np.random.default_rng(8)
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)])
+    w = g.random((T, k))
+    w = (w / w.sum(1, keepdims=True)).astype(np.float32)
+    a = g.standard_normal((T, I)).astype(np.float32)
+    aq, sa = oq.quant_rows(a, "int8")
+    a2q = np.repeat(aq, k, axis=0)
+    sa2 = np.repeat(sa.reshape(-1), k)
+    W = (g.standard_normal((D, I)) * 0.1).astype(np.float32)
+    Wq, sW = oq.quant_rows(W, "int8")
+    w2q, sw2 = np.tile(Wq, (E, 1)), np.tile(sW.reshape(-1), E)
+    got = omoe.gemm2(a2q, w2q, sa2, sw2, ids, w, D, True, "int8")
+    dense = og.run_torch(aq, Wq, sa.reshape(-1), sW.reshape(-1), "int8", "f64")
+    assert np.allclose(got, dense * w.astype(np.float64).sum(1, keepdims=True), rtol=1e-12, atol=1e-12)
+    assert np.allclose(got, dense, rtol=1e-6, atol=1e-6)
+    # without the weights the slots add up: k times the dense product
+    assert np.allclose(omoe.gemm2(a2q, w2q, sa2, sw2, ids, w, D, False, "int8"), k * dense, rtol=1e-12)
+    sid, sw, eid, post = omoe.moe_sorting(ids, w, E, 4)
+    alt = omoe.gemm2_sorted(a2q, w2q, sa2, sw2, sid, sw, eid, post[0], 4, T, k, D, True, "int8")
+    assert np.allclose(alt, got, rtol=1e-12, atol=1e-12)
