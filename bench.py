@@ -132,9 +132,77 @@ class QuantRunner:
     time = Runner.time
 
 
+class MoeStageWorkload:
+    """One stage of an MoE layer (``workloads.MOE_WORKLOADS``): M = routes (tokens * topk),
+    N = the stage's output width, K = its reduction width; bytes = the active experts' weights
+    plus activations, scales, outputs and routing metadata once; flops = 2 * routes * N_total * K
+    (stage 1 counts gate and up)."""
+
+    def __init__(self, name: str, base: workloads.MoeWorkload, stage: int, active_experts: int):
+        self.name, self.base, self.stage, self.kind = name, base, stage, base.kind
+        self.M = base.routes
+        self.N = 2 * base.inter_dim if stage == 1 else base.model_dim
+        self.K = base.model_dim if stage == 1 else base.inter_dim
+        self.seed = base.seed
+        self.flops = base.flops1 if stage == 1 else base.flops2
+        self.bytes = workloads.moe_bytes(base, stage, active_experts)
+        self.note = f"MoE stage {stage}, {base.note}: {base.tokens} tokens, E={base.experts} top-{base.topk}, " \
+                    f"model_dim {base.model_dim}, inter_dim {base.inter_dim}, {active_experts} experts active"
+
+
+# bench name -> (MoE workload, stage)
+# (the R variants run stage 2 in reduce mode: per-route rows, then the top-k reduction)
+MOE_BENCH = {"MP1": ("DSP", 1), "MP2": ("DSP", 2), "MP2R": ("DSP", 2), "MD1": ("DSD", 1), "MD2": ("DSD", 2),
+             "MD2R": ("DSD", 2)}
+
+
+class MoeRunner:
+    def __init__(self, name: str, dev, min_rotation_bytes=0):
+        from flydsl_amd.kernels.moe_gemm_2stage import compile_moe_gemm1, compile_moe_gemm2
+
+        key, stage = MOE_BENCH[name]
+        base = workloads.MOE_WORKLOADS[key]
+        p = workloads.moe_problem(base, dev, with_stage2_input=stage == 2)
+        active = int(torch.unique(p["topk_ids"]).numel())
+        self.w = MoeStageWorkload(name, base, stage, active)
+        self.p, self.stage = p, stage
+        kw = dict(model_dim=base.model_dim, inter_dim=base.inter_dim, experts=base.experts, topk=base.topk,
+                  tile_m=base.tile_m, tile_k=128, in_dtype=base.kind)
+        if stage == 1:
+            self.fn = compile_moe_gemm1(**kw, tile_n=base.tile_n1, doweight_stage1=False, out_dtype="f16")
+            self.out = torch.empty(base.tokens, base.topk, base.inter_dim, dtype=torch.float16, device=dev)
+            self.args = (_dev_flat(p["x"], dev), _dev_flat(p["w1_shuf"], dev), p["sx"], p["sw1"])
+            self.nk = (base.inter_dim, base.model_dim)
+        elif name.endswith("R"):
+            from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+            # every route is written (no mask), so the intermediate needs no zeroing
+            self.fn = compile_moe_gemm2_ex(**kw, tile_n=base.tile_n2, doweight_stage2=True, out_dtype="f16",
+                                           mode=MoeGemm2Mode.REDUCE, zero_intermediate=False)
+            self.out = torch.zeros(base.tokens, base.model_dim, dtype=torch.float16, device=dev)
+            self.args = (_dev_flat(p["a2"], dev), _dev_flat(p["w2_shuf"], dev), p["sa2"], p["sw2"])
+            self.nk = (base.model_dim, base.inter_dim)
+        else:
+            self.fn = compile_moe_gemm2(**kw, tile_n=base.tile_n2, doweight_stage2=True, out_dtype="f16")
+            self.out = torch.zeros(base.tokens, base.model_dim, dtype=torch.float16, device=dev)
+            self.args = (_dev_flat(p["a2"], dev), _dev_flat(p["w2_shuf"], dev), p["sa2"], p["sw2"])
+            self.nk = (base.model_dim, base.inter_dim)
+        self.copies = 1
+        self.variant = f"moe_gemm{stage}_{base.tile_m}x{base.tile_n1 if stage == 1 else base.tile_n2}" + \
+            ("+reduce" if name.endswith("R") else "")
+
+    def launch(self, i, stream):
+        p, b = self.p, self.w.base
+        self.fn(self.out, *self.args, p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"],
+                p["num_valid_ids"], b.tokens, self.nk[0], self.nk[1], p["blocks"], stream)
+
+    time = Runner.time
+
+
 def make_runner(name, dev, **kw):
     if name == "Q":
         return QuantRunner(QuantWorkload(), dev, **kw)
+    if name in MOE_BENCH:
+        return MoeRunner(name, dev, **kw)
     return Runner(workloads.WORKLOADS[name], dev, **kw)
 
 
@@ -314,7 +382,8 @@ def main():
 
     extra = [n for n in args.secondary.split(",") if n]
     if args.all:
-        extra += [n for n in list(workloads.WORKLOADS) + ["Q"] if n not in extra and n != args.workload]
+        extra += [n for n in list(workloads.WORKLOADS) + ["Q"] + list(MOE_BENCH)
+                  if n not in extra and n != args.workload]
     sec = {}
     for name in extra:
         r2 = make_runner(name, dev)
@@ -322,7 +391,7 @@ def main():
         log(f"[bench] preparing {name} {w2.kind} {w2.M}x{w2.N}x{w2.K}")
         log(f"[bench] timing {name} variant={r2.variant}")
         ms2, _ = r2.time(max(5, args.steps // 2), max(2, args.warmup // 2))
-        b2 = "hbm" if name in ("C1", "C2", "Q") else "mfma"
+        b2 = "hbm" if name in ("C1", "C2", "Q", "MD1", "MD2", "MD2R") else "mfma"
         sec[name] = {"ms": round(ms2, 5), "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
         if w2.flops:

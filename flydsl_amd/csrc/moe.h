@@ -41,9 +41,14 @@ struct MoeArgs {
   int tokens, topk, N, K;      // N: inter_dim (stage 1) or model_dim (stage 2); K in bytes
   int experts;
   int doweight;
+  int blocks;                  // sorted blocks (size_expert_ids)
 };
 
-enum MoeOut : int { MOE_OUT_F16 = 0, MOE_OUT_BF16 = 1, MOE_OUT_F32 = 2 };
+// Stage-2 outputs: F16/BF16/F32 accumulate into out[token] with atomics; *_ROWS store each
+// route's row out[token*topk + slot] with plain stores (the reduce mode, summed by
+// moe_reduce_kernel afterwards).  Stage 1 takes F16 or BF16.
+enum MoeOut : int { MOE_OUT_F16 = 0, MOE_OUT_BF16 = 1, MOE_OUT_F32 = 2, MOE_OUT_F16_ROWS = 3, MOE_OUT_BF16_ROWS = 4 };
+constexpr bool moe_out_bf16(int o) { return o == MOE_OUT_BF16 || o == MOE_OUT_BF16_ROWS; }
 
 // x * sigmoid(x) = x / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal
 // (reference moe_gemm_2stage.py:271-281 evaluates it the same way)
@@ -75,11 +80,21 @@ __global__ void __launch_bounds__(256) moe_gemm_kernel(MoeArgs p) {
   static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "MoE input kinds");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2][C::STG];
 
-  // flattened grid: column tile fastest, then sorted block
+  // Workgroups are dealt to the 8 XCDs round-robin.  Logical tile L (column tile fastest, then
+  // sorted block) runs as workgroup (L % chunk) * 8 + L / chunk, i.e. each XCD takes one
+  // contiguous range of L, so the consecutive blocks of one expert share that XCD's L2 copy of
+  // the expert's weights instead of each XCD fetching them.  The grid has at least 8 * chunk
+  // workgroups.
+  // Only the tiles of blocks below num_valid_ids are dealt out, so a short routing (decode)
+  // still spreads over every XCD.
+  const int nv = p.num_valid[0];
   const int ntn = p.N / TN;
-  const int by = blockIdx.x / ntn;
-  const int n0 = (blockIdx.x - by * ntn) * TN;
-  if (by * TM >= p.num_valid[0]) return;
+  const int V = ntn * min((nv + TM - 1) / TM, p.blocks);
+  const int chunk = (V + 7) >> 3;
+  const int L = (blockIdx.x & 7) * chunk + (blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= chunk || L >= V) return;
+  const int by = L / ntn;
+  const int n0 = (L - by * ntn) * TN;
   const int e = p.expert_ids[by];
   if (e < 0 || e >= p.experts) return;
   const int K = p.K;
@@ -176,21 +191,36 @@ __global__ void __launch_bounds__(256) moe_gemm_kernel(MoeArgs p) {
     compute(lds[kt & 1]);
   }
 
-  // ---- epilogue: lane holds row mi*16 + l16 of the block, columns 4*lq .. 4*lq+3 of each
-  // 16-column block ----
+  // ---- epilogue, through LDS so that global writes are row-contiguous ----
+  // Phase 1: lane (l16, lq) holds row mi*16 + l16 of the block and columns 4*lq .. 4*lq+3 of
+  // each 16-column block; it scales them and writes them to an LDS tile [TM][TN] (padded rows).
+  // Phase 2: the workgroup walks the tile row by row, each wave instruction covering 256
+  // contiguous bytes of one output row: 16-byte stores (stage 1) or 4-byte atomics (stage 2;
+  // fp16/bf16 as packed pairs).  Scattered 4-lane fragments would touch 16 cache lines per
+  // instruction, which costs the atomics 8x their useful rate.
   constexpr bool kScaled = !kind_is_16bit(KIND);
+  constexpr bool kRows = STAGE == 1 || OUT == MOE_OUT_F16_ROWS || OUT == MOE_OUT_BF16_ROWS;  // plain stores
+  constexpr int ESZ = (STAGE == 2 && OUT == MOE_OUT_F32) ? 4 : 2;
+  constexpr int RS = TN * ESZ + 16;            // LDS bytes per tile row (padding spreads banks)
+  static_assert(TM * RS + TM * 4 <= 2 * C::STG, "output tile fits in the stage buffers");
+  uint8_t* ot = &lds[0][0];
+  int32_t* rowdst = (int32_t*)(ot + TM * RS);  // destination row per tile row, -1 for padding
+  workgroup_barrier();                         // every wave is done with the last K tile
 #pragma unroll
   for (int mi = 0; mi < MR; ++mi) {
-    const int i = by * TM + mi * 16 + l16;
+    const int r = mi * 16 + l16;
+    const int i = by * TM + r;
     const int id = p.sorted_ids[i];
     const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
-    if (t >= p.tokens || s >= p.topk) continue;
+    const bool valid = t < p.tokens && s < p.topk;
+    if (wave == 0 && lq == 0) rowdst[r] = !valid ? -1 : (kRows ? t * p.topk + s : t);
     const int arow = STAGE == 1 ? t : t * p.topk + s;
-    const float sx = kScaled ? p.sa[arow] : 1.f;
-    const float rw = p.doweight ? p.sorted_w[i] : 1.f;
+    const float sx = kScaled && valid ? p.sa[arow] : 1.f;
+    const float rw = p.doweight && valid ? p.sorted_w[i] : 1.f;
 #pragma unroll
     for (int ni = 0; ni < NR; ++ni) {
-      const int n = n0 + (wave * NR + ni) * 16 + lq * 4;
+      const int c = (wave * NR + ni) * 16 + lq * 4;
+      const int n = n0 + c;
       float v[4];
       if constexpr (STAGE == 1) {
         f32x4 swg = f32x4{1.f, 1.f, 1.f, 1.f}, swu = swg;
@@ -199,43 +229,98 @@ __global__ void __launch_bounds__(256) moe_gemm_kernel(MoeArgs p) {
           swu = *(const f32x4*)(p.sw + (size_t)e * 2 * p.N + p.N + n);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float g = ((float)acc[0][mi][ni][r] * sx) * swg[r];
-          const float u = ((float)acc[1][mi][ni][r] * sx) * swu[r];
-          v[r] = silu_f(g) * u;
-          if (p.doweight) v[r] *= rw;
+        for (int q = 0; q < 4; ++q) {
+          const float g = ((float)acc[0][mi][ni][q] * sx) * swg[q];
+          const float u = ((float)acc[1][mi][ni][q] * sx) * swu[q];
+          v[q] = silu_f(g) * u;
+          if (p.doweight) v[q] *= rw;
         }
-        const size_t o = ((size_t)t * p.topk + s) * p.N + n;
-        if constexpr (OUT == MOE_OUT_BF16)
-          *(i32x2*)((__bf16*)p.out + o) = pack_out4<true>(v);
-        else
-          *(i32x2*)((_Float16*)p.out + o) = pack_out4<false>(v);
       } else {
         f32x4 swd = f32x4{1.f, 1.f, 1.f, 1.f};
         if constexpr (kScaled) swd = *(const f32x4*)(p.sw + (size_t)e * p.N + n);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          v[r] = ((float)acc[0][mi][ni][r] * sx) * swd[r];
-          if (p.doweight) v[r] *= rw;
-        }
-        const size_t o = (size_t)t * p.N + n;
-        if constexpr (OUT == MOE_OUT_F32) {
-          float* dst = (float*)p.out + o;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) unsafeAtomicAdd(dst + r, v[r]);
-        } else if constexpr (OUT == MOE_OUT_BF16) {
-          typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-          bf16x2* dst = (bf16x2*)((__bf16*)p.out + o);
-          __builtin_amdgcn_global_atomic_fadd_v2bf16(dst, bf16x2{(__bf16)v[0], (__bf16)v[1]});
-          __builtin_amdgcn_global_atomic_fadd_v2bf16(dst + 1, bf16x2{(__bf16)v[2], (__bf16)v[3]});
-        } else {
-          typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-          f16x2* dst = (f16x2*)((_Float16*)p.out + o);
-          __builtin_amdgcn_global_atomic_fadd_v2f16(dst, f16x2{(_Float16)v[0], (_Float16)v[1]});
-          __builtin_amdgcn_global_atomic_fadd_v2f16(dst + 1, f16x2{(_Float16)v[2], (_Float16)v[3]});
+        for (int q = 0; q < 4; ++q) {
+          v[q] = ((float)acc[0][mi][ni][q] * sx) * swd[q];
+          if (p.doweight) v[q] *= rw;
         }
       }
+      uint8_t* dst = ot + r * RS + c * ESZ;
+      if constexpr (ESZ == 4)
+        *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+      else
+        *(i32x2*)dst = pack_out4<moe_out_bf16(OUT)>(v);
     }
+  }
+  workgroup_barrier();
+  if constexpr (kRows) {
+    constexpr int CPR = TN * 2 / 16;           // 16-byte chunks per output row
+    for (int idx = tid; idx < TM * CPR; idx += 256) {
+      const int r = idx / CPR, cc = idx - r * CPR;
+      const int d = rowdst[r];
+      if (d < 0) continue;
+      const i32x4 val = *(const i32x4*)(ot + r * RS + cc * 16);
+      *(i32x4*)((uint8_t*)p.out + ((size_t)d * p.N + n0) * 2 + cc * 16) = val;
+    }
+  } else {
+    constexpr int WPR = TN * ESZ / 4;          // 4-byte words per output row
+    for (int idx = tid; idx < TM * WPR; idx += 256) {
+      const int r = idx / WPR, wd = idx - r * WPR;
+      const int d = rowdst[r];
+      if (d < 0) continue;
+      uint8_t* dst = (uint8_t*)p.out + ((size_t)d * p.N + n0) * ESZ + wd * 4;
+      const uint8_t* src = ot + r * RS + wd * 4;
+      if constexpr (OUT == MOE_OUT_F32) {
+        unsafeAtomicAdd((float*)dst, *(const float*)src);
+      } else if constexpr (OUT == MOE_OUT_BF16) {
+        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_global_atomic_fadd_v2bf16((bf16x2*)dst, *(const bf16x2*)src);
+      } else {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_global_atomic_fadd_v2f16((f16x2*)dst, *(const f16x2*)src);
+      }
+    }
+  }
+}
+
+// Reduce mode, second kernel: y[t][d] = sum over slots k of x[t][k][d] (slots with
+// valid_mask[t][k] == 0 skipped when a mask is given), fp32 sums, one 16-byte vector of d per
+// thread; x is read once, so it is loaded non-temporally (reference compile_moe_reduction,
+// kernels/moe_gemm_2stage.py:2484-2604).  DT: 0 fp16, 1 bf16, 2 fp32.
+template <int DT>
+__global__ void __launch_bounds__(256) moe_reduce_kernel(void* y, const void* x, const int8_t* mask, int tokens,
+                                                         int topk, int D) {
+  constexpr int ESZ = DT == 2 ? 4 : 2;
+  constexpr int VE = 16 / ESZ;                 // elements per vector
+  const int vpr = D / VE;                      // vectors per row
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)tokens * vpr) return;
+  const int t = (int)(idx / vpr), v = (int)(idx - (long)t * vpr);
+  float acc[VE];
+#pragma unroll
+  for (int q = 0; q < VE; ++q) acc[q] = 0.f;
+  const i32x4* src = (const i32x4*)x + ((long)t * topk * vpr + v);
+  for (int k = 0; k < topk; ++k) {
+    if (mask && mask[(long)t * topk + k] == 0) continue;
+    const i32x4 w = __builtin_nontemporal_load(src + (long)k * vpr);
+    if constexpr (DT == 2) {
+      const f32x4 f = __builtin_bit_cast(f32x4, w);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] += f[q];
+    } else {
+      typedef typename OutT<DT == 1>::type ET;
+      typedef ET ET8 __attribute__((ext_vector_type(8)));
+      const ET8 h = __builtin_bit_cast(ET8, w);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] += (float)h[q];
+    }
+  }
+  i32x4* dst = (i32x4*)y + idx;
+  if constexpr (DT == 2) {
+    *dst = __builtin_bit_cast(i32x4, f32x4{acc[0], acc[1], acc[2], acc[3]});
+  } else {
+    const float lo[4] = {acc[0], acc[1], acc[2], acc[3]}, hi[4] = {acc[4], acc[5], acc[6], acc[7]};
+    const i32x2 a = pack_out4<DT == 1>(lo), b = pack_out4<DT == 1>(hi);
+    *dst = i32x4{a.x, a.y, b.x, b.y};
   }
 }
 

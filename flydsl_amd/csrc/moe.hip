@@ -44,7 +44,7 @@ int pick_tile_n(int N) {
 int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
                const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
                const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
-               int tile_n, int in_dtype, int out_dtype, int doweight, hipStream_t stream) {
+               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, hipStream_t stream) {
   const char* what = stage == 1 ? "moe_gemm1" : "moe_gemm2";
   if (tokens < 0 || N <= 0 || K <= 0 || blocks < 0 || experts <= 0)
     return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d N=%d K=%d blocks=%d experts=%d", what, tokens, N, K,
@@ -74,10 +74,12 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (a_rows * kb >= (1L << 31) || w_rows * kb >= (1L << 31))
     return fail(hipErrorInvalidValue, "%s: activation or per-expert weight above 2^31 bytes", what);
   int mout;
-  if (out_dtype == FLYGEMM_OUT_FP16) mout = MOE_OUT_F16;
-  else if (out_dtype == FLYGEMM_OUT_BF16) mout = MOE_OUT_BF16;
-  else if (out_dtype == FLYGEMM_OUT_F32 && stage == 2) mout = MOE_OUT_F32;
-  else return fail(hipErrorInvalidValue, "%s: out_dtype %d not supported", what, out_dtype);
+  const bool rows = stage == 2 && !accumulate;
+  if (out_dtype == FLYGEMM_OUT_FP16) mout = rows ? MOE_OUT_F16_ROWS : MOE_OUT_F16;
+  else if (out_dtype == FLYGEMM_OUT_BF16) mout = rows ? MOE_OUT_BF16_ROWS : MOE_OUT_BF16;
+  else if (out_dtype == FLYGEMM_OUT_F32 && stage == 2 && accumulate) mout = MOE_OUT_F32;
+  else return fail(hipErrorInvalidValue, "%s: out_dtype %d not supported%s", what, out_dtype,
+                   rows ? " without accumulation (fp16 or bf16)" : "");
   if (tokens == 0 || blocks == 0) return 0;
   if (!out || !a || !w || !sorted_ids || !expert_ids || !num_valid)
     return fail(hipErrorInvalidValue, "%s: null tensor pointer", what);
@@ -89,17 +91,21 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
     fn = mout == MOE_OUT_BF16 ? moe_kind<1, MOE_OUT_BF16>(kind, tile_m, tile_n) : moe_kind<1, MOE_OUT_F16>(kind, tile_m, tile_n);
   else if (mout == MOE_OUT_F32)
     fn = moe_kind<2, MOE_OUT_F32>(kind, tile_m, tile_n);
+  else if (mout == MOE_OUT_F16_ROWS)
+    fn = moe_kind<2, MOE_OUT_F16_ROWS>(kind, tile_m, tile_n);
+  else if (mout == MOE_OUT_BF16_ROWS)
+    fn = moe_kind<2, MOE_OUT_BF16_ROWS>(kind, tile_m, tile_n);
   else
     fn = mout == MOE_OUT_BF16 ? moe_kind<2, MOE_OUT_BF16>(kind, tile_m, tile_n) : moe_kind<2, MOE_OUT_F16>(kind, tile_m, tile_n);
   if (!fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d", what, tile_m, tile_n);
 
   MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
                sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
-               doweight ? 1 : 0};
-  // grid (N / tile_n, blocks) in the reference; here flattened with the column tile fastest, so
-  // the column tiles of one sorted block are dispatched together and share its gathered rows
+               doweight ? 1 : 0, blocks};
+  // grid (N / tile_n, blocks) in the reference; here one dimension, rounded up to a multiple of
+  // 8 for the kernel's XCD-aware order (the extra workgroups exit at once)
   const long ntn = N / tile_n;
-  const long g = ntn * blocks;
+  const long g = (ntn * blocks + 7) / 8 * 8;
   if (g >= (1L << 31)) return fail(hipErrorInvalidValue, "%s: grid too large", what);
   hipLaunchKernelGGL(fn, dim3((unsigned)g), dim3(256), 0, stream, args);
   hipError_t e = hipGetLastError();
@@ -118,17 +124,45 @@ int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scal
                       int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream) {
   return moe_launch(1, out, x, w, scale_x, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights, num_valid_ids,
                     tokens, inter_dim, model_dim, size_expert_ids, experts, topk, tile_m, tile_n, in_dtype, out_dtype,
-                    doweight_stage1, (hipStream_t)stream);
+                    doweight_stage1, 1, (hipStream_t)stream);
 }
 
 int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* scale_a2, const float* scale_w,
                       const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
                       const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
-                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, void* stream) {
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, int32_t accumulate,
+                      void* stream) {
   return moe_launch(2, out, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
                     num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
-                    in_dtype, out_dtype, doweight_stage2, (hipStream_t)stream);
+                    in_dtype, out_dtype, doweight_stage2, accumulate, (hipStream_t)stream);
+}
+
+int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t tokens, int32_t topk,
+                       int32_t model_dim, int32_t dtype, void* stream) {
+  if (tokens < 0 || topk < 1 || model_dim <= 0)
+    return fail(hipErrorInvalidValue, "moe_reduce: invalid sizes tokens=%d topk=%d model_dim=%d", tokens, topk,
+                model_dim);
+  if (dtype != FLYGEMM_OUT_FP16 && dtype != FLYGEMM_OUT_BF16 && dtype != FLYGEMM_OUT_F32)
+    return fail(hipErrorInvalidValue, "moe_reduce: dtype %d not supported", dtype);
+  const int ve = dtype == FLYGEMM_OUT_F32 ? 4 : 8;
+  if (model_dim % ve != 0)
+    return fail(hipErrorInvalidValue, "moe_reduce: model_dim=%d must be a multiple of %d (16-byte vectors)",
+                model_dim, ve);
+  if (tokens == 0) return 0;
+  if (!y || !x) return fail(hipErrorInvalidValue, "moe_reduce: null tensor pointer");
+  if (((uintptr_t)y | (uintptr_t)x) & 15) return fail(hipErrorInvalidValue, "moe_reduce: misaligned pointer");
+  const long n = (long)tokens * (model_dim / ve);
+  const long g = (n + 255) / 256;
+  if (g >= (1L << 31)) return fail(hipErrorInvalidValue, "moe_reduce: too large");
+  void (*fn)(void*, const void*, const int8_t*, int, int, int) =
+      dtype == FLYGEMM_OUT_FP16 ? moe_reduce_kernel<0> : dtype == FLYGEMM_OUT_BF16 ? moe_reduce_kernel<1>
+                                                                                   : moe_reduce_kernel<2>;
+  hipLaunchKernelGGL(fn, dim3((unsigned)g), dim3(256), 0, (hipStream_t)stream, y, x, (const int8_t*)valid_mask,
+                     tokens, topk, model_dim);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(e, "launch of moe_reduce failed: %s", hipGetErrorString(e));
+  return 0;
 }
 
 }  // extern "C"

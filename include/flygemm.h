@@ -122,18 +122,30 @@ int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scal
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
                       int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream);
 
-/* Stage 2: out [tokens][model_dim] += sum over routes (a2[t*topk+s].W2[e*D+n]) * sa[t*topk+s]
- *   * sw[e*D+n] (* sorted_weights if doweight_stage2), accumulated with device atomics (the
- *   caller zeroes `out` first; the order of the additions is unspecified).  a2 [tokens*topk]
- *   [inter_dim], W2 [experts*model_dim][inter_dim], scale_a2 [tokens*topk], scale_w
- *   [experts*model_dim].  out_dtype fp16, bf16 or fp32.  Replaces the launcher of
- *   compile_moe_gemm2 with accumulate=True (reference kernels/moe_gemm_2stage.py:1267-2481;
- *   oracle tests/kernels/test_ref.py:78-141). */
+/* Stage 2, per route r = (t, s) of expert e: y_r[n] = (a2[t*topk+s].W2[e*D+n]) * sa[t*topk+s]
+ *   * sw[e*D+n] (* sorted_weights if doweight_stage2); a2 [tokens*topk][inter_dim], W2
+ *   [experts*model_dim][inter_dim], scale_a2 [tokens*topk], scale_w [experts*model_dim].
+ *   accumulate != 0: out [tokens][model_dim] += sum over the token's routes, with device atomics
+ *     (the caller zeroes `out` first; the order of the additions is unspecified); out_dtype
+ *     fp16, bf16 or fp32.
+ *   accumulate == 0: out [tokens*topk][model_dim] row t*topk+s = y_r, plain stores (rows no
+ *     route writes are left untouched); out_dtype fp16 or bf16; flygemm_moe_reduce sums them.
+ *   Replaces the launcher of compile_moe_gemm2(accumulate=True/False)
+ *   (reference kernels/moe_gemm_2stage.py:1267-2481; oracle tests/kernels/test_ref.py:78-141). */
 int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* scale_a2, const float* scale_w,
                       const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
                       const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
-                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, void* stream);
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, int32_t accumulate,
+                      void* stream);
+
+/* Reduce mode, second step: y [tokens][model_dim] = sum over k < topk of x [tokens][topk]
+ * [model_dim] (only slots with valid_mask[t*topk+k] != 0 when valid_mask, int8 [tokens*topk], is
+ * given), fp32 sums; dtype fp16, bf16 or fp32 for both x and y; model_dim a multiple of 8 (4 for
+ * fp32); x and y 16-byte aligned.  Replaces the launcher of compile_moe_reduction (reference
+ * kernels/moe_gemm_2stage.py:2484-2604). */
+int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t tokens, int32_t topk,
+                       int32_t model_dim, int32_t dtype, void* stream);
 
 /* Kernel variant table (replaces the reference's per-call tile kwargs,
  * kernels/preshuffle_gemm.py:39-53, with a static table). */

@@ -252,3 +252,79 @@ def test_launcher_checks(gpu):
         fn(out.float(), H.dev_flat(p["x"], gpu), H.dev_flat(p["w1_shuf"], gpu), p["sx"], p["sw1"],
            p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"], p["num_valid_ids"], w.tokens,
            w.inter_dim, w.model_dim, p["blocks"])
+
+
+@pytest.mark.parametrize("kind", ["fp8", "bf16"])
+@pytest.mark.parametrize("shape", ["MS", "MM"])
+@pytest.mark.parametrize("out_dtype", ["f16", "bf16"])
+def test_stage2_reduce_mode(gpu, kind, shape, out_dtype):
+    """Reduce mode (reference compile_moe_gemm2_ex(mode='reduce'), test_moe_gemm.py:1363-1475):
+    per-route rows with plain stores, then the top-k reduction."""
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+
+    p = _problem(shape, kind, gpu, seed=21)
+    w = p["workload"]
+    _say(f"stage2 reduce {shape} {kind} {out_dtype}")
+    fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                              tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=128, doweight_stage2=True, in_dtype=kind,
+                              out_dtype=out_dtype, mode=MoeGemm2Mode.REDUCE)
+    out = torch.full((w.tokens, w.model_dim), float("nan"), dtype=OUT_T[out_dtype], device=gpu)
+    empty = torch.empty(0, dtype=torch.float32, device=gpu)
+    fn(out, H.dev_flat(p["a2"], gpu), H.dev_flat(p["w2_shuf"], gpu), empty if p["sa2"] is None else p["sa2"],
+       empty if p["sw2"] is None else p["sw2"], p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"],
+       p["num_valid_ids"], w.tokens, w.model_dim, w.inter_dim, p["blocks"])
+    torch.cuda.synchronize()
+    _check(out, ref_stage2(p, True), what=f"reduce {shape} {kind} {out_dtype}")
+
+
+def test_stage2_reduce_mode_with_valid_mask(gpu):
+    """Slots whose valid_mask is 0 are left out of the sum (the reference's masked reduction)."""
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+
+    p = _problem("MM", "fp8", gpu, seed=22)
+    w = p["workload"]
+    g = torch.Generator(device=gpu).manual_seed(3)
+    mask = (torch.rand(w.tokens, w.topk, generator=g, device=gpu) > 0.3).to(torch.int8)
+    _say("stage2 reduce masked")
+    fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                              tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=128, doweight_stage2=True,
+                              out_dtype="f16", mode=MoeGemm2Mode.REDUCE, valid_mask=mask)
+    out = torch.empty(w.tokens, w.model_dim, dtype=torch.float16, device=gpu)
+    fn(out, H.dev_flat(p["a2"], gpu), H.dev_flat(p["w2_shuf"], gpu), p["sa2"], p["sw2"], p["sorted_ids"],
+       p["sorted_expert_ids"], p["sorted_weights"], p["num_valid_ids"], w.tokens, w.model_dim, w.inter_dim,
+       p["blocks"], valid_mask=mask)
+    torch.cuda.synchronize()
+    # masked slots contribute nothing: the oracle with their routing weight set to 0
+    tw = _np(p["topk_weights"]) * _np(mask).astype(np.float32)
+    ref = omoe.gemm2(_host(p["a2"]), _host(p["w2"]), _np(p["sa2"]), _np(p["sw2"]), _np(p["topk_ids"]), tw,
+                     w.model_dim, True, w.kind)
+    _check(out, ref, what="reduce masked")
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
+def test_moe_reduction_bit_exact(gpu, dt):
+    """y = sum over slots in fp32, in slot order, then one rounding: bit-exact against numpy."""
+    from flydsl_amd.kernels.moe_gemm_2stage import compile_moe_reduction
+    from oracle import numerics as on
+
+    T, k, D = 77, 6, 520
+    g = torch.Generator(device=gpu).manual_seed(8)
+    x = (torch.randn(T, k, D, generator=g, device=gpu) * 3).to(OUT_T[dt])
+    mask = (torch.rand(T, k, generator=g, device=gpu) > 0.25).to(torch.int8)
+    for use_mask in (False, True):
+        _say(f"reduction {dt} mask={use_mask}")
+        fn = compile_moe_reduction(topk=k, model_dim=D, dtype_str=dt, use_mask=use_mask)
+        y = torch.empty(T, D, dtype=OUT_T[dt], device=gpu)
+        fn(x.view(-1), y.view(-1), mask.view(-1) if use_mask else None, T)
+        torch.cuda.synchronize()
+        xs = x.float().cpu().numpy()
+        m = _np(mask).astype(bool) if use_mask else np.ones((T, k), bool)
+        acc = np.zeros((T, D), np.float32)
+        for s in range(k):
+            acc = np.where(m[:, s:s + 1], (acc + xs[:, s]).astype(np.float32), acc)
+        if dt == "f32":
+            assert np.array_equal(y.cpu().numpy(), acc)
+        elif dt == "f16":
+            assert np.array_equal(y.cpu().numpy(), acc.astype(np.float16))
+        else:
+            assert np.array_equal(H.bits16(y), on.bf16_rne(acc))

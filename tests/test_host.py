@@ -204,13 +204,22 @@ def test_moe_abi_rejects_bad_arguments_before_launch():
     assert s1(topk=0) != 0 and b"topk" in err()
     assert s1(tokens=1 << 24) != 0 and b"2^24" in err()
     assert s1(tokens=0) == 0 and s1(blocks=0) == 0                # nothing to do
-    rc = lib.flygemm_moe_gemm2(p, p, p, None, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, None, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 1, None)
     assert rc != 0 and b"null scale" in err()
-    rc = lib.flygemm_moe_gemm2(p, p, p, None, None, p, p, None, p, 64, 256, 128, 12, 4, 2, 16, 64, 3, 2, 1, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, None, None, p, p, None, p, 64, 256, 128, 12, 4, 2, 16, 64, 3, 2, 1, 1, None)
     assert rc != 0 and b"sorted_weights" in err()
+    # reduce mode (accumulate == 0) writes fp16/bf16 rows only
+    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 0, None)
+    assert rc != 0 and b"without accumulation" in err()
     # a per-expert weight slab above 2^31 bytes is refused
-    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 8, 65536, 65536, 12, 4, 2, 16, 256, 0, 2, 0, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 8, 65536, 65536, 12, 4, 2, 16, 256, 0, 2, 0, 1, None)
     assert rc != 0 and b"2^31" in err()
+    # the reduction
+    assert lib.flygemm_moe_reduce(p, p, None, 4, 2, 100, 1, None) != 0 and b"multiple of 8" in err()
+    assert lib.flygemm_moe_reduce(p, p, None, 4, 0, 128, 1, None) != 0 and b"invalid sizes" in err()
+    assert lib.flygemm_moe_reduce(p, p, None, 4, 2, 128, 7, None) != 0 and b"dtype" in err()
+    assert lib.flygemm_moe_reduce(ctypes.c_void_p(8), p, None, 4, 2, 128, 1, None) != 0 and b"misaligned" in err()
+    assert lib.flygemm_moe_reduce(p, p, None, 0, 2, 128, 1, None) == 0
 
 
 def test_moe_launchers_validate_like_reference():
@@ -228,8 +237,13 @@ def test_moe_launchers_validate_like_reference():
         compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype="bf16", group_size=32)
     with pytest.raises(ValueError):
         compile_moe_gemm2(**kw, doweight_stage2=True, out_dtype="f32", accumulate=False)
-    with pytest.raises(NotImplementedError):
-        compile_moe_gemm2(**kw, doweight_stage2=True, accumulate=False)
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex, compile_moe_reduction
+    assert compile_moe_gemm2_ex(**kw, doweight_stage2=True, mode=MoeGemm2Mode.REDUCE).mode == "reduce"
+    assert not compile_moe_gemm2(**kw, doweight_stage2=True, accumulate=False).accumulate
+    with pytest.raises(ValueError):
+        compile_moe_reduction(topk=2, model_dim=100)
+    with pytest.raises(ValueError):
+        compile_moe_reduction(topk=2, model_dim=128, dtype_str="fp8")
     fn = compile_moe_gemm2(**kw, doweight_stage2=True, out_dtype="float")
     assert fn.out_dtype == "f32"
     c = torch.empty(64 * 256, dtype=torch.float32)
