@@ -42,11 +42,16 @@ struct MoeArgs {
   int experts;
   int doweight;
   int blocks;                  // sorted blocks (size_expert_ids)
+  int nsplit;                  // column ranges per run (workgroups per run)
+  int out_mode;                // MoeOut
+  uint32_t out_bytes;          // size of out (buffer bounds of the epilogue stores)
 };
 
 // Stage-2 outputs: F16/BF16/F32 accumulate into out[token] with atomics; *_ROWS store each
 // route's row out[token*topk + slot] with plain stores (the reduce mode, summed by
 // moe_reduce_kernel afterwards).  Stage 1 takes F16 or BF16.
+typedef void (*MoeFn)(MoeArgs);
+
 enum MoeOut : int { MOE_OUT_F16 = 0, MOE_OUT_BF16 = 1, MOE_OUT_F32 = 2, MOE_OUT_F16_ROWS = 3, MOE_OUT_BF16_ROWS = 4 };
 constexpr bool moe_out_bf16(int o) { return o == MOE_OUT_BF16 || o == MOE_OUT_BF16_ROWS; }
 
@@ -57,81 +62,149 @@ __device__ __forceinline__ float silu_f(float x) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
-template <int STAGE, int KIND, int TM, int TN>
+// F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
+// bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
+// F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
+// bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
+template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32>
 struct MoeCfg {
-  static constexpr int NW = 4;
-  static constexpr int MR = TM / 16;                 // 16-row blocks (every wave covers all rows)
-  static constexpr int NR = TN / 64;                 // 16-column blocks per wave
-  static constexpr int NB = STAGE == 1 ? 2 : 1;      // weight halves: gate and up in stage 1
-  static constexpr int A_BYTES = TM * KT;
-  static constexpr int B_BYTES = NB * (TN / 16) * 2048;
-  static constexpr int A_DMA = A_BYTES / 1024;       // 1 KB DMA instructions per K tile
-  static constexpr int B_DMA = B_BYTES / 1024;
-  static constexpr int AQ = (A_DMA + NW - 1) / NW;   // A instructions per wave
-  static constexpr int STG = A_BYTES + B_BYTES;
-  static_assert(TM % 16 == 0 && TN % 64 == 0 && A_BYTES % 1024 == 0 && B_DMA % NW == 0, "tile shape");
-  static_assert(2 * STG <= 160 * 1024, "two stages must fit in LDS");
+  static constexpr int TME = TM * R;                  // rows of one run: up to R routing blocks
+  static constexpr int MR = TME / 16;                 // 16-row blocks (every wave covers all rows)
+  static constexpr int NR = TN / (16 * NW);           // 16-column blocks per wave and weight half
+  static constexpr int NB = STAGE == 1 ? 2 : 1;       // weight halves: gate and up in stage 1
+  static constexpr int A_BYTES = TME * KT;            // A part of one LDS slot
+  static constexpr int B_BYTES = NB * (TN / 16) * 2048;  // B part: NB x TN columns x 128 bytes
+  static constexpr int SLOT = A_BYTES + B_BYTES;
+  static constexpr int A_DMA = A_BYTES / 1024;        // 1 KB DMA instructions per K tile
+  static constexpr int AQ = (A_DMA + NW - 1) / NW;    // per wave
+  static constexpr int BQ = B_BYTES / 1024 / NW;      // per wave
+  static constexpr int ESZ = F32 ? 4 : 2;
+  // epilogue tile row: TN values, then 16 bytes holding the row's destination (the padding also
+  // spreads the rows over the LDS banks)
+  static constexpr int RS = TN * ESZ + 16;
+  static constexpr int CH = (SLOT / RS) / 16 * 16 < TME ? (SLOT / RS) / 16 * 16 : TME;  // rows per chunk
+  static constexpr int NCH = (TME + CH - 1) / CH;
+  static constexpr int CPR = TN * 2 / 16;             // 16-byte chunks per output row (plain stores)
+  static constexpr int NSTC = (CH * CPR + NW * 64 - 1) / (NW * 64);  // stores per thread per chunk
+  static constexpr int NST = NSTC * NCH;              // per thread per column tile
+  static_assert(TM % 16 == 0 && NR >= 1 && TN % (16 * NW) == 0 && A_BYTES % 1024 == 0, "tile shape");
+  static_assert(B_BYTES % (1024 * NW) == 0, "B DMA split over the waves");
+  static_assert(CH >= 16 && 2 * SLOT <= 160 * 1024, "LDS budget");
 };
 
-template <int STAGE, int KIND, int TM, int TN, int OUT>
-__global__ void __launch_bounds__(256) moe_gemm_kernel(MoeArgs p) {
-  using C = MoeCfg<STAGE, KIND, TM, TN>;
-  constexpr int NW = C::NW, MR = C::MR, NR = C::NR, NB = C::NB;
+// One workgroup (NW waves) per (run, column range): a run is up to R consecutive routing blocks of
+// one expert (a block starts a run when its index is a multiple of R or its expert differs from
+// the previous block's), so the weight tile of each K step serves up to R*TM rows; the
+// workgroup then walks its column tiles and K tiles as one pipeline.
+//   Each K step: A (the gathered rows) and B (the expert's preshuffled weight rows of the column
+//   tile, gate and up in stage 1) go global -> LDS by DMA into a 2-slot ring, one step ahead.
+//   Wave w owns columns [w*TN/NW, (w+1)*TN/NW) of the tile, for all rows.
+//   Epilogue at the end of each column tile, through the slot the last step computed from, in
+//   chunks of CH rows: scaled values into an LDS tile, then row-contiguous 16-byte stores (stage
+//   1, per-route rows) or 4-byte atomics.
+template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32>
+__global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
+  using C = MoeCfg<STAGE, KIND, TM, R, TN, NW, F32>;
+  static_assert(STAGE == 2 || !F32, "stage 1 writes 2-byte outputs");
   static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "MoE input kinds");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][C::STG];
+  constexpr int MR = C::MR, NR = C::NR, NB = C::NB, TME = C::TME, NT = NW * 64;
+  const int mode = p.out_mode;
+  const bool rows = STAGE == 1 || mode == MOE_OUT_F16_ROWS || mode == MOE_OUT_BF16_ROWS;
+  const bool obf16 = moe_out_bf16(mode);
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * C::SLOT];
 
-  // Workgroups are dealt to the 8 XCDs round-robin.  Logical tile L (column tile fastest, then
-  // sorted block) runs as workgroup (L % chunk) * 8 + L / chunk, i.e. each XCD takes one
-  // contiguous range of L, so the consecutive blocks of one expert share that XCD's L2 copy of
-  // the expert's weights instead of each XCD fetching them.  The grid has at least 8 * chunk
-  // workgroups.
-  // Only the tiles of blocks below num_valid_ids are dealt out, so a short routing (decode)
-  // still spreads over every XCD.
+  // ---- which run and which column tiles ----
+  // Logical id L = block * nsplit + split over the blocks below num_valid_ids, dealt to the 8
+  // XCDs in contiguous ranges (workgroup (L % chunk) * 8 + L / chunk; XCDs take workgroups
+  // round-robin), so consecutive runs of one expert share an XCD's L2 copy of its weights.
   const int nv = p.num_valid[0];
-  const int ntn = p.N / TN;
-  const int V = ntn * min((nv + TM - 1) / TM, p.blocks);
+  const int nbv = min((nv + TM - 1) / TM, p.blocks);
+  const int V = nbv * p.nsplit;
   const int chunk = (V + 7) >> 3;
   const int L = (blockIdx.x & 7) * chunk + (blockIdx.x >> 3);
   if ((int)(blockIdx.x >> 3) >= chunk || L >= V) return;
-  const int by = L / ntn;
-  const int n0 = (L - by * ntn) * TN;
-  const int e = p.expert_ids[by];
+  const int b0 = L / p.nsplit;
+  const int split = L - b0 * p.nsplit;
+  const int e = p.expert_ids[b0];
   if (e < 0 || e >= p.experts) return;
+  if (R > 1 && b0 % R != 0 && p.expert_ids[b0 - 1] == e) return;   // inside another run
+  int nblk = 1;
+  if constexpr (R > 1) {
+    const int lim = min((b0 / R + 1) * R, nbv);
+    while (b0 + nblk < lim && p.expert_ids[b0 + nblk] == e) ++nblk;
+  }
+  const int rows_valid = nblk * TM;
+  const int ntn = p.N / TN;
+  const int j0 = split * ntn / p.nsplit, j1 = (split + 1) * ntn / p.nsplit;
+  if (j0 >= j1) return;
   const int K = p.K;
   const int nk = K / KT;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
   const int a_rows = STAGE == 1 ? p.tokens : p.tokens * p.topk;
+  constexpr bool kScaled = !kind_is_16bit(KIND);
 
+  // ---- per-row facts, fixed for the workgroup's life ----
+  // Every load below is unconditional (indices clamped into range, the result masked after), so
+  // they all go out before the first wait.
   // A gather: DMA instruction q fills tile rows 8q .. 8q+7; lane l brings the chunk that
-  // belongs in slot l%8 of row 8q + l/8.  Padding entries (token >= tokens) read zeros.
+  // belongs in slot l%8 of row 8q + l/8.  Padding rows read zeros (offset past the buffer).
   uint32_t va[C::AQ];
+  int ida[C::AQ], idr[MR];
+#pragma unroll
+  for (int j = 0; j < C::AQ; ++j)
+    ida[j] = p.sorted_ids[b0 * TM + min(min((wave + j * NW) * 8 + (lane >> 3), TME - 1), rows_valid - 1)];
+#pragma unroll
+  for (int mi = 0; mi < MR; ++mi) idr[mi] = p.sorted_ids[b0 * TM + min(mi * 16 + l16, rows_valid - 1)];
 #pragma unroll
   for (int j = 0; j < C::AQ; ++j) {
-    const int rloc = min((wave + j * NW) * 8 + (lane >> 3), TM - 1);
-    const int id = p.sorted_ids[by * TM + rloc];
+    const int rloc = min((wave + j * NW) * 8 + (lane >> 3), TME - 1);
+    const int id = ida[j];
     const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+    const bool ok = rloc < rows_valid && t < p.tokens && s < p.topk;
     const int row = STAGE == 1 ? t : t * p.topk + s;
     const int c = (lane & 7) ^ ((rloc >> 1) & 7);
-    va[j] = (t < p.tokens && s < p.topk) ? (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
+    va[j] = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
   }
+  // this lane's rows mi*16 + l16: scale, routing weight, destination row (-1: padding)
+  float sx_r[MR], rw_r[MR];
+  int dst_r[MR];
+#pragma unroll
+  for (int mi = 0; mi < MR; ++mi) {
+    const int r = mi * 16 + l16;
+    const int id = idr[mi];
+    const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+    const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
+    dst_r[mi] = !ok ? -1 : (rows ? t * p.topk + s : t);
+    const int arow = ok ? (STAGE == 1 ? t : t * p.topk + s) : 0;
+    const float sxv = kScaled ? p.sa[arow] : 1.f;
+    const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
+    sx_r[mi] = ok ? sxv : 0.f;
+    rw_r[mi] = ok ? rwv : 0.f;
+  }
+
   const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
   // this expert's weight rows only (the whole array may exceed 32-bit offsets)
   const int wrows = STAGE == 1 ? 2 * p.N : p.N;
   const sgpr4 rsrc_w = buf_desc(p.w + (size_t)e * (size_t)wrows * (size_t)K, (uint32_t)wrows * (uint32_t)K);
   const uint32_t vb = (uint32_t)lane * 16u;
 
-  auto issue = [&](uint8_t* st, int kt) {
+  // DMA of step (column tile jt, K tile kt) into ring slot `slot`: A rows, then the B blocks
+  // (local 16-column block lb: gate -- or W2 -- for lb < TN/16, up after), each 2 KB per K tile
+  // in the preshuffled layout, copied verbatim.
+  auto issue = [&](int jt, int kt, int slot) {
+    uint8_t* st = ring + slot * C::SLOT;
 #pragma unroll
     for (int j = 0; j < C::AQ; ++j) {
       const int q = wave + j * NW;
       if (q < C::A_DMA) dma16(rsrc_a, st + q * 1024, va[j], (uint32_t)kt * KT);
     }
+    const int n0 = jt * TN;
 #pragma unroll
-    for (int j = 0; j < C::B_DMA / NW; ++j) {
-      const int q = wave + j * NW;           // 1 KB piece q: local 16-row block q/2, half q%2
-      const int lb = q >> 1;                 // blocks [0, TN/16): gate (or W2); then up
+    for (int j = 0; j < C::BQ; ++j) {
+      const int q = wave + j * NW;           // 1 KB piece q: local block q/2, half q%2
+      const int lb = q >> 1;
       const int nb = lb < TN / 16 ? n0 / 16 + lb : (p.N + n0) / 16 + (lb - TN / 16);
       const uint32_t so = (uint32_t)nb * 16u * (uint32_t)K + (uint32_t)kt * 2048u + (uint32_t)(q & 1) * 1024u;
       dma16(rsrc_w, st + C::A_BYTES + q * 1024, vb, __builtin_amdgcn_readfirstlane(so));
@@ -140,145 +213,168 @@ __global__ void __launch_bounds__(256) moe_gemm_kernel(MoeArgs p) {
 
   typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
   AccT acc[NB][MR][NR];
-#pragma unroll
-  for (int h = 0; h < NB; ++h)
-#pragma unroll
-    for (int i = 0; i < MR; ++i)
-#pragma unroll
-      for (int j = 0; j < NR; ++j) acc[h][i][j] = AccT{0, 0, 0, 0};
 
-  // One K tile: the A fragments of every row block are read once, then each weight fragment
-  // is read and applied to all of them.  B is the MFMA's first operand, so each accumulator
-  // tile holds its 16x16 block of the output transposed.
+  // One K tile: this wave's B fragments read once, then row block by row block, the next row's
+  // A fragment read ahead of this row's MFMAs.  B is the MFMA's first operand, so each
+  // accumulator tile holds its 16x16 output block transposed.
   auto compute = [&](const uint8_t* sA) {
     const uint8_t* sB = sA + C::A_BYTES;
-    i32x4 alo[MR], ahi[MR];
-#pragma unroll
-    for (int mi = 0; mi < MR; ++mi) {
+    auto load_a = [&](int mi, i32x4& lo, i32x4& hi) {
       const int row = mi * 16 + l16;
       const int sw = (row >> 1) & 7;
-      alo[mi] = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
-      ahi[mi] = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
-    }
+      lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
+      hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
+    };
+    i32x4 bl[NB][NR], bh[NB][NR];
 #pragma unroll
     for (int h = 0; h < NB; ++h)
 #pragma unroll
       for (int ni = 0; ni < NR; ++ni) {
         const int off = (h * (TN / 16) + wave * NR + ni) * 2048 + lq * 256 + l16 * 16;
-        const i32x4 blo = *(const i32x4*)(sB + off);
-        const i32x4 bhi = *(const i32x4*)(sB + off + 1024);
-        if constexpr (KIND == KIND_FP8) {
-          const i32x8 bf = i32x8{blo.x, blo.y, blo.z, blo.w, bhi.x, bhi.y, bhi.z, bhi.w};
-#pragma unroll
-          for (int mi = 0; mi < MR; ++mi)
-            acc[h][mi][ni] = mfma_fp8(bf, i32x8{alo[mi].x, alo[mi].y, alo[mi].z, alo[mi].w, ahi[mi].x, ahi[mi].y,
-                                                ahi[mi].z, ahi[mi].w},
-                                      acc[h][mi][ni]);
-        } else {
-#pragma unroll
-          for (int mi = 0; mi < MR; ++mi) acc[h][mi][ni] = mfma_k64<KIND>(blo, alo[mi], acc[h][mi][ni]);
-#pragma unroll
-          for (int mi = 0; mi < MR; ++mi) acc[h][mi][ni] = mfma_k64<KIND>(bhi, ahi[mi], acc[h][mi][ni]);
-        }
+        bl[h][ni] = *(const i32x4*)(sB + off);
+        bh[h][ni] = *(const i32x4*)(sB + off + 1024);
       }
+    i32x4 alo, ahi;
+    load_a(0, alo, ahi);
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) {
+      const i32x4 lo = alo, hi = ahi;
+      if (mi + 1 < MR) load_a(mi + 1, alo, ahi);
+#pragma unroll
+      for (int h = 0; h < NB; ++h)
+#pragma unroll
+        for (int ni = 0; ni < NR; ++ni) {
+          if constexpr (KIND == KIND_FP8) {
+            acc[h][mi][ni] = mfma_fp8(__builtin_shufflevector(bl[h][ni], bh[h][ni], 0, 1, 2, 3, 4, 5, 6, 7),
+                                      __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[h][mi][ni]);
+          } else {
+            acc[h][mi][ni] = mfma_k64<KIND>(bl[h][ni], lo, acc[h][mi][ni]);
+            acc[h][mi][ni] = mfma_k64<KIND>(bh[h][ni], hi, acc[h][mi][ni]);
+          }
+        }
+    }
   };
 
-  issue(lds[0], 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_dma();
-    workgroup_barrier();  // tile kt has landed; every wave is done reading the other stage
-    if (kt + 1 < nk) issue(lds[(kt + 1) & 1], kt + 1);
-    compute(lds[kt & 1]);
-  }
+  auto col_scale = [&](int jt, int h, int ni) -> f32x4 {
+    const int n = jt * TN + (wave * NR + ni) * 16 + lq * 4;
+    return kScaled ? *(const f32x4*)(p.sw + (size_t)e * wrows + (h ? p.N : 0) + n) : f32x4{1.f, 1.f, 1.f, 1.f};
+  };
 
-  // ---- epilogue, through LDS so that global writes are row-contiguous ----
-  // Phase 1: lane (l16, lq) holds row mi*16 + l16 of the block and columns 4*lq .. 4*lq+3 of
-  // each 16-column block; it scales them and writes them to an LDS tile [TM][TN] (padded rows).
-  // Phase 2: the workgroup walks the tile row by row, each wave instruction covering 256
-  // contiguous bytes of one output row: 16-byte stores (stage 1) or 4-byte atomics (stage 2;
-  // fp16/bf16 as packed pairs).  Scattered 4-lane fragments would touch 16 cache lines per
-  // instruction, which costs the atomics 8x their useful rate.
-  constexpr bool kScaled = !kind_is_16bit(KIND);
-  constexpr bool kRows = STAGE == 1 || OUT == MOE_OUT_F16_ROWS || OUT == MOE_OUT_BF16_ROWS;  // plain stores
-  constexpr int ESZ = (STAGE == 2 && OUT == MOE_OUT_F32) ? 4 : 2;
-  constexpr int RS = TN * ESZ + 16;            // LDS bytes per tile row (padding spreads banks)
-  static_assert(TM * RS + TM * 4 <= 2 * C::STG, "output tile fits in the stage buffers");
-  uint8_t* ot = &lds[0][0];
-  int32_t* rowdst = (int32_t*)(ot + TM * RS);  // destination row per tile row, -1 for padding
-  workgroup_barrier();                         // every wave is done with the last K tile
+  // Epilogue of column tile jt in the LDS slot `ot` (free once every wave is past the barrier
+  // below), CH rows at a time.  Phase 1: lane (l16, lq) holds row mi*16 + l16, columns
+  // 4*lq .. 4*lq+3 of each of its 16-column blocks; scaled, into the chunk tile.  Phase 2:
+  // row-contiguous writes, each wave instruction covering 256 contiguous bytes of output.
+  // Row stores are buffer stores, exactly NST per thread (padding rows get an offset past the
+  // buffer), so a later wait can leave them in flight.
+  const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
+  // column scales of the current tile, loaded at its first step ahead of that step's DMA (so
+  // the next step's wait covers them and the epilogue waits for nothing)
+  f32x4 sc[NB][NR];
+  auto epilogue = [&](int jt, uint8_t* ot) {
+    const int n0 = jt * TN;
+    workgroup_barrier();  // every wave is done computing from the slot
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) {
-    const int r = mi * 16 + l16;
-    const int i = by * TM + r;
-    const int id = p.sorted_ids[i];
-    const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
-    const bool valid = t < p.tokens && s < p.topk;
-    if (wave == 0 && lq == 0) rowdst[r] = !valid ? -1 : (kRows ? t * p.topk + s : t);
-    const int arow = STAGE == 1 ? t : t * p.topk + s;
-    const float sx = kScaled && valid ? p.sa[arow] : 1.f;
-    const float rw = p.doweight && valid ? p.sorted_w[i] : 1.f;
+    for (int ch = 0; ch < C::NCH; ++ch) {
+      if (ch > 0) workgroup_barrier();  // the previous chunk's rows have been read out
 #pragma unroll
-    for (int ni = 0; ni < NR; ++ni) {
-      const int c = (wave * NR + ni) * 16 + lq * 4;
-      const int n = n0 + c;
-      float v[4];
-      if constexpr (STAGE == 1) {
-        f32x4 swg = f32x4{1.f, 1.f, 1.f, 1.f}, swu = swg;
-        if constexpr (kScaled) {
-          swg = *(const f32x4*)(p.sw + (size_t)e * 2 * p.N + n);
-          swu = *(const f32x4*)(p.sw + (size_t)e * 2 * p.N + p.N + n);
-        }
+      for (int mi = ch * C::CH / 16; mi < min((ch + 1) * C::CH / 16, MR); ++mi) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int r = mi * 16 + l16 - ch * C::CH;
+        if (wave == 0 && lq == 0) *(int*)(ot + r * C::RS + TN * C::ESZ) = dst_r[mi];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float g = ((float)acc[0][mi][ni][q] * sx) * swg[q];
-          const float u = ((float)acc[1][mi][ni][q] * sx) * swu[q];
-          v[q] = silu_f(g) * u;
-          if (p.doweight) v[q] *= rw;
-        }
-      } else {
-        f32x4 swd = f32x4{1.f, 1.f, 1.f, 1.f};
-        if constexpr (kScaled) swd = *(const f32x4*)(p.sw + (size_t)e * p.N + n);
+        for (int ni = 0; ni < NR; ++ni) {
+          const int c = (wave * NR + ni) * 16 + lq * 4;
+          float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          v[q] = ((float)acc[0][mi][ni][q] * sx) * swd[q];
-          if (p.doweight) v[q] *= rw;
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (STAGE == 1) {
+              const float g = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
+              const float u = ((float)acc[1][mi][ni][q] * sx_r[mi]) * sc[1][ni][q];
+              v[q] = silu_f(g) * u;
+            } else {
+              v[q] = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
+            }
+            if (p.doweight) v[q] *= rw_r[mi];
+          }
+          uint8_t* dst = ot + r * C::RS + c * C::ESZ;
+          if constexpr (C::ESZ == 4)
+            *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+          else
+            *(i32x2*)dst = obf16 ? pack_out4<true>(v) : pack_out4<false>(v);
         }
       }
-      uint8_t* dst = ot + r * RS + c * ESZ;
-      if constexpr (ESZ == 4)
-        *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+      workgroup_barrier();
+      const int nrows = min(C::CH, TME - ch * C::CH);
+      if (!F32 && rows) {
+#pragma unroll
+        for (int it = 0; it < C::NSTC; ++it) {
+          const int idx0 = it * NT + tid;
+          const int idx = min(idx0, nrows * C::CPR - 1);
+          const int r = idx / C::CPR, cc = idx - r * C::CPR;
+          const int d = idx0 < nrows * C::CPR ? *(const int*)(ot + r * C::RS + TN * C::ESZ) : -1;
+          const i32x4 val = *(const i32x4*)(ot + r * C::RS + cc * 16);
+          const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)n0) * 2u + cc * 16u;
+          __builtin_amdgcn_raw_buffer_store_b128(val, rsrc_o, off, 0, 0);
+        }
+      } else {
+        constexpr int WPR = TN * C::ESZ / 4;    // 4-byte words per output row
+        for (int idx = tid; idx < nrows * WPR; idx += NT) {
+          const int r = idx / WPR, wd = idx - r * WPR;
+          const int d = *(const int*)(ot + r * C::RS + TN * C::ESZ);
+          if (d < 0) continue;
+          uint8_t* dst = (uint8_t*)p.out + ((size_t)d * p.N + n0) * C::ESZ + wd * 4;
+          const uint8_t* src = ot + r * C::RS + wd * 4;
+          if constexpr (F32) {
+            unsafeAtomicAdd((float*)dst, *(const float*)src);
+          } else if (obf16) {
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            __builtin_amdgcn_global_atomic_fadd_v2bf16((bf16x2*)dst, *(const bf16x2*)src);
+          } else {
+            typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+            __builtin_amdgcn_global_atomic_fadd_v2f16((f16x2*)dst, *(const f16x2*)src);
+          }
+        }
+      }
+    }
+  };
+
+  // ---- the pipeline over (column tile, K tile) steps ----
+  // Each step waits for its slot's DMA (issued one step earlier), publishes the slot with the
+  // barrier, issues the next step's DMA into the other slot -- the next K tile, or the first of
+  // the next column tile -- and computes.  The epilogue's row stores go out after that DMA, so
+  // the next step's wait leaves them in flight (vector memory operations retire in issue order).
+  int slot = 0;
+  bool keep_stores = false;
+  issue(j0, 0, 0);
+  for (int jt = j0; jt < j1; ++jt) {
+#pragma unroll
+    for (int h = 0; h < NB; ++h)
+#pragma unroll
+      for (int i = 0; i < MR; ++i)
+#pragma unroll
+        for (int j = 0; j < NR; ++j) acc[h][i][j] = AccT{0, 0, 0, 0};
+    for (int kt = 0; kt < nk; ++kt) {
+      if (keep_stores)
+        wait_vmem_leaving<C::NST>();
       else
-        *(i32x2*)dst = pack_out4<moe_out_bf16(OUT)>(v);
-    }
-  }
-  workgroup_barrier();
-  if constexpr (kRows) {
-    constexpr int CPR = TN * 2 / 16;           // 16-byte chunks per output row
-    for (int idx = tid; idx < TM * CPR; idx += 256) {
-      const int r = idx / CPR, cc = idx - r * CPR;
-      const int d = rowdst[r];
-      if (d < 0) continue;
-      const i32x4 val = *(const i32x4*)(ot + r * RS + cc * 16);
-      *(i32x4*)((uint8_t*)p.out + ((size_t)d * p.N + n0) * 2 + cc * 16) = val;
-    }
-  } else {
-    constexpr int WPR = TN * ESZ / 4;          // 4-byte words per output row
-    for (int idx = tid; idx < TM * WPR; idx += 256) {
-      const int r = idx / WPR, wd = idx - r * WPR;
-      const int d = rowdst[r];
-      if (d < 0) continue;
-      uint8_t* dst = (uint8_t*)p.out + ((size_t)d * p.N + n0) * ESZ + wd * 4;
-      const uint8_t* src = ot + r * RS + wd * 4;
-      if constexpr (OUT == MOE_OUT_F32) {
-        unsafeAtomicAdd((float*)dst, *(const float*)src);
-      } else if constexpr (OUT == MOE_OUT_BF16) {
-        typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-        __builtin_amdgcn_global_atomic_fadd_v2bf16((bf16x2*)dst, *(const bf16x2*)src);
-      } else {
-        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-        __builtin_amdgcn_global_atomic_fadd_v2f16((f16x2*)dst, *(const f16x2*)src);
+        wait_dma();
+      keep_stores = false;
+      workgroup_barrier();
+      if (kt == 0) {
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+          for (int ni = 0; ni < NR; ++ni) sc[h][ni] = col_scale(jt, h, ni);
       }
+      if (kt + 1 < nk)
+        issue(jt, kt + 1, slot ^ 1);
+      else if (jt + 1 < j1)
+        issue(jt + 1, 0, slot ^ 1);
+      compute(ring + slot * C::SLOT);
+      slot ^= 1;
     }
+    epilogue(jt, ring + (slot ^ 1) * C::SLOT);
+    keep_stores = rows;
   }
 }
 

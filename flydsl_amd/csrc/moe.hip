@@ -9,35 +9,48 @@
 
 using namespace flygemm;
 
+// Kernel tables, one per stage (stage 2 lives in moe_stage2.hip, compiled in parallel).
+// Instantiated tiles: runs of one routing block (R = 1, 4 waves) for every (tile_m, tile_n);
+// runs of 128 rows (stage 1) or 256 rows (stage 2) with 256-column tiles and 8 waves.
+namespace flygemm {
+MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32);
+}
+
 namespace {
 
-typedef void (*MoeFn)(MoeArgs);
-
-template <int STAGE, int KIND, int OUT>
-MoeFn moe_tile(int tm, int tn) {
-#define T(M_, N_) \
-  if (tm == M_ && tn == N_) return moe_gemm_kernel<STAGE, KIND, M_, N_, OUT>;
-  T(16, 64) T(16, 128) T(16, 256) T(32, 64) T(32, 128) T(32, 256) T(64, 64) T(64, 128) T(64, 256)
+template <int KIND>
+MoeFn moe_stage1_tile(int tm, int r, int tn) {
+#define T(M_, R_, N_, W_) \
+  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, W_, false>;
+  T(16, 1, 64, 4) T(16, 1, 128, 4) T(16, 1, 256, 4) T(32, 1, 64, 4) T(32, 1, 128, 4) T(32, 1, 256, 4)
+  T(64, 1, 64, 4) T(64, 1, 128, 4) T(64, 1, 256, 4)
+  T(16, 8, 256, 8) T(32, 4, 256, 8) T(64, 2, 256, 8)
 #undef T
   return nullptr;
 }
 
-template <int STAGE, int OUT>
-MoeFn moe_kind(int kind, int tm, int tn) {
+MoeFn moe_stage1_kernel(int kind, int tm, int r, int tn) {
   switch (kind) {
-    case KIND_FP8: return moe_tile<STAGE, KIND_FP8, OUT>(tm, tn);
-    case KIND_INT8: return moe_tile<STAGE, KIND_INT8, OUT>(tm, tn);
-    case KIND_BF16: return moe_tile<STAGE, KIND_BF16, OUT>(tm, tn);
-    case KIND_F16: return moe_tile<STAGE, KIND_F16, OUT>(tm, tn);
+    case KIND_FP8: return moe_stage1_tile<KIND_FP8>(tm, r, tn);
+    case KIND_INT8: return moe_stage1_tile<KIND_INT8>(tm, r, tn);
+    case KIND_BF16: return moe_stage1_tile<KIND_BF16>(tm, r, tn);
+    case KIND_F16: return moe_stage1_tile<KIND_F16>(tm, r, tn);
     default: return nullptr;
   }
 }
 
+// Estimated runs (workgroups before column splitting): routing blocks grouped R at a time, plus
+// one partial run per expert that has routes.
+long est_runs(int tokens, int topk, int experts, int tm, int r) {
+  const long routes = (long)tokens * topk;
+  return routes / ((long)tm * r) + (routes < experts ? routes : experts);
+}
+
 // Column tile when the caller leaves it open (tile_n <= 0): the widest of 256/128/64 that
-// divides N and still gives every sorted block at least two column tiles.
-int pick_tile_n(int N) {
+// divides N and still gives about two workgroups per CU.
+int pick_tile_n(int N, long runs) {
   for (int tn : {256, 128})
-    if (N % tn == 0 && N / tn >= 2) return tn;
+    if (N % tn == 0 && runs * (N / tn) >= 512) return tn;
   return 64;
 }
 
@@ -53,7 +66,17 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (tokens >= (1 << 24)) return fail(hipErrorInvalidValue, "%s: tokens=%d must be below 2^24", what, tokens);
   if (tile_m != 16 && tile_m != 32 && tile_m != 64)
     return fail(hipErrorInvalidValue, "%s: tile_m=%d must be 16, 32 or 64", what, tile_m);
-  if (tile_n <= 0) tile_n = pick_tile_n(N);
+  // Runs of several routing blocks when experts hold two or more blocks on average: 128 rows
+  // (stage 1, gate and up) or 256 rows (stage 2) per workgroup of 8 waves, with 256-column
+  // tiles.  The caller's tile_n is then overridden: tiling does not change the results.
+  const long routes = (long)tokens * topk;
+  int R = 1;
+  if (routes >= 2L * tile_m * experts && N % 256 == 0 && tile_n != 64 &&
+      (tile_n <= 0 || tile_n == 128 || tile_n == 256)) {
+    R = (stage == 1 ? 128 : 256) / tile_m;
+    tile_n = 256;
+  }
+  if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
   if (tile_n != 64 && tile_n != 128 && tile_n != 256)
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
   if (N % tile_n != 0) return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
@@ -86,28 +109,29 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (!is16 && (!sa || !sw)) return fail(hipErrorInvalidValue, "%s: null scale pointer", what);
   if (doweight && !sorted_w) return fail(hipErrorInvalidValue, "%s: null sorted_weights with doweight", what);
 
-  MoeFn fn = nullptr;
-  if (stage == 1)
-    fn = mout == MOE_OUT_BF16 ? moe_kind<1, MOE_OUT_BF16>(kind, tile_m, tile_n) : moe_kind<1, MOE_OUT_F16>(kind, tile_m, tile_n);
-  else if (mout == MOE_OUT_F32)
-    fn = moe_kind<2, MOE_OUT_F32>(kind, tile_m, tile_n);
-  else if (mout == MOE_OUT_F16_ROWS)
-    fn = moe_kind<2, MOE_OUT_F16_ROWS>(kind, tile_m, tile_n);
-  else if (mout == MOE_OUT_BF16_ROWS)
-    fn = moe_kind<2, MOE_OUT_BF16_ROWS>(kind, tile_m, tile_n);
-  else
-    fn = mout == MOE_OUT_BF16 ? moe_kind<2, MOE_OUT_BF16>(kind, tile_m, tile_n) : moe_kind<2, MOE_OUT_F16>(kind, tile_m, tile_n);
-  if (!fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d", what, tile_m, tile_n);
+  const long out_bytes = (stage == 1 || !accumulate) ? (long)tokens * topk * N * 2
+                                                     : (long)tokens * N * (mout == MOE_OUT_F32 ? 4 : 2);
+  if (out_bytes > 0xFFFFFF00L) return fail(hipErrorInvalidValue, "%s: output above 4 GB", what);
 
+  MoeFn fn = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n)
+                        : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32);
+  if (!fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
+
+  // column ranges per run: about 1024 workgroups in all
+  const long ntn = N / tile_n;
+  const long runs = est_runs(tokens, topk, experts, tile_m, R);
+  long nsplit = (1024 + runs - 1) / runs;
+  nsplit = nsplit < 1 ? 1 : (nsplit > ntn ? ntn : nsplit);
   MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
                sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
-               doweight ? 1 : 0, blocks};
-  // grid (N / tile_n, blocks) in the reference; here one dimension, rounded up to a multiple of
-  // 8 for the kernel's XCD-aware order (the extra workgroups exit at once)
-  const long ntn = N / tile_n;
-  const long g = (ntn * blocks + 7) / 8 * 8;
+               doweight ? 1 : 0, blocks, (int)nsplit, mout, (uint32_t)out_bytes};
+  // grid (N / tile_n, blocks) in the reference; here one dimension over (block, column range),
+  // rounded up to a multiple of 8 for the kernel's XCD-aware order (the extra workgroups and
+  // those that do not start a run exit at once)
+  const long g = (nsplit * blocks + 7) / 8 * 8;
   if (g >= (1L << 31)) return fail(hipErrorInvalidValue, "%s: grid too large", what);
-  hipLaunchKernelGGL(fn, dim3((unsigned)g), dim3(256), 0, stream, args);
+  // the run kernels (R > 1) have 8 waves, the others 4
+  hipLaunchKernelGGL(fn, dim3((unsigned)g), dim3(R > 1 ? 512 : 256), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of %s failed: %s", what, hipGetErrorString(e));
   return 0;

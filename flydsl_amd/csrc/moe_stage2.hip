@@ -1,0 +1,37 @@
+// Kernel table of MoE stage 2 (the down projection), in a translation unit of its own so the
+// library's sources compile in parallel.  Tiles as listed with the stage-1 table in moe.hip.
+#include <hip/hip_runtime.h>
+
+#include "moe.h"
+
+namespace flygemm {
+
+namespace {
+template <int KIND, bool F32>
+MoeFn stage2_tile(int tm, int r, int tn) {
+#define T(M_, R_, N_, W_) \
+  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, W_, F32>;
+  T(16, 1, 64, 4) T(16, 1, 128, 4) T(16, 1, 256, 4) T(32, 1, 64, 4) T(32, 1, 128, 4) T(32, 1, 256, 4)
+  T(64, 1, 64, 4) T(64, 1, 128, 4) T(64, 1, 256, 4)
+  T(16, 16, 256, 8) T(32, 8, 256, 8) T(64, 4, 256, 8)
+#undef T
+  return nullptr;
+}
+
+template <int KIND>
+MoeFn stage2_kind(int tm, int r, int tn, bool f32) {
+  return f32 ? stage2_tile<KIND, true>(tm, r, tn) : stage2_tile<KIND, false>(tm, r, tn);
+}
+}  // namespace
+
+MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32) {
+  switch (kind) {
+    case KIND_FP8: return stage2_kind<KIND_FP8>(tm, r, tn, f32);
+    case KIND_INT8: return stage2_kind<KIND_INT8>(tm, r, tn, f32);
+    case KIND_BF16: return stage2_kind<KIND_BF16>(tm, r, tn, f32);
+    case KIND_F16: return stage2_kind<KIND_F16>(tm, r, tn, f32);
+    default: return nullptr;
+  }
+}
+
+}  // namespace flygemm

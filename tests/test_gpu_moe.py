@@ -328,3 +328,19 @@ def test_moe_reduction_bit_exact(gpu, dt):
             assert np.array_equal(y.cpu().numpy(), acc.astype(np.float16))
         else:
             assert np.array_equal(H.bits16(y), on.bf16_rne(acc))
+
+
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+@pytest.mark.parametrize("kind,tile_n", [("fp8", 128), ("fp8", 256), ("int8", 256), ("bf16", 128)])
+def test_runs_of_blocks(gpu, tile_m, kind, tile_n):
+    """Experts holding many routing blocks: the kernels group up to 128 rows of one expert per
+    workgroup (the grouping ends at expert boundaries and at multiples of 128 / tile_m blocks)."""
+    w = W.moe_custom(600, 512, 256, 5, 2, tile_m, tile_n, tile_n, kind, seed=tile_m * 7 + tile_n)
+    p = W.moe_problem(w, gpu)
+    rows = np.unique(np.r_[np.arange(0, 600, 7), 599])
+    _say(f"runs {kind} tile {tile_m}x{tile_n}")
+    o1 = run_stage1(p, gpu, "f16", doweight=True)
+    o2 = run_stage2(p, gpu, "bf16", doweight=False)
+    torch.cuda.synchronize()
+    _check(o1, ref_stage1(p, True, rows), rows, what=f"runs stage1 {tile_m}x{tile_n}")
+    _check(o2, ref_stage2(p, False, rows), rows, what=f"runs stage2 {tile_m}x{tile_n}")
