@@ -84,9 +84,7 @@ struct MoeCfg {
   static constexpr int RS = TN * ESZ + 16;
   static constexpr int CH = (SLOT / RS) / 16 * 16 < TME ? (SLOT / RS) / 16 * 16 : TME;  // rows per chunk
   static constexpr int NCH = (TME + CH - 1) / CH;
-  static constexpr int CPR = TN * 2 / 16;             // 16-byte chunks per output row (plain stores)
-  static constexpr int NSTC = (CH * CPR + NW * 64 - 1) / (NW * 64);  // stores per thread per chunk
-  static constexpr int NST = NSTC * NCH;              // per thread per column tile
+  static constexpr int NST = MR * NR;                 // direct row stores per thread per column tile
   static_assert(TM % 16 == 0 && NR >= 1 && TN % (16 * NW) == 0 && A_BYTES % 1024 == 0, "tile shape");
   static_assert(B_BYTES % (1024 * NW) == 0, "B DMA split over the waves");
   static_assert(CH >= 16 && 2 * SLOT <= 160 * 1024, "LDS budget");
@@ -99,9 +97,9 @@ struct MoeCfg {
 //   Each K step: A (the gathered rows) and B (the expert's preshuffled weight rows of the column
 //   tile, gate and up in stage 1) go global -> LDS by DMA into a 2-slot ring, one step ahead.
 //   Wave w owns columns [w*TN/NW, (w+1)*TN/NW) of the tile, for all rows.
-//   Epilogue at the end of each column tile, through the slot the last step computed from, in
-//   chunks of CH rows: scaled values into an LDS tile, then row-contiguous 16-byte stores (stage
-//   1, per-route rows) or 4-byte atomics.
+//   Epilogue at the end of each column tile: row outputs (stage 1, reduce mode) are stored
+//   straight from the accumulators; atomic accumulation goes through the slot the last step
+//   computed from, in chunks of CH rows, so each wave instruction adds 256 contiguous bytes.
 template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32>
 __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   using C = MoeCfg<STAGE, KIND, TM, R, TN, NW, F32>;
@@ -260,18 +258,47 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
     return kScaled ? *(const f32x4*)(p.sw + (size_t)e * wrows + (h ? p.N : 0) + n) : f32x4{1.f, 1.f, 1.f, 1.f};
   };
 
-  // Epilogue of column tile jt in the LDS slot `ot` (free once every wave is past the barrier
-  // below), CH rows at a time.  Phase 1: lane (l16, lq) holds row mi*16 + l16, columns
-  // 4*lq .. 4*lq+3 of each of its 16-column blocks; scaled, into the chunk tile.  Phase 2:
-  // row-contiguous writes, each wave instruction covering 256 contiguous bytes of output.
-  // Row stores are buffer stores, exactly NST per thread (padding rows get an offset past the
-  // buffer), so a later wait can leave them in flight.
+  // Epilogue of column tile jt.  Lane (l16, lq) holds row mi*16 + l16, columns 4*lq .. 4*lq+3
+  // of each of its 16-column blocks.  Atomic outputs: through the LDS slot `ot` (free once every
+  // wave is past the barrier below), CH rows at a time -- phase 1 writes the scaled values,
+  // phase 2 adds them row-contiguously, each wave instruction covering 256 contiguous bytes
+  // (scattered 4-lane fragments would touch 16 cache lines per instruction, which costs the
+  // atomics 8x their useful rate).
   const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
   // column scales of the current tile, loaded at its first step ahead of that step's DMA (so
   // the next step's wait covers them and the epilogue waits for nothing)
   f32x4 sc[NB][NR];
   auto epilogue = [&](int jt, uint8_t* ot) {
     const int n0 = jt * TN;
+    if (!F32 && rows) {
+      // Row outputs (stage 1, reduce mode): straight from the accumulators, 8 bytes per lane
+      // (4 columns of one row), exactly NST buffer stores per thread (padding rows get an
+      // offset past the buffer).  Partial lines merge in the write-back L2, so this costs no
+      // more HBM traffic than staged full-line stores and saves the LDS round trip.
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < NR; ++ni) {
+          const int c = (wave * NR + ni) * 16 + lq * 4;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (STAGE == 1) {
+              const float g = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
+              const float u = ((float)acc[1][mi][ni][q] * sx_r[mi]) * sc[1][ni][q];
+              v[q] = silu_f(g) * u;
+            } else {
+              v[q] = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
+            }
+            if (p.doweight) v[q] *= rw_r[mi];
+          }
+          const int d = dst_r[mi];
+          const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)(n0 + c)) * 2u;
+          __builtin_amdgcn_raw_buffer_store_b64(obf16 ? pack_out4<true>(v) : pack_out4<false>(v), rsrc_o, off, 0, 0);
+        }
+      }
+      return;
+    }
     workgroup_barrier();  // every wave is done computing from the slot
 #pragma unroll
     for (int ch = 0; ch < C::NCH; ++ch) {
@@ -305,18 +332,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
       }
       workgroup_barrier();
       const int nrows = min(C::CH, TME - ch * C::CH);
-      if (!F32 && rows) {
-#pragma unroll
-        for (int it = 0; it < C::NSTC; ++it) {
-          const int idx0 = it * NT + tid;
-          const int idx = min(idx0, nrows * C::CPR - 1);
-          const int r = idx / C::CPR, cc = idx - r * C::CPR;
-          const int d = idx0 < nrows * C::CPR ? *(const int*)(ot + r * C::RS + TN * C::ESZ) : -1;
-          const i32x4 val = *(const i32x4*)(ot + r * C::RS + cc * 16);
-          const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)n0) * 2u + cc * 16u;
-          __builtin_amdgcn_raw_buffer_store_b128(val, rsrc_o, off, 0, 0);
-        }
-      } else {
+      {
         constexpr int WPR = TN * C::ESZ / 4;    // 4-byte words per output row
         for (int idx = tid; idx < nrows * WPR; idx += NT) {
           const int r = idx / WPR, wd = idx - r * WPR;
