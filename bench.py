@@ -187,8 +187,8 @@ class MoeRunner:
             self.args = (_dev_flat(p["a2"], dev), _dev_flat(p["w2_shuf"], dev), p["sa2"], p["sw2"])
             self.nk = (base.model_dim, base.inter_dim)
         self.copies = 1
-        self.variant = f"moe_gemm{stage}_{base.tile_m}x{base.tile_n1 if stage == 1 else base.tile_n2}" + \
-            ("+reduce" if name.endswith("R") else "")
+        # the library picks the column tile and the rows per workgroup (profiles name the kernel)
+        self.variant = f"moe_gemm{stage} tile_m={base.tile_m}" + (" +reduce" if name.endswith("R") else "")
 
     def launch(self, i, stream):
         p, b = self.p, self.w.base

@@ -66,6 +66,11 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (tokens >= (1 << 24)) return fail(hipErrorInvalidValue, "%s: tokens=%d must be below 2^24", what, tokens);
   if (tile_m != 16 && tile_m != 32 && tile_m != 64)
     return fail(hipErrorInvalidValue, "%s: tile_m=%d must be 16, 32 or 64", what, tile_m);
+  // the caller's tile is checked as the reference checks it, before the choices below
+  if (tile_n > 0 && tile_n != 64 && tile_n != 128 && tile_n != 256)
+    return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
+  if (tile_n > 0 && N % tile_n != 0)
+    return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
   // Runs of several routing blocks when experts hold two or more blocks on average: 128 rows
   // (stage 1, gate and up) or 256 rows (stage 2) per workgroup of 8 waves, with 256-column
   // tiles.  The caller's tile_n is then overridden: tiling does not change the results.
@@ -77,6 +82,12 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
     tile_n = 256;
   }
   if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
+  // Few runs (decode): narrower column tiles until there are workgroups for every CU (each
+  // workgroup streams its own weight columns, so parallelism is bandwidth here).
+  if (R == 1 && (tile_n == 128 || tile_n == 256)) {
+    const long runs1 = est_runs(tokens, topk, experts, tile_m, 1);
+    while (tile_n > 64 && runs1 * (N / tile_n) < 256 && N % (tile_n / 2) == 0) tile_n /= 2;
+  }
   if (tile_n != 64 && tile_n != 128 && tile_n != 256)
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
   if (N % tile_n != 0) return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
