@@ -153,7 +153,7 @@ class MoeStageWorkload:
 # bench name -> (MoE workload, stage)
 # (the R variants run stage 2 in reduce mode: per-route rows, then the top-k reduction)
 MOE_BENCH = {"MP1": ("DSP", 1), "MP2": ("DSP", 2), "MP2R": ("DSP", 2), "MD1": ("DSD", 1), "MD2": ("DSD", 2),
-             "MD2R": ("DSD", 2)}
+             "MD2R": ("DSD", 2), "MB1": ("DSB", 1), "MB2": ("DSB", 2)}
 
 
 class MoeRunner:
@@ -168,6 +168,12 @@ class MoeRunner:
         self.p, self.stage = p, stage
         kw = dict(model_dim=base.model_dim, inter_dim=base.inter_dim, experts=base.experts, topk=base.topk,
                   tile_m=base.tile_m, tile_k=128, in_dtype=base.kind)
+        if base.kind == "fp8_block":
+            from flydsl_amd.kernels.moe_blockscale_2stage import (compile_moe_blockscale_gemm1,
+                                                                  compile_moe_blockscale_gemm2)
+            kw.pop("in_dtype")
+            compile_moe_gemm1 = lambda **k: compile_moe_blockscale_gemm1(**k)   # noqa: E731
+            compile_moe_gemm2 = lambda **k: compile_moe_blockscale_gemm2(**k)   # noqa: E731
         if stage == 1:
             self.fn = compile_moe_gemm1(**kw, tile_n=base.tile_n1, doweight_stage1=False, out_dtype="f16")
             self.out = torch.empty(base.tokens, base.topk, base.inter_dim, dtype=torch.float16, device=dev)
@@ -391,7 +397,7 @@ def main():
         log(f"[bench] preparing {name} {w2.kind} {w2.M}x{w2.N}x{w2.K}")
         log(f"[bench] timing {name} variant={r2.variant}")
         ms2, _ = r2.time(max(5, args.steps // 2), max(2, args.warmup // 2))
-        b2 = "hbm" if name in ("C1", "C2", "Q", "MD1", "MD2", "MD2R") else "mfma"
+        b2 = "hbm" if name in ("C1", "C2", "Q", "MD1", "MD2", "MD2R", "MB1", "MB2") else "mfma"
         sec[name] = {"ms": round(ms2, 5), "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
         if w2.flops:

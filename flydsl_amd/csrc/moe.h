@@ -100,9 +100,14 @@ struct MoeCfg {
 //   Epilogue at the end of each column tile: row outputs (stage 1, reduce mode) are stored
 //   straight from the accumulators; atomic accumulation goes through the slot the last step
 //   computed from, in chunks of CH rows, so each wave instruction adds 256 contiguous bytes.
-template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32>
+// BS: blockscale (fp8): sa = x scales [K/128][rows of A] (K-block major), sw = weight scales
+// [E*wrows/128][K/128] (one per 128x128 block); each K step's MFMA partial is scaled by
+// sa[kb][row] * sw[row block of the column][kb] and added to the accumulator (reference
+// kernels/moe_blockscale_2stage.py:677-777 for stage 1, :1836-1880 for stage 2).
+template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32, bool BS = false>
 __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   using C = MoeCfg<STAGE, KIND, TM, R, TN, NW, F32>;
+  static_assert(!BS || KIND == KIND_FP8, "blockscale is fp8");
   static_assert(STAGE == 2 || !F32, "stage 1 writes 2-byte outputs");
   static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "MoE input kinds");
   constexpr int MR = C::MR, NR = C::NR, NB = C::NB, TME = C::TME, NT = NW * 64;
@@ -141,7 +146,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
   const int a_rows = STAGE == 1 ? p.tokens : p.tokens * p.topk;
-  constexpr bool kScaled = !kind_is_16bit(KIND);
+  constexpr bool kScaled = !kind_is_16bit(KIND) && !BS;  // per-token / per-row scales in the epilogue
 
   // ---- per-row facts, fixed for the workgroup's life ----
   // Every load below is unconditional (indices clamped into range, the result masked after), so
@@ -167,7 +172,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   }
   // this lane's rows mi*16 + l16: scale, routing weight, destination row (-1: padding)
   float sx_r[MR], rw_r[MR];
-  int dst_r[MR];
+  int dst_r[MR], arow_r[MR];
 #pragma unroll
   for (int mi = 0; mi < MR; ++mi) {
     const int r = mi * 16 + l16;
@@ -176,9 +181,10 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
     const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
     dst_r[mi] = !ok ? -1 : (rows ? t * p.topk + s : t);
     const int arow = ok ? (STAGE == 1 ? t : t * p.topk + s) : 0;
+    arow_r[mi] = arow;
     const float sxv = kScaled ? p.sa[arow] : 1.f;
     const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
-    sx_r[mi] = ok ? sxv : 0.f;
+    sx_r[mi] = ok ? sxv : 0.f;  // 0 keeps padding rows finite; 1 for unscaled kinds
     rw_r[mi] = ok ? rwv : 0.f;
   }
 
@@ -212,6 +218,24 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
   AccT acc[NB][MR][NR];
 
+  // blockscale factors of the current step (bsa_c: this lane's rows, bsw_c: its 16-column
+  // blocks) and of the next (bsa_n / bsw_n, loaded before the next step's DMA is issued and
+  // copied at that step's top, after its wait -- a copy earlier would wait for the DMA)
+  float bsa_c[BS ? MR : 1], bsa_n[BS ? MR : 1], bsw_c[NB][BS ? NR : 1], bsw_n[NB][BS ? NR : 1];
+  auto load_bs = [&](int jt, int kt) {
+    if constexpr (BS) {
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) bsa_n[mi] = p.sa[kt * a_rows + arow_r[mi]];
+#pragma unroll
+      for (int h = 0; h < NB; ++h)
+#pragma unroll
+        for (int ni = 0; ni < NR; ++ni) {
+          const int wr = e * wrows + (h ? p.N : 0) + jt * TN + (wave * NR + ni) * 16;
+          bsw_n[h][ni] = p.sw[(wr / 128) * nk + kt];
+        }
+    }
+  };
+
   // One K tile: this wave's B fragments read once, then row block by row block, the next row's
   // A fragment read ahead of this row's MFMAs.  B is the MFMA's first operand, so each
   // accumulator tile holds its 16x16 output block transposed.
@@ -242,7 +266,16 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
       for (int h = 0; h < NB; ++h)
 #pragma unroll
         for (int ni = 0; ni < NR; ++ni) {
-          if constexpr (KIND == KIND_FP8) {
+          if constexpr (BS) {
+            const f32x4 part = mfma_fp8(__builtin_shufflevector(bl[h][ni], bh[h][ni], 0, 1, 2, 3, 4, 5, 6, 7),
+                                        __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7),
+                                        f32x4{0.f, 0.f, 0.f, 0.f});
+            const float sc_k = bsa_c[mi] * bsw_c[h][ni];
+            acc[h][mi][ni].x = __builtin_fmaf(part.x, sc_k, acc[h][mi][ni].x);
+            acc[h][mi][ni].y = __builtin_fmaf(part.y, sc_k, acc[h][mi][ni].y);
+            acc[h][mi][ni].z = __builtin_fmaf(part.z, sc_k, acc[h][mi][ni].z);
+            acc[h][mi][ni].w = __builtin_fmaf(part.w, sc_k, acc[h][mi][ni].w);
+          } else if constexpr (KIND == KIND_FP8) {
             acc[h][mi][ni] = mfma_fp8(__builtin_shufflevector(bl[h][ni], bh[h][ni], 0, 1, 2, 3, 4, 5, 6, 7),
                                       __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[h][mi][ni]);
           } else {
@@ -361,6 +394,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   // the next step's wait leaves them in flight (vector memory operations retire in issue order).
   int slot = 0;
   bool keep_stores = false;
+  load_bs(j0, 0);
   issue(j0, 0, 0);
   for (int jt = j0; jt < j1; ++jt) {
 #pragma unroll
@@ -376,6 +410,18 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
         wait_dma();
       keep_stores = false;
       workgroup_barrier();
+      if constexpr (BS) {
+#pragma unroll
+        for (int mi = 0; mi < MR; ++mi) bsa_c[mi] = bsa_n[mi];
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+          for (int ni = 0; ni < NR; ++ni) bsw_c[h][ni] = bsw_n[h][ni];
+        if (kt + 1 < nk)
+          load_bs(jt, kt + 1);
+        else if (jt + 1 < j1)
+          load_bs(jt + 1, 0);
+      }
       if (kt == 0) {
 #pragma unroll
         for (int h = 0; h < NB; ++h)

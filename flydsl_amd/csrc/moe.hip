@@ -13,28 +13,31 @@ using namespace flygemm;
 // Instantiated tiles: runs of one routing block (R = 1, 4 waves) for every (tile_m, tile_n);
 // runs of 128 rows (stage 1) or 256 rows (stage 2) with 256-column tiles and 8 waves.
 namespace flygemm {
-MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32);
+MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
 }
 
 namespace {
 
-template <int KIND>
+template <int KIND, bool BS>
 MoeFn moe_stage1_tile(int tm, int r, int tn) {
 #define T(M_, R_, N_, W_) \
-  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, W_, false>;
+  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, W_, false, BS>;
   T(16, 1, 64, 4) T(16, 1, 128, 4) T(16, 1, 256, 4) T(32, 1, 64, 4) T(32, 1, 128, 4) T(32, 1, 256, 4)
   T(64, 1, 64, 4) T(64, 1, 128, 4) T(64, 1, 256, 4)
-  T(16, 8, 256, 8) T(32, 4, 256, 8) T(64, 2, 256, 8)
+  if constexpr (!BS) {  // the blockscale partials and factors do not fit next to the run tiles
+    T(16, 8, 256, 8) T(32, 4, 256, 8) T(64, 2, 256, 8)
+  }
 #undef T
   return nullptr;
 }
 
-MoeFn moe_stage1_kernel(int kind, int tm, int r, int tn) {
+MoeFn moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
+  if (bs) return kind == KIND_FP8 ? moe_stage1_tile<KIND_FP8, true>(tm, r, tn) : nullptr;
   switch (kind) {
-    case KIND_FP8: return moe_stage1_tile<KIND_FP8>(tm, r, tn);
-    case KIND_INT8: return moe_stage1_tile<KIND_INT8>(tm, r, tn);
-    case KIND_BF16: return moe_stage1_tile<KIND_BF16>(tm, r, tn);
-    case KIND_F16: return moe_stage1_tile<KIND_F16>(tm, r, tn);
+    case KIND_FP8: return moe_stage1_tile<KIND_FP8, false>(tm, r, tn);
+    case KIND_INT8: return moe_stage1_tile<KIND_INT8, false>(tm, r, tn);
+    case KIND_BF16: return moe_stage1_tile<KIND_BF16, false>(tm, r, tn);
+    case KIND_F16: return moe_stage1_tile<KIND_F16, false>(tm, r, tn);
     default: return nullptr;
   }
 }
@@ -57,8 +60,10 @@ int pick_tile_n(int N, long runs) {
 int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
                const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
                const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
-               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, hipStream_t stream) {
-  const char* what = stage == 1 ? "moe_gemm1" : "moe_gemm2";
+               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, bool bs,
+               hipStream_t stream) {
+  const char* what = bs ? (stage == 1 ? "moe_blockscale_gemm1" : "moe_blockscale_gemm2")
+                        : (stage == 1 ? "moe_gemm1" : "moe_gemm2");
   if (tokens < 0 || N <= 0 || K <= 0 || blocks < 0 || experts <= 0)
     return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d N=%d K=%d blocks=%d experts=%d", what, tokens, N, K,
                 blocks, experts);
@@ -76,7 +81,7 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   // tiles.  The caller's tile_n is then overridden: tiling does not change the results.
   const long routes = (long)tokens * topk;
   int R = 1;
-  if (routes >= 2L * tile_m * experts && N % 256 == 0 && tile_n != 64 &&
+  if (!bs && routes >= 2L * tile_m * experts && N % 256 == 0 && tile_n != 64 &&
       (tile_n <= 0 || tile_n == 128 || tile_n == 256)) {
     R = (stage == 1 ? 128 : 256) / tile_m;
     tile_n = 256;
@@ -124,8 +129,11 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
                                                      : (long)tokens * N * (mout == MOE_OUT_F32 ? 4 : 2);
   if (out_bytes > 0xFFFFFF00L) return fail(hipErrorInvalidValue, "%s: output above 4 GB", what);
 
-  MoeFn fn = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n)
-                        : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32);
+  if (bs && (2L * N) % (stage == 1 ? 128 : 256) != 0)
+    return fail(hipErrorInvalidValue, "%s: %s=%d must be a multiple of 128 (weight scale blocks)", what,
+                stage == 1 ? "2*inter_dim" : "model_dim", stage == 1 ? 2 * N : N);
+  MoeFn fn = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n, bs)
+                        : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
   if (!fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
 
   // column ranges per run: about 1024 workgroups in all
@@ -159,7 +167,7 @@ int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scal
                       int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream) {
   return moe_launch(1, out, x, w, scale_x, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights, num_valid_ids,
                     tokens, inter_dim, model_dim, size_expert_ids, experts, topk, tile_m, tile_n, in_dtype, out_dtype,
-                    doweight_stage1, 1, (hipStream_t)stream);
+                    doweight_stage1, 1, false, (hipStream_t)stream);
 }
 
 int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* scale_a2, const float* scale_w,
@@ -170,7 +178,35 @@ int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* sca
                       void* stream) {
   return moe_launch(2, out, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
                     num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
-                    in_dtype, out_dtype, doweight_stage2, accumulate, (hipStream_t)stream);
+                    in_dtype, out_dtype, doweight_stage2, accumulate, false, (hipStream_t)stream);
+}
+
+int flygemm_moe_blockscale_gemm1(void* out, const void* x, const void* w, const float* x_scale_t,
+                                 const float* w_scale, const int32_t* sorted_token_ids,
+                                 const int32_t* sorted_expert_ids, const float* sorted_weights,
+                                 const int32_t* num_valid_ids, int32_t tokens, int32_t inter_dim, int32_t model_dim,
+                                 int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m,
+                                 int32_t tile_n, int32_t scale_block_k, int32_t out_dtype, int32_t doweight_stage1,
+                                 void* stream) {
+  if (scale_block_k != 128)
+    return fail(hipErrorInvalidValue, "moe_blockscale_gemm1: scale_block_k=%d: only 128 is supported", scale_block_k);
+  return moe_launch(1, out, x, w, x_scale_t, w_scale, sorted_token_ids, sorted_expert_ids, sorted_weights,
+                    num_valid_ids, tokens, inter_dim, model_dim, size_expert_ids, experts, topk, tile_m, tile_n,
+                    FLYGEMM_IN_FP8, out_dtype, doweight_stage1, 1, true, (hipStream_t)stream);
+}
+
+int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const float* a2_scale_t,
+                                 const float* w_scale, const int32_t* sorted_token_ids,
+                                 const int32_t* sorted_expert_ids, const float* sorted_weights,
+                                 const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
+                                 int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m,
+                                 int32_t tile_n, int32_t scale_block_k, int32_t out_dtype, int32_t doweight_stage2,
+                                 int32_t accumulate, void* stream) {
+  if (scale_block_k != 128)
+    return fail(hipErrorInvalidValue, "moe_blockscale_gemm2: scale_block_k=%d: only 128 is supported", scale_block_k);
+  return moe_launch(2, out, a2, w, a2_scale_t, w_scale, sorted_token_ids, sorted_expert_ids, sorted_weights,
+                    num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
+                    FLYGEMM_IN_FP8, out_dtype, doweight_stage2, accumulate, true, (hipStream_t)stream);
 }
 
 int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t tokens, int32_t topk,

@@ -7,24 +7,30 @@
 namespace flygemm {
 
 namespace {
-template <int KIND, bool F32>
+template <int KIND, bool F32, bool BS>
 MoeFn stage2_tile(int tm, int r, int tn) {
 #define T(M_, R_, N_, W_) \
-  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, W_, F32>;
+  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, W_, F32, BS>;
   T(16, 1, 64, 4) T(16, 1, 128, 4) T(16, 1, 256, 4) T(32, 1, 64, 4) T(32, 1, 128, 4) T(32, 1, 256, 4)
   T(64, 1, 64, 4) T(64, 1, 128, 4) T(64, 1, 256, 4)
-  T(16, 16, 256, 8) T(32, 8, 256, 8) T(64, 4, 256, 8)
+  if constexpr (!BS) {  // the blockscale partials and factors do not fit next to the run tiles
+    T(16, 16, 256, 8) T(32, 8, 256, 8) T(64, 4, 256, 8)
+  }
 #undef T
   return nullptr;
 }
 
 template <int KIND>
 MoeFn stage2_kind(int tm, int r, int tn, bool f32) {
-  return f32 ? stage2_tile<KIND, true>(tm, r, tn) : stage2_tile<KIND, false>(tm, r, tn);
+  return f32 ? stage2_tile<KIND, true, false>(tm, r, tn) : stage2_tile<KIND, false, false>(tm, r, tn);
 }
 }  // namespace
 
-MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32) {
+MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs) {
+  if (bs)
+    return kind != KIND_FP8 ? nullptr
+                            : (f32 ? stage2_tile<KIND_FP8, true, true>(tm, r, tn)
+                                   : stage2_tile<KIND_FP8, false, true>(tm, r, tn));
   switch (kind) {
     case KIND_FP8: return stage2_kind<KIND_FP8>(tm, r, tn, f32);
     case KIND_INT8: return stage2_kind<KIND_INT8>(tm, r, tn, f32);

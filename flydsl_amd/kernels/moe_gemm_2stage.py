@@ -66,7 +66,7 @@ def _check_common(in_dtype, group_size, tile_m, tile_n, tile_k):
 
 class _MoeStage:
     def __init__(self, stage, *, model_dim, inter_dim, experts, topk, tile_m, tile_n, tile_k, doweight, in_dtype,
-                 out_dtype, elem, accumulate=True):
+                 out_dtype, elem, accumulate=True, blockscale=False):
         self.stage = stage
         self.model_dim, self.inter_dim = int(model_dim), int(inter_dim)
         self.experts, self.topk = int(experts), int(topk)
@@ -75,6 +75,7 @@ class _MoeStage:
         self.in_dtype, self.out_dtype = in_dtype, out_dtype
         self.elem = elem
         self.accumulate = bool(accumulate)
+        self.blockscale = bool(blockscale)   # fp8 with 1x128 / 128x128 block scales
 
     def __call__(self, arg_out, arg_x, arg_w, arg_scale_x, arg_scale_w, arg_sorted_token_ids, arg_expert_ids,
                  arg_sorted_weights, arg_num_valid_ids, tokens, n_in, k_in, size_expert_ids, stream=None):
@@ -102,8 +103,9 @@ class _MoeStage:
         else:
             x = device_ptr(arg_x, "arg_x", a_rows * K, elem_bytes=1)
             w = device_ptr(arg_w, "arg_w", w_rows * K, elem_bytes=1)
-            sx = device_ptr(arg_scale_x, "arg_scale_x", a_rows, dtypes=(torch.float32,))
-            sw = device_ptr(arg_scale_w, "arg_scale_w", w_rows, dtypes=(torch.float32,))
+            nsx, nsw = (a_rows * (K // 128), w_rows // 128 * (K // 128)) if self.blockscale else (a_rows, w_rows)
+            sx = device_ptr(arg_scale_x, "arg_scale_x", nsx, dtypes=(torch.float32,))
+            sw = device_ptr(arg_scale_w, "arg_scale_w", nsw, dtypes=(torch.float32,))
         # moe_sorting allocates tokens*topk + E*tile_m - topk entries, which need not fill the
         # last block; the kernels read entries only below num_valid_ids[0]
         n_sorted = min(blocks * self.tile_m, max(tokens * topk + E * self.tile_m - topk, 0))
@@ -113,13 +115,13 @@ class _MoeStage:
                if self.doweight else 0)
         nv = device_ptr(arg_num_valid_ids, "arg_num_valid_ids", 1, dtypes=(torch.int32,))
         lib = _lib.load()
-        args = (o, x, w, sx, sw, ids, eids, sws, nv, tokens, N, K, blocks, E, topk, self.tile_m, self.tile_n,
-                _lib.FLYGEMM_IN[_BUILT_IN[self.in_dtype]], _lib.FLYGEMM_OUT[out_name], int(self.doweight))
-        if self.stage == 1:
-            rc = lib.flygemm_moe_gemm1(*args, h_stream)
-        else:
-            rc = lib.flygemm_moe_gemm2(*args, int(self.accumulate), h_stream)
-        _lib.check(rc, f"flygemm_moe_gemm{self.stage}")
+        dt = 128 if self.blockscale else _lib.FLYGEMM_IN[_BUILT_IN[self.in_dtype]]   # scale_block_k / in_dtype
+        args = (o, x, w, sx, sw, ids, eids, sws, nv, tokens, N, K, blocks, E, topk, self.tile_m, self.tile_n, dt,
+                _lib.FLYGEMM_OUT[out_name], int(self.doweight))
+        name = f"flygemm_moe_{'blockscale_' if self.blockscale else ''}gemm{self.stage}"
+        fn = getattr(lib, name)
+        rc = fn(*args, h_stream) if self.stage == 1 else fn(*args, int(self.accumulate), h_stream)
+        _lib.check(rc, name)
 
 
 def compile_moe_gemm1(*, model_dim: int, inter_dim: int, experts: int, topk: int, tile_m: int, tile_n: int,

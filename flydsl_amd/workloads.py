@@ -131,7 +131,7 @@ class MoeWorkload:
     tile_m: int
     tile_n1: int
     tile_n2: int
-    kind: str = "fp8"     # "fp8" | "int8" | "bf16" | "fp16"
+    kind: str = "fp8"     # "fp8" | "int8" | "bf16" | "fp16" | "fp8_block" (1x128 / 128x128 block scales)
     seed: int = 0
     note: str = ""
 
@@ -154,6 +154,8 @@ MOE_WORKLOADS = {
     "ML": MoeWorkload("ML", 333, 4096, 2048, 17, 9, 64, 128, 256, note="reference test shape L"),
     "DSP": MoeWorkload("DSP", 8192, 7168, 256, 128, 8, 64, 256, 256, seed=1, note="DS-TP8-prefill-S"),
     "DSD": MoeWorkload("DSD", 8, 7168, 256, 256, 8, 32, 256, 256, seed=2, note="DS-TP8-decode-bs8"),
+    "DSB": MoeWorkload("DSB", 128, 7168, 256, 256, 8, 16, 256, 256, "fp8_block", seed=3,
+                       note="DS-V3-M128 blockscale (test_moe_blockscale.py:201)"),
 }
 
 
@@ -164,10 +166,13 @@ def moe_custom(tokens, model_dim, inter_dim, experts, topk, tile_m, tile_n1, til
 _MOE_T16 = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
-def _moe_quant(x: torch.Tensor, kind: str):
-    """-> (q, scale [rows] fp32 or None) with rows over the last dimension."""
+def _moe_quant(x: torch.Tensor, kind: str, weight: bool = False):
+    """-> (q, scale) : per-row fp32 scales [rows] (fp8 / int8), None (16-bit), or for "fp8_block"
+    block scales [rows/128, K/128] (weights) or [rows, K/128] (activations)."""
     if kind in _MOE_T16:
         return x.to(_MOE_T16[kind]), None
+    if kind == "fp8_block":
+        return quant.blockscale_quant(x, 128 if weight else 1, 128)
     q, s = quant.pertoken_quant(x.reshape(-1, x.shape[-1]), quant.FP8 if kind == "fp8" else torch.int8)
     return q.reshape(x.shape), s.reshape(-1)
 
@@ -192,8 +197,8 @@ def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
     vals, topk_ids = torch.topk(score, k=k, dim=1)
     topk_w = torch.softmax(vals, dim=1).float()
     xq, sx = _moe_quant(x, w.kind)
-    w1q, sw1 = _moe_quant(w1, w.kind)
-    w2q, sw2 = _moe_quant(w2, w.kind)
+    w1q, sw1 = _moe_quant(w1, w.kind, weight=True)
+    w2q, sw2 = _moe_quant(w2, w.kind, weight=True)
     del w1, w2
     sid, sw, eid, post = moe_sorting(topk_ids.to(torch.int32), topk_w, E, w.tile_m)
     out = dict(workload=w, x=xq, sx=sx, w1=w1q, sw1=sw1, w1_shuf=quant.shuffle_weight(w1q), w2=w2q, sw2=sw2,
@@ -203,6 +208,14 @@ def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
     if with_stage2_input:
         a2 = torch.randn(T * k, I, generator=g, device=device) * s
         out["a2"], out["sa2"] = _moe_quant(a2, w.kind)
+    if w.kind == "fp8_block":
+        # the kernels take activation block scales K-block major ([K/128, rows], the reference's
+        # transpose_scale layout) and weight block scales flat; *_blocks keep [rows, K/128]
+        out["sx_blocks"], out["sx"] = sx, sx.t().contiguous().view(-1)
+        out["sw1"], out["sw2"] = sw1.contiguous().view(-1), sw2.contiguous().view(-1)
+        out["sw1_blocks"], out["sw2_blocks"] = sw1, sw2
+        if with_stage2_input:
+            out["sa2_blocks"], out["sa2"] = out["sa2"], out["sa2"].t().contiguous().view(-1)
     return out
 
 
@@ -212,6 +225,9 @@ def moe_bytes(w: MoeWorkload, stage: int, active_experts: int) -> int:
     eb = 2 if w.kind in _MOE_T16 else 1
     T, D, I, k = w.tokens, w.model_dim, w.inter_dim, w.topk
     meta = 4 * (T * k + w.experts * w.tile_m) * 2
+    bs = w.kind == "fp8_block"   # block scales: per (row, 128 K) for activations, 128 x 128 for weights
     if stage == 1:
-        return active_experts * 2 * I * D * eb + T * D * eb + T * k * I * 2 + (T + active_experts * 2 * I) * 4 + meta
-    return active_experts * D * I * eb + T * k * I * eb + T * D * 2 + (T * k + active_experts * D) * 4 + meta
+        sc = (T * (D // 128) + active_experts * (2 * I // 128) * (D // 128)) if bs else (T + active_experts * 2 * I)
+        return active_experts * 2 * I * D * eb + T * D * eb + T * k * I * 2 + sc * 4 + meta
+    sc = (T * k * (I // 128) + active_experts * (D // 128) * (I // 128)) if bs else (T * k + active_experts * D)
+    return active_experts * D * I * eb + T * k * I * eb + T * D * 2 + sc * 4 + meta

@@ -139,6 +139,32 @@ int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* sca
                       int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, int32_t accumulate,
                       void* stream);
 
+/* Blockscale MoE (fp8, per-block scales, ScaleBlockM = 1, N = K = 128): each 128-deep K block's
+ * partial product is scaled before it is accumulated,
+ *   acc[r][n] = sum_kb (sum_{k in kb} a[r][k] * w[n][k]) * a_scale_t[kb][r] * w_scale[n/128][kb],
+ * with r the A row (stage 1: token t; stage 2: t*topk + s) and n the weight row of the expert
+ * slab (e*2I + n / e*2I + I + n in stage 1, e*D + n in stage 2).  a_scale_t fp32 [K/128][rows of
+ * A] (K-block major); w_scale fp32 [rows of W / 128][K/128].  Then stage 1: out = silu(gate) * up
+ * (* sorted_weights if doweight); stage 2 as flygemm_moe_gemm2 (atomic or per-route rows).
+ * scale_block_k must be 128; 2*inter_dim (stage 1) / model_dim (stage 2) a multiple of 128.
+ * Replaces the launchers of compile_moe_blockscale_gemm1 / _gemm2 (reference
+ * kernels/moe_blockscale_2stage.py:75-1217, :1220-2445; oracle
+ * tests/kernels/test_moe_blockscale.py:64-133). */
+int flygemm_moe_blockscale_gemm1(void* out, const void* x, const void* w, const float* x_scale_t,
+                                 const float* w_scale, const int32_t* sorted_token_ids,
+                                 const int32_t* sorted_expert_ids, const float* sorted_weights,
+                                 const int32_t* num_valid_ids, int32_t tokens, int32_t inter_dim, int32_t model_dim,
+                                 int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m,
+                                 int32_t tile_n, int32_t scale_block_k, int32_t out_dtype, int32_t doweight_stage1,
+                                 void* stream);
+int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const float* a2_scale_t,
+                                 const float* w_scale, const int32_t* sorted_token_ids,
+                                 const int32_t* sorted_expert_ids, const float* sorted_weights,
+                                 const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
+                                 int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m,
+                                 int32_t tile_n, int32_t scale_block_k, int32_t out_dtype, int32_t doweight_stage2,
+                                 int32_t accumulate, void* stream);
+
 /* Reduce mode, second step: y [tokens][model_dim] = sum over k < topk of x [tokens][topk]
  * [model_dim] (only slots with valid_mask[t*topk+k] != 0 when valid_mask, int8 [tokens*topk], is
  * given), fp32 sums; dtype fp16, bf16 or fp32 for both x and y; model_dim a multiple of 8 (4 for

@@ -21,11 +21,19 @@ grouped GEMMs, restated in numpy.
 Activations and weights arrive as quantized bytes (fp8 e4m3fn, int8) with fp32 per-row scales,
 or as bf16/fp16 bit patterns without scales; the products are evaluated in float64.
 
+* ``gemm1_blockscale`` / ``gemm2_blockscale``  ``torch_stage1_blockscale_ref`` /
+                    ``torch_stage2_blockscale_ref`` (``tests/kernels/test_moe_blockscale.py:64-133``):
+                    fp8 activations scaled per (row, 128-wide K block), weights per 128 x 128
+                    block, then the route loops above.
+
 Pins (``tests/test_oracle.py``): a hand-worked sorting example; sorting invariants on random
 routings (every route exactly once, runs padded and expert-homogeneous, the padded total);
 silu's closed-form values and the identity ``silu(x) - silu(-x) = x``; gate/up order through
 weights that zero one half; ``gemm2`` against one dense matmul when all experts are equal and the
-routing weights sum to one; sorted-walk forms against the route forms.
+routing weights sum to one; sorted-walk forms against the route forms; the blockscale forms
+against the dense blockscale oracle (``gemm.run_torch_blockscale``, itself pinned) with every
+token routed to one expert, and against the per-row forms when every block scale of a row is
+equal.
 """
 from __future__ import annotations
 
@@ -156,4 +164,66 @@ def gemm2_sorted(a2_q, w2_q, sa2, sw2, sorted_ids, sorted_w, sorted_eids, num_va
     for i, t, s, e in _sorted_routes(sorted_ids, sorted_eids, num_valid, block_size, tokens, topk):
         y = _expert_w(w2_q, sw2, kind, model_dim, e) @ a2[t * topk + s]
         out[t] += y * float(sorted_w[i]) if doweight else y
+    return out
+
+
+# ---- blockscale (fp8, 1 x 128 activation blocks, 128 x 128 weight blocks) -----------------
+# Restates torch_stage1_blockscale_ref / torch_stage2_blockscale_ref
+# (tests/kernels/test_moe_blockscale.py:64-133): activations dequantized per (row, 128-wide K
+# block), weights per 128 x 128 block of the flattened [E*rows, K] array, then the same route
+# loops as gemm1 / gemm2.
+
+def _dequant_blocks(q, scale, row0: int = 0, blk: int = 128) -> np.ndarray:
+    """fp8 bytes [R, K] times scale [R / rb, K / blk] expanded (rb = blk for weights, 1 for
+    activations -- told apart by the scale's row count)."""
+    from .numerics import e4m3fn_decode
+    v = e4m3fn_decode(np.asarray(q)).astype(np.float64)
+    s = np.asarray(scale, dtype=np.float64)
+    rb = v.shape[0] // s.shape[0] if s.shape[0] != v.shape[0] else 1
+    return v * np.repeat(np.repeat(s, rb, axis=0), blk, axis=1)[:, :v.shape[1]]
+
+
+def gemm1_blockscale(x_q, w1_q, x_scale, w1_scale, topk_ids, topk_weights, inter_dim: int, doweight: bool,
+                     tokens_subset=None) -> np.ndarray:
+    """x_q [T, D] fp8; x_scale [T, D/128]; w1_q [E*2I, D] fp8 unshuffled; w1_scale [E*2I/128, D/128]."""
+    ids = np.asarray(topk_ids).astype(np.int64)
+    T, topk = ids.shape
+    rows = 2 * inter_dim
+    E = np.asarray(w1_q).shape[0] // rows
+    x = _dequant_blocks(x_q, x_scale)
+    out = np.zeros((T, topk, inter_dim))
+    sel = _selected(T, tokens_subset)
+    for e in range(E):
+        t_idx, s_idx = np.nonzero((ids == e) & sel[:, None])
+        if len(t_idx) == 0:
+            continue
+        w = _dequant_blocks(np.asarray(w1_q)[e * rows:(e + 1) * rows],
+                            np.asarray(w1_scale)[e * rows // 128:(e + 1) * rows // 128])
+        y = x[t_idx] @ w.T
+        v = silu(y[:, :inter_dim]) * y[:, inter_dim:]
+        if doweight:
+            v = v * np.asarray(topk_weights, np.float64)[t_idx, s_idx][:, None]
+        out[t_idx, s_idx] = v
+    return out
+
+
+def gemm2_blockscale(a2_q, w2_q, a2_scale, w2_scale, topk_ids, topk_weights, model_dim: int, doweight: bool,
+                     tokens_subset=None) -> np.ndarray:
+    """a2_q [T*topk, I] fp8; a2_scale [T*topk, I/128]; w2_q [E*D, I]; w2_scale [E*D/128, I/128]."""
+    ids = np.asarray(topk_ids).astype(np.int64)
+    T, topk = ids.shape
+    E = np.asarray(w2_q).shape[0] // model_dim
+    sel = _selected(T, tokens_subset)
+    a2 = _dequant_blocks(a2_q, a2_scale)
+    out = np.zeros((T, model_dim))
+    for e in range(E):
+        t_idx, s_idx = np.nonzero((ids == e) & sel[:, None])
+        if len(t_idx) == 0:
+            continue
+        w = _dequant_blocks(np.asarray(w2_q)[e * model_dim:(e + 1) * model_dim],
+                            np.asarray(w2_scale)[e * model_dim // 128:(e + 1) * model_dim // 128])
+        y = a2[t_idx * topk + s_idx] @ w.T
+        if doweight:
+            y = y * np.asarray(topk_weights, np.float64)[t_idx, s_idx][:, None]
+        np.add.at(out, t_idx, y)
     return out

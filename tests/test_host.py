@@ -252,3 +252,26 @@ def test_moe_launchers_validate_like_reference():
     i = torch.empty(200, dtype=torch.int32)
     with pytest.raises(ValueError, match="GPU tensor"):
         fn(c, b, b, s, s, i, i, s, i, 64, 256, 128, 12)
+
+
+def test_moe_blockscale_validation():
+    from flydsl_amd.kernels.moe_blockscale_2stage import (compile_moe_blockscale_gemm1, compile_moe_blockscale_gemm2,
+                                                          compile_moe_blockscale_gemm2_ex)
+    kw = dict(model_dim=512, inter_dim=128, experts=4, topk=2, tile_m=16, tile_n=64, tile_k=128)
+    with pytest.raises(ValueError):
+        compile_moe_blockscale_gemm1(**kw, doweight_stage1=False, scale_block_k=64)
+    with pytest.raises(ValueError):
+        compile_moe_blockscale_gemm1(**{**kw, "inter_dim": 96}, doweight_stage1=False)   # 2I % 128
+    with pytest.raises(ValueError):
+        compile_moe_blockscale_gemm2(**{**kw, "model_dim": 320}, doweight_stage2=True)  # model_dim % 128
+    with pytest.raises(ValueError):
+        compile_moe_blockscale_gemm2(**kw, doweight_stage2=True, out_dtype="f32", accumulate=False)
+    with pytest.raises(ValueError):
+        compile_moe_blockscale_gemm2_ex(**kw, doweight_stage2=True, in_dtype="int8")
+    lib = _lib.load()
+    p = ctypes.c_void_p(256)
+    rc = lib.flygemm_moe_blockscale_gemm1(p, p, p, p, p, p, p, p, p, 16, 128, 512, 6, 4, 2, 16, 64, 64, 1, 0, None)
+    assert rc != 0 and b"scale_block_k" in lib.flygemm_last_error()
+    rc = lib.flygemm_moe_blockscale_gemm2(p, p, p, p, p, p, p, p, p, 16, 320, 128, 6, 4, 2, 16, 64, 128, 1, 1, 1,
+                                          None)
+    assert rc != 0 and b"multiple of 128" in lib.flygemm_last_error()

@@ -708,3 +708,69 @@ def test_moe_gemm2_equal_experts_is_one_dense_matmul():
     sid, sw, eid, post = omoe.moe_sorting(ids, w, E, 4)
     alt = omoe.gemm2_sorted(a2q, w2q, sa2, sw2, sid, sw, eid, post[0], 4, T, k, D, True, "int8")
     assert np.allclose(alt, got, rtol=1e-12, atol=1e-12)
+
+
+def _bs_case(seed, T=5, D=256, I=64, E=3, k=2):
+    g = np.random.default_rng(seed)
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)])
+    w = g.random((T, k)).astype(np.float32)
+    x = g.standard_normal((T, D)).astype(np.float32)
+    w1 = (g.standard_normal((E * 2 * I, D)) * 0.3).astype(np.float32)
+    xq, xs = oq.quant_blocks(x, 1, 128)
+    w1q, w1s = oq.quant_blocks(w1, 128, 128)
+    return ids, w, xq, xs, w1q, w1s
+
+
+def test_moe_blockscale_one_expert_is_the_dense_blockscale_oracle():
+    """Every token routed to expert 0 (top-1): gate and up are dense blockscale GEMMs of x with
+    the expert's gate / up rows (gemm.run_torch_blockscale, pinned above)."""
+    T, D, I, E = 6, 384, 64, 2
+    ids, w, xq, xs, w1q, w1s = _bs_case(4, T, D, I, E, 1)
+    ids[:] = 0
+    got = omoe.gemm1_blockscale(xq, w1q, xs, w1s, ids, w, I, False)
+    gate = og.run_torch_blockscale(xq, w1q[:I], xs, w1s[:I // 128 or 1], "f64") if I >= 128 else None
+    # I = 64 rows share one 128-row scale block: expand by hand for the gate and up halves
+    from oracle.numerics import e4m3fn_decode
+    xd = e4m3fn_decode(xq).astype(np.float64) * np.repeat(xs, 128, axis=1)
+    wd = e4m3fn_decode(w1q[:2 * I]).astype(np.float64) * np.repeat(np.repeat(w1s[:1], 2 * I, 0), 128, 1)
+    y = xd @ wd.T
+    assert np.allclose(got[:, 0], omoe.silu(y[:, :I]) * y[:, I:], rtol=1e-12, atol=1e-12)
+    assert gate is None
+    # with 128-row halves the dense oracle applies directly
+    T, D, I, E = 4, 256, 128, 2
+    ids, w, xq, xs, w1q, w1s = _bs_case(5, T, D, I, E, 1)
+    ids[:] = 1
+    got = omoe.gemm1_blockscale(xq, w1q, xs, w1s, ids, w, I, True)
+    rows = slice(2 * I, 4 * I)
+    g_ = og.run_torch_blockscale(xq, w1q[2 * I:3 * I], xs, w1s[2:3], "f64")
+    u_ = og.run_torch_blockscale(xq, w1q[3 * I:4 * I], xs, w1s[3:4], "f64")
+    # (the dense oracle rounds the dequantized operands to float32 first)
+    assert np.allclose(got[:, 0], omoe.silu(g_) * u_ * w[:, :1], rtol=1e-5, atol=1e-5)
+    del rows
+
+
+def test_moe_blockscale_stage2_one_expert_and_uniform_scales():
+    T, I, D, E, k = 5, 256, 128, 2, 2
+    g = np.random.default_rng(9)
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)])
+    w = g.random((T, k)).astype(np.float32)
+    a2 = g.standard_normal((T * k, I)).astype(np.float32)
+    w2 = (g.standard_normal((E * D, I)) * 0.1).astype(np.float32)
+    a2q, a2s = oq.quant_blocks(a2, 1, 128)
+    w2q, w2s = oq.quant_blocks(w2, 128, 128)
+    got = omoe.gemm2_blockscale(a2q, w2q, a2s, w2s, ids, w, D, True)
+    # route by route through the dense blockscale oracle
+    ref = np.zeros((T, D))
+    for t in range(T):
+        for s in range(k):
+            e = ids[t, s]
+            r = t * k + s
+            ref[t] += w[t, s] * og.run_torch_blockscale(a2q[r:r + 1], w2q[e * D:(e + 1) * D], a2s[r:r + 1],
+                                                         w2s[e * D // 128:(e + 1) * D // 128], "f64")[0]
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6)
+    # equal scales across K blocks reduce to the per-row form
+    a2s_u = np.repeat(a2s[:, :1], a2s.shape[1], axis=1)
+    w2s_u = np.repeat(w2s[:, :1], w2s.shape[1], axis=1)
+    got_u = omoe.gemm2_blockscale(a2q, w2q, a2s_u, w2s_u, ids, w, D, True)
+    row_u = omoe.gemm2(a2q, w2q, a2s_u[:, 0], np.repeat(w2s_u[:, 0], 128), ids, w, D, True, "fp8")
+    assert np.allclose(got_u, row_u, rtol=1e-5, atol=1e-6)   # dequant_rows rounds to float32
