@@ -66,11 +66,14 @@ __device__ __forceinline__ float silu_f(float x) {
 // bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
 // F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
 // bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
-template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32>
+template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, int NS_ = 2>
 struct MoeCfg {
+  static constexpr int NS = NS_;                      // LDS ring slots: the DMA runs NS-1 steps ahead
+  static constexpr int NW = WM * WN;                  // waves: WM across the rows, WN across the columns
   static constexpr int TME = TM * R;                  // rows of one run: up to R routing blocks
-  static constexpr int MR = TME / 16;                 // 16-row blocks (every wave covers all rows)
-  static constexpr int NR = TN / (16 * NW);           // 16-column blocks per wave and weight half
+  static constexpr int TMW = TME / WM;                // rows per wave
+  static constexpr int MR = TMW / 16;                 // 16-row blocks per wave
+  static constexpr int NR = TN / (16 * WN);           // 16-column blocks per wave and weight half
   static constexpr int NB = STAGE == 1 ? 2 : 1;       // weight halves: gate and up in stage 1
   static constexpr int A_BYTES = TME * KT;            // A part of one LDS slot
   static constexpr int B_BYTES = NB * (TN / 16) * 2048;  // B part: NB x TN columns x 128 bytes
@@ -85,18 +88,22 @@ struct MoeCfg {
   static constexpr int CH = (SLOT / RS) / 16 * 16 < TME ? (SLOT / RS) / 16 * 16 : TME;  // rows per chunk
   static constexpr int NCH = (TME + CH - 1) / CH;
   static constexpr int NST = MR * NR;                 // direct row stores per thread per column tile
-  static_assert(TM % 16 == 0 && NR >= 1 && TN % (16 * NW) == 0 && A_BYTES % 1024 == 0, "tile shape");
+  static_assert(TM % 16 == 0 && NR >= 1 && TN % (16 * WN) == 0 && TMW % 16 == 0 && A_BYTES % 1024 == 0,
+                "tile shape");
   static_assert(B_BYTES % (1024 * NW) == 0, "B DMA split over the waves");
-  static_assert(CH >= 16 && 2 * SLOT <= 160 * 1024, "LDS budget");
+  static_assert(CH >= 16 && NS * SLOT <= 160 * 1024, "LDS budget");
+  static_assert(NS == 2 || (NS == 3 && A_DMA % NW == 0), "a 3-slot ring counts equal DMA issues per wave");
+  static constexpr int DMA_PER_STEP = (NS == 3 ? A_DMA / NW : 0) + BQ;  // per wave (3-slot ring)
 };
 
-// One workgroup (NW waves) per (run, column range): a run is up to R consecutive routing blocks of
+// One workgroup (WM x WN waves) per (run, column range): a run is up to R consecutive routing blocks of
 // one expert (a block starts a run when its index is a multiple of R or its expert differs from
 // the previous block's), so the weight tile of each K step serves up to R*TM rows; the
 // workgroup then walks its column tiles and K tiles as one pipeline.
 //   Each K step: A (the gathered rows) and B (the expert's preshuffled weight rows of the column
 //   tile, gate and up in stage 1) go global -> LDS by DMA into a 2-slot ring, one step ahead.
-//   Wave w owns columns [w*TN/NW, (w+1)*TN/NW) of the tile, for all rows.
+//   Wave (wm, wn) owns rows [wm*TME/WM, (wm+1)*TME/WM) and columns [wn*TN/WN, (wn+1)*TN/WN) of
+//   the tile (of the gate and of the up half in stage 1, so silu(gate) * up pairs in registers).
 //   Epilogue at the end of each column tile: row outputs (stage 1, reduce mode) are stored
 //   straight from the accumulators; atomic accumulation goes through the slot the last step
 //   computed from, in chunks of CH rows, so each wave instruction adds 256 contiguous bytes.
@@ -104,9 +111,11 @@ struct MoeCfg {
 // [E*wrows/128][K/128] (one per 128x128 block); each K step's MFMA partial is scaled by
 // sa[kb][row] * sw[row block of the column][kb] and added to the accumulator (reference
 // kernels/moe_blockscale_2stage.py:677-777 for stage 1, :1836-1880 for stage 2).
-template <int STAGE, int KIND, int TM, int R, int TN, int NW, bool F32, bool BS = false>
-__global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
-  using C = MoeCfg<STAGE, KIND, TM, R, TN, NW, F32>;
+template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, bool BS = false, int NS = 2>
+__global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
+  using C = MoeCfg<STAGE, KIND, TM, R, TN, WM, WN, F32, NS>;
+  static_assert(NS == 2 || (!BS && STAGE == 1), "the 3-slot ring is for stage 1 row outputs");
+  constexpr int NW = C::NW, TMW = C::TMW;
   static_assert(!BS || KIND == KIND_FP8, "blockscale is fp8");
   static_assert(STAGE == 2 || !F32, "stage 1 writes 2-byte outputs");
   static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "MoE input kinds");
@@ -114,7 +123,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   const int mode = p.out_mode;
   const bool rows = STAGE == 1 || mode == MOE_OUT_F16_ROWS || mode == MOE_OUT_BF16_ROWS;
   const bool obf16 = moe_out_bf16(mode);
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * C::SLOT];
 
   // ---- which run and which column tiles ----
   // Logical id L = block * nsplit + split over the blocks below num_valid_ids, dealt to the 8
@@ -144,6 +153,8 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   const int nk = K / KT;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int rw0 = wm * TMW;    // this wave's first row
   const int l16 = lane & 15, lq = lane >> 4;
   const int a_rows = STAGE == 1 ? p.tokens : p.tokens * p.topk;
   constexpr bool kScaled = !kind_is_16bit(KIND) && !BS;  // per-token / per-row scales in the epilogue
@@ -159,7 +170,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   for (int j = 0; j < C::AQ; ++j)
     ida[j] = p.sorted_ids[b0 * TM + min(min((wave + j * NW) * 8 + (lane >> 3), TME - 1), rows_valid - 1)];
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) idr[mi] = p.sorted_ids[b0 * TM + min(mi * 16 + l16, rows_valid - 1)];
+  for (int mi = 0; mi < MR; ++mi) idr[mi] = p.sorted_ids[b0 * TM + min(rw0 + mi * 16 + l16, rows_valid - 1)];
 #pragma unroll
   for (int j = 0; j < C::AQ; ++j) {
     const int rloc = min((wave + j * NW) * 8 + (lane >> 3), TME - 1);
@@ -175,7 +186,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   int dst_r[MR], arow_r[MR];
 #pragma unroll
   for (int mi = 0; mi < MR; ++mi) {
-    const int r = mi * 16 + l16;
+    const int r = rw0 + mi * 16 + l16;
     const int id = idr[mi];
     const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
     const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
@@ -230,7 +241,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
       for (int h = 0; h < NB; ++h)
 #pragma unroll
         for (int ni = 0; ni < NR; ++ni) {
-          const int wr = e * wrows + (h ? p.N : 0) + jt * TN + (wave * NR + ni) * 16;
+          const int wr = e * wrows + (h ? p.N : 0) + jt * TN + (wn * NR + ni) * 16;
           bsw_n[h][ni] = p.sw[(wr / 128) * nk + kt];
         }
     }
@@ -242,7 +253,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   auto compute = [&](const uint8_t* sA) {
     const uint8_t* sB = sA + C::A_BYTES;
     auto load_a = [&](int mi, i32x4& lo, i32x4& hi) {
-      const int row = mi * 16 + l16;
+      const int row = rw0 + mi * 16 + l16;
       const int sw = (row >> 1) & 7;
       lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
       hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
@@ -252,7 +263,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
     for (int h = 0; h < NB; ++h)
 #pragma unroll
       for (int ni = 0; ni < NR; ++ni) {
-        const int off = (h * (TN / 16) + wave * NR + ni) * 2048 + lq * 256 + l16 * 16;
+        const int off = (h * (TN / 16) + wn * NR + ni) * 2048 + lq * 256 + l16 * 16;
         bl[h][ni] = *(const i32x4*)(sB + off);
         bh[h][ni] = *(const i32x4*)(sB + off + 1024);
       }
@@ -287,7 +298,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   };
 
   auto col_scale = [&](int jt, int h, int ni) -> f32x4 {
-    const int n = jt * TN + (wave * NR + ni) * 16 + lq * 4;
+    const int n = jt * TN + (wn * NR + ni) * 16 + lq * 4;
     return kScaled ? *(const f32x4*)(p.sw + (size_t)e * wrows + (h ? p.N : 0) + n) : f32x4{1.f, 1.f, 1.f, 1.f};
   };
 
@@ -312,7 +323,7 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
       for (int mi = 0; mi < MR; ++mi) {
 #pragma unroll
         for (int ni = 0; ni < NR; ++ni) {
-          const int c = (wave * NR + ni) * 16 + lq * 4;
+          const int c = (wn * NR + ni) * 16 + lq * 4;
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -337,13 +348,14 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
     for (int ch = 0; ch < C::NCH; ++ch) {
       if (ch > 0) workgroup_barrier();  // the previous chunk's rows have been read out
 #pragma unroll
-      for (int mi = ch * C::CH / 16; mi < min((ch + 1) * C::CH / 16, MR); ++mi) {
+      for (int mi = 0; mi < MR; ++mi) {
+        if ((rw0 + mi * 16) / C::CH != ch) continue;   // wave-uniform: this row block is in another chunk
         __builtin_amdgcn_sched_barrier(0);
-        const int r = mi * 16 + l16 - ch * C::CH;
-        if (wave == 0 && lq == 0) *(int*)(ot + r * C::RS + TN * C::ESZ) = dst_r[mi];
+        const int r = rw0 + mi * 16 + l16 - ch * C::CH;
+        if (wn == 0 && lq == 0) *(int*)(ot + r * C::RS + TN * C::ESZ) = dst_r[mi];
 #pragma unroll
         for (int ni = 0; ni < NR; ++ni) {
-          const int c = (wave * NR + ni) * 16 + lq * 4;
+          const int c = (wn * NR + ni) * 16 + lq * 4;
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -392,6 +404,47 @@ __global__ void __launch_bounds__(NW * 64) moe_gemm_kernel(MoeArgs p) {
   // barrier, issues the next step's DMA into the other slot -- the next K tile, or the first of
   // the next column tile -- and computes.  The epilogue's row stores go out after that DMA, so
   // the next step's wait leaves them in flight (vector memory operations retire in issue order).
+  if constexpr (NS == 3) {
+    // Three slots, the DMA two steps ahead (for stage 1, whose gathered rows miss the L2 and
+    // whose tiles are long).  A step's DMA is complete once no more than the next step's
+    // DMA_PER_STEP operations are outstanding; the last step waits for everything.  Row stores
+    // and column scales issued between may make that wait longer, never too short.
+    const int S = (j1 - j0) * nk;
+    int ij = j0, ik = 0;  // the next step to issue
+    auto issue_next = [&](int sl) {
+      issue(ij, ik, sl);
+      if (++ik == nk) { ik = 0; ++ij; }
+    };
+    issue_next(0);
+    if (S > 1) issue_next(1);
+    int s = 0, slot = 0;
+    for (int jt = j0; jt < j1; ++jt) {
+#pragma unroll
+      for (int h = 0; h < NB; ++h)
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+#pragma unroll
+          for (int j = 0; j < NR; ++j) acc[h][i][j] = AccT{0, 0, 0, 0};
+      for (int kt = 0; kt < nk; ++kt, ++s) {
+        if (s + 1 < S)
+          waitcnt<C::DMA_PER_STEP>();
+        else
+          wait_dma();
+        workgroup_barrier();  // step s's slot is published; every wave is done with step s-1's
+        if (kt == 0) {
+#pragma unroll
+          for (int h = 0; h < NB; ++h)
+#pragma unroll
+            for (int ni = 0; ni < NR; ++ni) sc[h][ni] = col_scale(jt, h, ni);
+        }
+        if (s + 2 < S) issue_next(slot == 0 ? 2 : slot - 1);   // the slot step s-1 used
+        compute(ring + slot * C::SLOT);
+        slot = slot == 2 ? 0 : slot + 1;
+      }
+      epilogue(jt, nullptr);   // row outputs: stored from registers, no LDS staging
+    }
+    return;
+  }
   int slot = 0;
   bool keep_stores = false;
   load_bs(j0, 0);

@@ -20,12 +20,13 @@ namespace {
 
 template <int KIND, bool BS>
 MoeFn moe_stage1_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, W_) \
-  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, W_, false, BS>;
-  T(16, 1, 64, 4) T(16, 1, 128, 4) T(16, 1, 256, 4) T(32, 1, 64, 4) T(32, 1, 128, 4) T(32, 1, 256, 4)
-  T(64, 1, 64, 4) T(64, 1, 128, 4) T(64, 1, 256, 4)
+#define T(M_, R_, N_, WM_, WN_, NS_) \
+  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS, NS_>;
+  T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
+  T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)
+  T(64, 1, 256, 1, 4, 2)
   if constexpr (!BS) {  // the blockscale partials and factors do not fit next to the run tiles
-    T(16, 8, 256, 8) T(32, 4, 256, 8) T(64, 2, 256, 8)
+    T(16, 8, 128, 2, 4, 3) T(32, 4, 128, 2, 4, 3) T(64, 2, 128, 2, 4, 3)
   }
 #undef T
   return nullptr;
@@ -76,15 +77,15 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
   if (tile_n > 0 && N % tile_n != 0)
     return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
-  // Runs of several routing blocks when experts hold two or more blocks on average: 128 rows
-  // (stage 1, gate and up) or 256 rows (stage 2) per workgroup of 8 waves, with 256-column
-  // tiles.  The caller's tile_n is then overridden: tiling does not change the results.
+  // Runs of several routing blocks when experts hold two or more blocks on average, on 2 x 4
+  // waves: stage 1 128 rows x 128 output columns (128 gate + 128 up weight rows) with a 3-slot
+  // DMA ring; stage 2 256 rows x 256 columns with 2 slots.  The caller's tile_n is then overridden: tiling does not change results.
   const long routes = (long)tokens * topk;
   int R = 1;
-  if (!bs && routes >= 2L * tile_m * experts && N % 256 == 0 && tile_n != 64 &&
-      (tile_n <= 0 || tile_n == 128 || tile_n == 256)) {
-    R = (stage == 1 ? 128 : 256) / tile_m;
-    tile_n = 256;
+  const int run_tn = stage == 1 ? 128 : 256;
+  if (!bs && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
+    R = (stage == 1 ? 128 : 256) / tile_m;   // stage 1: 128 rows, three LDS slots
+    tile_n = run_tn;
   }
   if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
   // Few runs (decode): narrower column tiles until there are workgroups for every CU (each

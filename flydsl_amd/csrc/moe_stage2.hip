@@ -9,12 +9,12 @@ namespace flygemm {
 namespace {
 template <int KIND, bool F32, bool BS>
 MoeFn stage2_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, W_) \
-  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, W_, F32, BS>;
-  T(16, 1, 64, 4) T(16, 1, 128, 4) T(16, 1, 256, 4) T(32, 1, 64, 4) T(32, 1, 128, 4) T(32, 1, 256, 4)
-  T(64, 1, 64, 4) T(64, 1, 128, 4) T(64, 1, 256, 4)
+#define T(M_, R_, N_, WM_, WN_) \
+  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, WM_, WN_, F32, BS>;
+  T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(16, 1, 256, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4)
+  T(32, 1, 256, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4) T(64, 1, 256, 1, 4)
   if constexpr (!BS) {  // the blockscale partials and factors do not fit next to the run tiles
-    T(16, 16, 256, 8) T(32, 8, 256, 8) T(64, 4, 256, 8)
+    T(16, 16, 256, 2, 4) T(32, 8, 256, 2, 4) T(64, 4, 256, 2, 4)
   }
 #undef T
   return nullptr;
