@@ -45,6 +45,7 @@ struct Shape {
   const char* name;
   int family;
   int bm, bn, threads;  // main: workgroup tile; decode: bm = 16*MR rows, bn = 16*NBW cols
+  bool split;           // main family with split-K
 };
 
 // Ordered by preference: the selector takes the first tile that yields enough workgroups.
@@ -56,6 +57,13 @@ struct Shape {
   X(256, 128, 2, 4)    \
   X(128, 256, 2, 4)    \
   X(256, 64, 4, 1)     \
+  X(128, 64, 2, 2)
+
+// Split-K tiles (the main kernel with SPLIT): for M too small to give every CU a tile.  Only
+// tiles whose waves hold 8 accumulator tiles, so the fixup's SPLIT_MAX partial sets fit in
+// registers next to the accumulators.
+#define SPLIT_SHAPES(X) \
+  X(64, 128, 1, 4)    \
   X(128, 64, 2, 2)
 
 #define DECODE_SHAPES(X) \
@@ -71,19 +79,24 @@ struct Shape {
   X(8, 2, 8, 1)
 
 const Shape kShapes[] = {
-#define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64},
+#define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64, false},
     MAIN_SHAPES(MS)
 #undef MS
-#define DS(MR, NBW, NW, U) {"decode_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64},
-        DECODE_SHAPES(DS)
+#define SS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN "_splitk", FAM_MAIN, BM, BN, WM * WN * 64, true},
+        SPLIT_SHAPES(SS)
+#undef SS
+#define DS(MR, NBW, NW, U) {"decode_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, false},
+            DECODE_SHAPES(DS)
 #undef DS
 };
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 #define COUNT(...) +1
-constexpr int kFirstDecode = 0 MAIN_SHAPES(COUNT);
+constexpr int kFirstSplit = 0 MAIN_SHAPES(COUNT);
+constexpr int kFirstDecode = kFirstSplit SPLIT_SHAPES(COUNT);
 #undef COUNT
 
-// One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
+// One row of kernels per (kind, epilogue, output dtype) combination, one column per shape,
+// then the split-K reduce kernel of that combination (index kNumShapes).
 template <int KIND, int EPI, bool BF16>
 struct KernelRow {
   static const KernelFn* get() {
@@ -91,11 +104,15 @@ struct KernelRow {
 #define MS(BM, BN, WM, WN) gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16>,
         MAIN_SHAPES(MS)
 #undef MS
+#define SS(BM, BN, WM, WN) gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16, true>,
+            SPLIT_SHAPES(SS)
+#undef SS
 #define DS(MR, NBW, NW, U) gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI, BF16>,
             DECODE_SHAPES(DS)
 #undef DS
+        splitk_reduce_kernel<KIND, EPI, BF16>,
     };
-    static_assert(sizeof(fns) / sizeof(fns[0]) == kNumShapes, "variant table mismatch");
+    static_assert(sizeof(fns) / sizeof(fns[0]) == kNumShapes + 1, "variant table mismatch");
     return fns;
   }
 };
@@ -122,8 +139,19 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
   return nullptr;
 }
 
+// Automatic split count for a split-K variant (measured on MI355X for 32..128 tiles of 64x128
+// and K = 4096..8192): 4 splits, 8 when there are at most 32 tiles, and at least 8 K tiles
+// per split.
+constexpr int kSplitMinK = 8;
+int auto_splits(long ntiles, int nk) {
+  long ks = 256 / (ntiles > 0 ? ntiles : 1);
+  if (ks < 4) ks = 4;
+  if (ks > SPLIT_MAX) ks = SPLIT_MAX;
+  if (ks > nk / kSplitMinK) ks = nk / kSplitMinK;
+  return ks < 1 ? 1 : (int)ks;
+}
+
 int select_variant(int M, int N, int K, int kind, int epi) {
-  (void)K;
   if (M <= 64) {
     // decode family: fewest rows that cover M, then the most column blocks per workgroup
     // that still leaves about one workgroup per CU
@@ -152,10 +180,59 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   for (int i = 0; i < n; ++i) {
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg) continue;
-    for (int v = 0; v < kFirstDecode; ++v)
+    // the last resort (64x128) leaves CUs idle when there are at most 128 tiles: split K
+    // across workgroups when K has at least 32 K tiles (shorter K gains nothing measurable)
+    const bool split = list[i].min_wg == 0 && wg <= 128 && K / KT >= 32;
+    const int v0 = split ? kFirstSplit : 0, v1 = split ? kFirstDecode : kFirstSplit;
+    for (int v = v0; v < v1; ++v)
       if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }
   return -1;
+}
+
+// Split-K workspace per (device, stream): the ks partial-sum slices, grown on demand and kept
+// for the life of the process.  Each stream has its own, so launches that run concurrently on
+// different streams never share one; launches on one stream run in order.  Growing it
+// allocates (and waits for the stream), so it refuses to happen under graph capture.
+int splitk_workspace(hipStream_t stream, size_t bytes, void** ws) {
+  struct Ws {
+    void* mem = nullptr;
+    size_t bytes = 0;
+  };
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, Ws> cache;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(e, "hipGetDevice: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(mu);
+  Ws& w = cache[std::make_pair(dev, stream)];
+  if (w.bytes < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return fail(e, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(hipErrorStreamCaptureUnsupported,
+                  "split-K workspace (%zu bytes) must be allocated before graph capture: run the same shape once "
+                  "on this stream outside capture",
+                  bytes);
+    const size_t nb = bytes > ((size_t)16 << 20) ? bytes : ((size_t)16 << 20);
+    if (w.mem) {
+      e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return fail(e, "hipStreamSynchronize: %s", hipGetErrorString(e));
+      e = hipFree(w.mem);
+      w.mem = nullptr;
+      w.bytes = 0;
+      if (e != hipSuccess) return fail(e, "hipFree: %s", hipGetErrorString(e));
+    }
+    e = hipMalloc(&w.mem, nb);
+    if (e != hipSuccess) {
+      w.mem = nullptr;
+      return fail(e, "split-K workspace of %zu bytes: %s", nb, hipGetErrorString(e));
+    }
+    w.bytes = nb;
+  }
+  *ws = w.mem;
+  return 0;
 }
 
 // Persistent grid for the large-M kernel: as many workgroups as can be resident at once
@@ -195,23 +272,41 @@ int check_common(const void* c, const void* a, const void* b, int M, int N, int 
   if ((long)(M + 256) * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N * 4 >= (1L << 31))
     return fail(hipErrorInvalidValue, "operand too large for 32-bit element offsets (M=%d N=%d K=%d)", M, N, K);
   if (M > 0 && (!c || !a || !b)) return fail(hipErrorInvalidValue, "null tensor pointer");
-  if (variant < -1 || variant >= kNumShapes) return fail(hipErrorInvalidValue, "unknown variant %d", variant);
+  if (variant < -1 || (variant >= 0 && ((variant & 0xFFFF) >= kNumShapes || (variant >> 24) != 0)))
+    return fail(hipErrorInvalidValue, "unknown variant %d", variant);
   return 0;
 }
 
-int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, hipStream_t stream) {
-  if (args.M == 0) return 0;
-  const int v = variant >= 0 ? variant : select_variant(args.M, args.N, args.K, kind, epi);
+// variant: -1 = the library's choice (tile and split count), else the variant index in bits
+// 0..15 and, for a split-K variant, the K split count in bits 16..23 (0 = automatic).
+int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args_in, hipStream_t stream) {
+  if (args_in.M == 0) return 0;
+  GemmArgs args = args_in;
+  const int v = variant >= 0 ? (variant & 0xFFFF) : select_variant(args.M, args.N, args.K, kind, epi);
+  const int ks_req = variant >= 0 ? (variant >> 16) & 0xFF : 0;
   const Shape& s = kShapes[v];
   if (s.family == FAM_DECODE && args.M > s.bm)
     return fail(hipErrorInvalidValue, "variant %s handles M <= %d, got M=%d", s.name, s.bm, args.M);
+  if (!s.split && ks_req > 1) return fail(hipErrorInvalidValue, "variant %s does not split K", s.name);
   const KernelFn* row = kernel_row(kind, epi, out_dtype);
   if (!row) return fail(hipErrorInvalidValue, "unsupported combination kind=%d epilogue=%d", kind, epi);
   dim3 grid;
   if (s.family == FAM_MAIN) {
     const long ntiles = (long)((args.M + s.bm - 1) / s.bm) * ((args.N + s.bn - 1) / s.bn);
+    const int nk = args.K / KT;
+    int ks = 1;
+    if (s.split) {
+      ks = ks_req ? ks_req : auto_splits(ntiles, nk);
+      if (ks > SPLIT_MAX || ks > nk)
+        return fail(hipErrorInvalidValue, "%d K splits: at most %d and at most K/128 = %d", ks, SPLIT_MAX, nk);
+      if (ks > 1) {
+        int rc = splitk_workspace(stream, (size_t)ks * args.M * args.N * 4, &args.ws);
+        if (rc) return rc;
+      }
+    }
+    args.ks = ks;
     int g = 0;
-    int rc = persistent_grid(row[v], s.threads, ntiles, &g);
+    int rc = persistent_grid(row[v], s.threads, ntiles * ks, &g);
     if (rc) return rc;
     grid = dim3(g);
   } else {
@@ -220,6 +315,12 @@ int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, 
   hipLaunchKernelGGL(row[v], grid, dim3(s.threads), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of %s failed: %s", s.name, hipGetErrorString(e));
+  if (args.ks > 1) {
+    const long quads = ((long)args.M * args.N) / 4;
+    hipLaunchKernelGGL(row[kNumShapes], dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, args);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(e, "launch of the split-K reduction failed: %s", hipGetErrorString(e));
+  }
   return 0;
 }
 
@@ -358,7 +459,9 @@ const char* flygemm_variant_name(int32_t v) {
 }
 
 int32_t flygemm_select_variant(int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t blockscale) {
-  return select_variant(M, N, K, in_dtype, blockscale ? EPI_BLOCK : EPI_ROWCOL);
+  // the kernels count K in bytes: two per element for 16-bit inputs, half for MXFP4
+  const int kb = (in_dtype == FLYGEMM_IN_BF16 || in_dtype == FLYGEMM_IN_FP16) ? 2 * K : (in_dtype == FLYGEMM_IN_FP4 ? K / 2 : K);
+  return select_variant(M, N, kb, in_dtype, blockscale ? EPI_BLOCK : EPI_ROWCOL);
 }
 
 const char* flygemm_last_error(void) { return g_err; }

@@ -120,6 +120,86 @@ def test_variants_ragged(gpu, kind, variant):
             assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
 
 
+# ---------------------------------------------------------------- split-K
+SPLIT = [i for i, n in enumerate(VARIANTS) if n.endswith("_splitk")]
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "fp8_block", "bf16"])
+@pytest.mark.parametrize("variant", SPLIT)
+@pytest.mark.parametrize("ks", [2, 3, 4, 8])
+def test_split_k_forced(gpu, kind, variant, ks):
+    """Forced K splits (bits 16..23 of the variant) on ragged shapes, including K ranges of
+    unequal length (ks not dividing K/128) and a split per K tile: int paths bit-exact (raw
+    accumulators and bf16 output), the rest within the bar.  Repeating the call gives the
+    same bits: the partial sums are added in split order whichever split finishes last."""
+    for (M, N, K) in [(100, 272, 1024), (130, 528, 2176), (7, 2112, 512)]:
+        if ks > K // 128:
+            continue
+        w = workloads.custom(kind, M, N, K, seed=M + N + K + ks, b_std=0.02 if kind == "int4" else 1.0)
+        ops = workloads.make_operands(w)
+        v = variant | (ks << 16)
+        _say(f"split-K {VARIANTS[variant]} ks={ks} {kind} {M}x{N}x{K}")
+        out = H.launch(ops, gpu, variant=v)
+        again = H.launch(ops, gpu, variant=v)
+        torch.cuda.synchronize()
+        assert torch.equal(out, again)
+        ref = H.check(ops, out)
+        if kind in ("int8", "int4"):
+            assert np.array_equal(H.raw_acc(ops, gpu, v).cpu().numpy(), ref)
+
+
+def test_split_k_two_streams_and_graph(gpu):
+    """Split-K launches on two streams at once (each stream has its own workspace), then the
+    same launch captured in a HIP graph after a warm-up outside capture: every replay, with
+    eager work in between, equals the eager result."""
+    names = VARIANTS
+    assert names[_lib.load().flygemm_select_variant(128, 4096, 4096, 0, 0)].endswith("_splitk")
+    opsA = workloads.make_operands(workloads.custom("int8", 128, 2048, 4096, seed=41))
+    opsB = workloads.make_operands(workloads.custom("int8", 128, 2048, 4096, seed=42))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    _say("split-K two streams")
+    outs = []
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            oa = H.launch(opsA, gpu, stream=s1)
+        with torch.cuda.stream(s2):
+            ob = H.launch(opsB, gpu, stream=s2)
+        outs.append((oa, ob))
+    torch.cuda.synchronize()
+    for oa, ob in outs:
+        H.check(opsA, oa)
+        H.check(opsB, ob)
+
+    _say("split-K graph replay")
+    ops = workloads.make_operands(workloads.custom("fp8", 128, 4096, 4096, seed=43))
+    eager = H.launch(ops, gpu)
+    torch.cuda.synchronize()
+    H.check(ops, eager)
+    a = ops["a"].to(gpu).view(torch.int8).view(-1)
+    b = ops["b_dev"].to(gpu).view(torch.int8).view(-1)
+    sa, sb = ops["sa"].to(gpu).view(-1), ops["sb"].to(gpu).view(-1)
+    c = torch.empty(128, 4096, dtype=torch.bfloat16, device=gpu)
+    from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
+    fn = compile_preshuffle_gemm_a8(K=4096, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(c.view(-1), a, b, sa, sb, 128, 4096, s)  # allocates this stream's workspace
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(c, eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        fn(c.view(-1), a, b, sa, sb, 128, 4096, s)
+    for i in range(3):
+        c.fill_(0)
+        H.launch(ops, gpu)  # eager split-K work on another stream between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, eager), f"replay {i}"
+
+
 @pytest.mark.parametrize("kind", ["fp8", "int8"])
 def test_odd_k_tile_count_and_fp16_out(gpu, kind):
     """K = 8320 = 65 K tiles (reference test shape), fp16 output."""

@@ -38,11 +38,17 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 0, 0)].startswith("decode_m1")
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
     # every shape gets a variant, and the five configurations get the tiles measured fastest
-    expect = {(128, 4096, 4096, 0, 0): "main_64x128_w1x4", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
+    expect = {(128, 4096, 4096, 0, 0): "main_64x128_w1x4_splitk", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
               (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_128x256_w2x4",
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
+    # split K only where the 64x128 tiles leave CUs idle and K has at least 32 K tiles
+    assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 0)] == "main_64x128_w1x4_splitk"
+    assert names[lib.flygemm_select_variant(128, 4096, 2048, 0, 0)] == "main_64x128_w1x4"
+    assert names[lib.flygemm_select_variant(256, 8192, 4096, 0, 0)] == "main_64x128_w1x4"
+    assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 1)] == "main_64x128_w1x4_splitk"
+    assert names[lib.flygemm_select_variant(128, 4096, 2048, 3, 0)] == "main_64x128_w1x4_splitk"  # 2 bytes/elt
     # MXFP4 decode keeps to at most 4 column blocks per workgroup
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 5, 0)] == "decode_m1_nb4_w8_u3"
     for m in (1, 17, 64, 65, 100, 1000, 5000):
@@ -66,6 +72,17 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc != 0 and b"in_dtype" in lib.flygemm_last_error()
     rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 256, 0, 0, 99, None)
     assert rc != 0 and b"variant" in lib.flygemm_last_error()
+    # split counts ride in bits 16..23 of the variant, for split-K variants only
+    names = _lib.variants()
+    sk, plain = names.index("main_64x128_w1x4_splitk"), names.index("main_64x128_w1x4")
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 1024, 0, 0, plain | (2 << 16), None)
+    assert rc != 0 and b"does not split K" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 2048, 0, 0, sk | (9 << 16), None)
+    assert rc != 0 and b"K splits" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 256, 0, 0, sk | (3 << 16), None)
+    assert rc != 0 and b"K splits" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 1024, 0, 0, sk | (1 << 24), None)
+    assert rc != 0 and b"unknown variant" in lib.flygemm_last_error()
     rc = lib.flygemm_blockscale(p, p, p, p, p, 16, 128, 256, 64, 0, -1, None)
     assert rc != 0 and b"scale_block_k" in lib.flygemm_last_error()
     rc = lib.flygemm_accumulators(p, p, p, -1, 128, 256, 0, -1, None)
