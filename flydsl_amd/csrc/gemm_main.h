@@ -53,6 +53,12 @@ struct MainCfg {
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB DMA instructions per wave per tile
   static constexpr int B_DMA = B_BYTES / 1024 / NW;
+  // LDS stages: three for the 4-wave tiles of at most 64x128 outputs (short steps), else two.
+  // Measured on MI355X: the third stage saves 4-18% on fp8/int8 shapes from 128x4096x4096 to
+  // 1024x7168x7168, but costs 12% on W4A8 256x14336x4096, whose half-size B steps are not
+  // waiting on their DMA.
+  static constexpr int NS = (NW == 4 && BM * BN <= 64 * 128 && KIND != KIND_INT4) ? 3 : 2;
+  static constexpr int DMA_PER_STEP = A_DMA + B_DMA;  // per wave, scale DMAs not counted
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "tile not divisible into wave DMAs");
 };
@@ -440,6 +446,54 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     kb_ = SPLIT ? s_ * nk / ks : 0;
     ke_ = SPLIT ? (s_ + 1) * nk / ks : nk;
   };
+  if constexpr (C::NS == 3) {
+    // Three LDS stages, the DMA two steps ahead (the 4-wave tiles, whose steps are short
+    // enough that one step of lead leaves them waiting on DMA latency).  A step's DMA is
+    // complete once no more than the next step's DMA_PER_STEP operations of this wave are
+    // outstanding (they retire in issue order); epilogue stores or the extra scale DMAs of
+    // some waves may make that wait longer, never too short.  The last issued step waits
+    // for everything.
+    __shared__ __attribute__((aligned(1024))) uint8_t lds2[STAGE];
+    auto ring = [&](int i) -> uint8_t* { return i == 0 ? lds0 : (i == 1 ? lds1 : lds2); };
+    int iw = blockIdx.x, ikt = 0, ike = 0;  // the next step to issue: item iw, K tile ikt
+    int im0 = 0, in0 = 0, idummy = 0;
+    if (iw < nitems) item(iw, im0, in0, ikt, ike, idummy);
+    int issued = 0;
+    auto issue_next = [&](int slot) {
+      issue(ring(slot), im0, in0, ikt);
+      ++issued;
+      if (++ikt == ike) {
+        iw += G;
+        if (iw < nitems) item(iw, im0, in0, ikt, ike, idummy);
+      }
+    };
+    if (iw < nitems) issue_next(0);
+    if (iw < nitems) issue_next(1);
+    int step = 0, slot = 0;
+    for (int w = blockIdx.x; w < nitems; w += G) {
+      int m0, n0, kb, ke, s;
+      item(w, m0, n0, kb, ke, s);
+#pragma unroll
+      for (int i = 0; i < MR; ++i)
+#pragma unroll
+        for (int j = 0; j < NR; ++j) acc[i][j] = AccT{0, 0, 0, 0};
+      for (int kt = kb; kt < ke; ++kt, ++step) {
+        if (issued > step + 1)
+          waitcnt<C::DMA_PER_STEP>();
+        else
+          wait_dma();
+        workgroup_barrier();  // step's stage is published; every wave is done with step-1's
+        if (iw < nitems) issue_next(slot == 0 ? 2 : slot - 1);  // the stage step-1 used
+        compute(ring(slot));
+        slot = slot == 2 ? 0 : slot + 1;
+      }
+      if (ks > 1)
+        store_partial(s, m0, n0);
+      else
+        epilogue(m0, n0);
+    }
+    return;
+  }
   int w = blockIdx.x;
   int m0, n0, kb, ke, s;
   item(w, m0, n0, kb, ke, s);
