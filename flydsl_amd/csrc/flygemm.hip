@@ -168,13 +168,15 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   }
   // main family: the first tile in a measured preference list that gives enough workgroups
   // to occupy the chip (256 CUs).  The blockscale epilogue's per-K-tile rescale needs more
-  // registers, which makes the 8-wave 128x256 tile its best; elsewhere 256x256 wins when it
-  // fills the chip and the 4-wave 64x128 tile (two resident per CU) wins below that.
+  // registers, which makes the 8-wave 256x128 tile its best; elsewhere 256x256 wins when it
+  // fills the chip, 128x128 when it gives more than one tile per CU (272+: at 256 tiles the
+  // 64x128 tile is still 3-25% faster, at 280-448 tiles 128x128 is 20-40% faster), and the
+  // 4-wave 64x128 tile (two resident per CU) below that.
   struct Pref {
     int bm, bn, threads, min_wg;
   };
-  static const Pref kRowcol[] = {{256, 256, 512, 240}, {128, 256, 512, 240}, {128, 128, 256, 480}, {64, 128, 256, 0}};
-  static const Pref kBlock[] = {{128, 256, 512, 200}, {128, 128, 256, 240}, {64, 128, 256, 0}};
+  static const Pref kRowcol[] = {{256, 256, 512, 240}, {128, 256, 512, 240}, {128, 128, 256, 272}, {64, 128, 256, 0}};
+  static const Pref kBlock[] = {{256, 128, 512, 200}, {128, 128, 256, 240}, {64, 128, 256, 0}};
   const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
   const int n = epi == EPI_BLOCK ? 3 : 4;
   for (int i = 0; i < n; ++i) {

@@ -39,10 +39,13 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
     # every shape gets a variant, and the five configurations get the tiles measured fastest
     expect = {(128, 4096, 4096, 0, 0): "main_64x128_w1x4_splitk", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
-              (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_128x256_w2x4",
+              (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_256x128_w2x4",
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
+    # 128x128 once it gives more than one tile per CU
+    assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
     # split K only where the 64x128 tiles leave CUs idle and K has at least 32 K tiles
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 0)] == "main_64x128_w1x4_splitk"
     assert names[lib.flygemm_select_variant(128, 4096, 2048, 0, 0)] == "main_64x128_w1x4"
