@@ -192,10 +192,11 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   return -1;
 }
 
-// Split-K workspace per (device, stream): the ks partial-sum slices, grown on demand and kept
-// for the life of the process.  Each stream has its own, so launches that run concurrently on
-// different streams never share one; launches on one stream run in order.  Growing it
-// allocates (and waits for the stream), so it refuses to happen under graph capture.
+// Split-K workspace per (device, stream): the ks partial-sum slices, grown on demand.  Each
+// stream has its own, so launches that run concurrently on different streams never share one;
+// launches on one stream run in order.  A workspace is never freed: kernels still queued, or a
+// graph captured earlier, may reference it, so growing allocates a larger one and keeps the old
+// one until the process ends.  Growing allocates, so it refuses to happen under graph capture.
 int splitk_workspace(hipStream_t stream, size_t bytes, void** ws) {
   struct Ws {
     void* mem = nullptr;
@@ -218,19 +219,10 @@ int splitk_workspace(hipStream_t stream, size_t bytes, void** ws) {
                   "on this stream outside capture",
                   bytes);
     const size_t nb = bytes > ((size_t)16 << 20) ? bytes : ((size_t)16 << 20);
-    if (w.mem) {
-      e = hipStreamSynchronize(stream);
-      if (e != hipSuccess) return fail(e, "hipStreamSynchronize: %s", hipGetErrorString(e));
-      e = hipFree(w.mem);
-      w.mem = nullptr;
-      w.bytes = 0;
-      if (e != hipSuccess) return fail(e, "hipFree: %s", hipGetErrorString(e));
-    }
-    e = hipMalloc(&w.mem, nb);
-    if (e != hipSuccess) {
-      w.mem = nullptr;
-      return fail(e, "split-K workspace of %zu bytes: %s", nb, hipGetErrorString(e));
-    }
+    void* mem = nullptr;
+    e = hipMalloc(&mem, nb);
+    if (e != hipSuccess) return fail(e, "split-K workspace of %zu bytes: %s", nb, hipGetErrorString(e));
+    w.mem = mem;  // the previous one (if any) stays allocated: see above
     w.bytes = nb;
   }
   *ws = w.mem;

@@ -13,9 +13,10 @@
  *    exception: a split-K launch (chosen for M > 64 when the output has at most 128 tiles of
  *    64x128, or forced through `variant`) writes ks fp32/int32 partial sums per output to a
  *    workspace that the library allocates the first time a stream needs it (at least 16 MiB,
- *    one per device and stream, kept until the process ends), then launches a second kernel
- *    that adds them in split order and applies the epilogue; growing the workspace
- *    synchronizes that stream and is refused while the stream is being captured into a graph.
+ *    one per device and stream; a larger call allocates a larger one, and none is ever freed
+ *    before the process ends, since queued kernels or captured graphs may still use it), then
+ *    launches a second kernel that adds them in split order and applies the epilogue.
+ *    Allocating is refused while the stream is being captured into a graph.
  *  - A is row-major [M][K] bytes.  B is the preshuffled [N][K] buffer produced by the
  *    reference's `shuffle_weight(b, layout=(16, 16))` (tests/utils.py:76-96): element
  *    (n, k) at byte (n/16)*16*K + (k/16)*256 + (n%16)*16 + (k%16).  INT4 B is that buffer
