@@ -153,12 +153,14 @@ int auto_splits(long ntiles, int nk) {
 
 int select_variant(int M, int N, int K, int kind, int epi) {
   // The decode family wins up to 16 rows; above that its per-row A traffic grows and the
-  // 64x128 tile (split-K when few tiles) is faster for fp8/int8/int4 with per-row scales:
-  // measured on MI355X for N x K in {28672x8192, 4096x4096, 7168x2048, 14336x4096 (int4),
-  // 8192x8192 (int8)}, 1.0-1.2x at 33-64 rows and 1.3-1.8x at 48-64 rows of the widest N; at
-  // 17-32 rows only the widest N (at least 200 column tiles of 128) prefers the tile.
-  const bool tile_small_m = epi == EPI_ROWCOL && (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_INT4) &&
-                            (M > 32 || (M > 16 && (N + 127) / 128 >= 200));
+  // 64x128 tile (split-K when few tiles) is faster above 32 rows -- and above 16 rows when N
+  // has at least 200 column tiles of 128, or at least 32 with the blockscale epilogue.
+  // Measured on MI355X for every kind: fp8/int8/int4 (N x K = 28672x8192, 4096x4096, 7168x2048,
+  // 14336x4096, 8192x8192), bf16 and MXFP4 (28672x8192, 8192x8192), blockscale (7168x7168,
+  // 2112x7168); e.g. 64x28672x8192 fp8 43.8 µs against 77.4, bf16 86 against 144,
+  // blockscale 64x7168x7168 18.1 against 33.2.
+  const int ncol = (N + 127) / 128;
+  const bool tile_small_m = M > 32 || (M > 16 && (ncol >= 200 || (epi == EPI_BLOCK && ncol >= 32)));
   if (M <= 64 && !tile_small_m) {
     // decode family: fewest rows that cover M, then the most column blocks per workgroup
     // that still leaves about one workgroup per CU

@@ -43,15 +43,17 @@ def test_variant_table():
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
-    # 17-64 rows: decode only up to 16 rows (32 for N below 200 column tiles of 128), for the
-    # per-row-scaled 8-bit kinds; others keep the decode family up to 64 rows
+    # 17-64 rows: decode only up to 32 rows (16 for very wide N, or blockscale with 32+ column
+    # tiles); the 64x128 tile (split-K when few tiles) above
     assert names[lib.flygemm_select_variant(64, 28672, 8192, 0, 0)] == "main_64x128_w1x4"
     assert names[lib.flygemm_select_variant(32, 28672, 8192, 0, 0)] == "main_64x128_w1x4"
     assert names[lib.flygemm_select_variant(32, 8192, 8192, 1, 0)].startswith("decode_m2")
     assert names[lib.flygemm_select_variant(48, 8192, 8192, 1, 0)] == "main_64x128_w1x4_splitk"
     assert names[lib.flygemm_select_variant(64, 7168, 2048, 2, 0)] == "main_64x128_w1x4"
-    assert names[lib.flygemm_select_variant(64, 8192, 8192, 3, 0)].startswith("decode_m4")
-    assert names[lib.flygemm_select_variant(64, 8192, 8192, 0, 1)].startswith("decode_m4")
+    assert names[lib.flygemm_select_variant(64, 8192, 8192, 3, 0)] == "main_64x128_w1x4_splitk"
+    assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "main_64x128_w1x4_splitk"
+    assert names[lib.flygemm_select_variant(32, 2112, 7168, 0, 1)].startswith("decode_m2")
+    assert names[lib.flygemm_select_variant(16, 7168, 7168, 0, 1)].startswith("decode_m1")
     # 128x128 once it gives more than one tile per CU
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x128_w2x2"
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
