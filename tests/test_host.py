@@ -54,6 +54,10 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "main_64x128_w1x4_splitk"
     assert names[lib.flygemm_select_variant(32, 2112, 7168, 0, 1)].startswith("decode_m2")
     assert names[lib.flygemm_select_variant(16, 7168, 7168, 0, 1)].startswith("decode_m1")
+    # 256x256 from about 160 tiles, then 128x128 from 272
+    assert names[lib.flygemm_select_variant(1536, 8192, 8192, 0, 0)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(512, 28672, 8192, 0, 0)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(1024, 8192, 8192, 0, 0)] == "main_128x128_w2x2"
     # 128x128 once it gives more than one tile per CU
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x128_w2x2"
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
