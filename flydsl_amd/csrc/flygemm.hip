@@ -176,8 +176,7 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     return best;
   }
   // main family: the first tile in a measured preference list that gives enough workgroups
-  // to occupy the chip (256 CUs).  The blockscale epilogue's per-K-tile rescale needs more
-  // registers, which makes the 8-wave 256x128 tile its best; elsewhere 256x256 wins from about
+  // to occupy the chip (256 CUs).  Without the blockscale epilogue 256x256 wins from about
   // 160 tiles (1536x8192x8192: 88 µs against 110 for 128x256; 512x28672x8192: 113 against
   // 166), 128x128 when it gives more than one tile per CU (272+: at 256 tiles the 64x128 tile
   // is still 3-25% faster, at 280-512 tiles 128x128 is 4-40% faster), and the 4-wave 64x128
@@ -186,9 +185,12 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     int bm, bn, threads, min_wg;
   };
   static const Pref kRowcol[] = {{256, 256, 512, 160}, {128, 128, 256, 272}, {64, 128, 256, 0}};
-  static const Pref kBlock[] = {{256, 128, 512, 200}, {128, 128, 256, 240}, {64, 128, 256, 0}};
+  // blockscale (measured on M = 128-4096 with N x K = 7168x7168, 2112x7168, 3072x1536,
+  // 24576x1536): 256x256 from 200 tiles (4096x24576x1536: 196 µs against 231 for 256x128),
+  // 256x128 from 160, 128x128 from 240
+  static const Pref kBlock[] = {{256, 256, 512, 200}, {256, 128, 512, 160}, {128, 128, 256, 240}, {64, 128, 256, 0}};
   const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
-  const int n = 3;
+  const int n = epi == EPI_BLOCK ? 4 : 3;
   for (int i = 0; i < n; ++i) {
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg) continue;

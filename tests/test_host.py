@@ -54,6 +54,9 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "main_64x128_w1x4_splitk"
     assert names[lib.flygemm_select_variant(32, 2112, 7168, 0, 1)].startswith("decode_m2")
     assert names[lib.flygemm_select_variant(16, 7168, 7168, 0, 1)].startswith("decode_m1")
+    # blockscale: 256x256 from 200 tiles, 256x128 from 160
+    assert names[lib.flygemm_select_variant(2048, 7168, 7168, 0, 1)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(2048, 3072, 1536, 0, 1)] == "main_256x128_w2x4"
     # 256x256 from about 160 tiles, then 128x128 from 272
     assert names[lib.flygemm_select_variant(1536, 8192, 8192, 0, 0)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(512, 28672, 8192, 0, 0)] == "main_256x256_w2x4"
