@@ -171,7 +171,10 @@ int select_variant(int M, int N, int K, int kind, int epi) {
       if (kShapes[v].bm != rows) continue;
       const int nbw = kShapes[v].bn / 16;
       if (kind == KIND_FP4 && nbw > 4) continue;  // MXFP4's scale words push 7 blocks past the register file
-      if (best < 0 || (nblk / nbw >= 240 && nbw > kShapes[best].bn / 16)) best = v;
+      // int4 blocks carry half the bytes: 4 blocks per workgroup beat 2 even at 224 workgroups
+      // (16x14336x4096: 7.6 µs against 8.5)
+      const int min_wg = kind == KIND_INT4 ? 200 : 240;
+      if (best < 0 || (nblk / nbw >= min_wg && nbw > kShapes[best].bn / 16)) best = v;
     }
     return best;
   }

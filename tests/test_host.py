@@ -70,6 +70,9 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(256, 8192, 4096, 0, 0)] == "main_64x128_w1x4"
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 1)] == "main_64x128_w1x4_splitk"
     assert names[lib.flygemm_select_variant(128, 4096, 2048, 3, 0)] == "main_64x128_w1x4_splitk"  # 2 bytes/elt
+    # int4 decode takes more column blocks per workgroup (half-size blocks)
+    assert names[lib.flygemm_select_variant(16, 14336, 4096, 2, 0)] == "decode_m1_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(16, 14336, 4096, 1, 0)] == "decode_m1_nb2_w8_u4"
     # MXFP4 decode keeps to at most 4 column blocks per workgroup
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 5, 0)] == "decode_m1_nb4_w8_u3"
     for m in (1, 17, 64, 65, 100, 1000, 5000):
