@@ -93,10 +93,11 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (R == 1 && (tile_n == 128 || tile_n == 256)) {
     const long runs1 = est_runs(tokens, topk, experts, tile_m, 1);
     while (tile_n > 64 && runs1 * (N / tile_n) < 256 && N % (tile_n / 2) == 0) tile_n /= 2;
-    // stage 2 of a decode-sized routing (up to 512 routes): 64-column tiles, whose short
-    // weight streams finish together (DS-V3 dims, 8 tokens top-8: 19.8 µs against 27.2 at 256
-    // columns; 32 tokens: 71.8 against 76.6; from 128 tokens on the difference is within +-7%)
-    if (stage == 2 && routes <= 512 && N % 64 == 0) tile_n = 64;
+    // decode-sized routings (stage 2 up to 512 routes, stage 1 up to 256): 64-column tiles,
+    // whose short weight streams finish together (DS-V3 dims, top-8: stage 2 at 8 tokens 19.8
+    // µs against 27.2 with 256 columns, at 32 tokens 71.8 against 76.6; stage 1 at 32 tokens
+    // 101 against 115; from 128 tokens on the wider tiles are within +-7%)
+    if (routes <= (stage == 2 ? 512 : 256) && N % 64 == 0) tile_n = 64;
   }
   if (tile_n != 64 && tile_n != 128 && tile_n != 256)
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
