@@ -80,16 +80,33 @@ class Runner:
         j = i % self.copies
         self.fn(self.c.view(-1), self.a[j], self.b[j], self.sa, self.sb, self.w.M, self.w.N, stream)
 
-    def time(self, steps, warmup):
+    def time(self, steps, warmup, graph=False):
+        """Average milliseconds per launch over ``steps`` launches, timed with HIP events on
+        the launch stream.  ``graph``: the launches are captured once into a HIP graph and
+        the timed region replays it, so a kernel shorter than the host's per-call cost
+        (about 9 us through the Python launcher) is timed at its own rate rather than at
+        the rate the host can issue calls."""
         stream = torch.cuda.current_stream()
         for i in range(warmup):
             self.launch(i, stream)
         torch.cuda.synchronize()
+        g = None
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cap = torch.cuda.current_stream()
+                for i in range(steps):
+                    self.launch(i, cap)
+            g.replay()  # first replay uploads the graph
+            torch.cuda.synchronize()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         start.record(stream)
-        for i in range(steps):
-            self.launch(i, stream)
+        if g is not None:
+            g.replay()
+        else:
+            for i in range(steps):
+                self.launch(i, stream)
         end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0

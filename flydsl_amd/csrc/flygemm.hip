@@ -3,7 +3,8 @@
 // Every entry point validates its arguments on the host, picks a kernel variant (or uses
 // the one the caller names), launches asynchronously on the caller's stream and returns 0
 // or a nonzero error code; the message of the last failure on the calling thread is
-// returned by flygemm_last_error().  Nothing here allocates device memory or synchronizes.
+// returned by flygemm_last_error().  Nothing here allocates device memory or synchronizes,
+// and every GEMM is one kernel launch.
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -44,8 +45,8 @@ enum Family { FAM_MAIN = 0, FAM_DECODE = 1 };
 struct Shape {
   const char* name;
   int family;
-  int bm, bn, threads;  // main: workgroup tile; decode: bm = 16*MR rows, bn = 16*NBW cols
-  bool split;           // main family with split-K
+  int bm, bn, threads;  // main: workgroup tile; decode/rows: bm = 16*MR rows, bn = 16*NBW cols
+  bool rows;            // row-blocked streaming variant (chosen for M > 64 with few output tiles)
 };
 
 // Ordered by preference: the selector takes the first tile that yields enough workgroups.
@@ -57,13 +58,6 @@ struct Shape {
   X(256, 128, 2, 4)    \
   X(128, 256, 2, 4)    \
   X(256, 64, 4, 1)     \
-  X(128, 64, 2, 2)
-
-// Split-K tiles (the main kernel with SPLIT): for M too small to give every CU a tile.  Only
-// tiles whose waves hold 8 accumulator tiles, so the fixup's SPLIT_MAX partial sets fit in
-// registers next to the accumulators.
-#define SPLIT_SHAPES(X) \
-  X(64, 128, 1, 4)    \
   X(128, 64, 2, 2)
 
 #define DECODE_SHAPES(X) \
@@ -78,25 +72,36 @@ struct Shape {
   X(8, 1, 8, 2)          \
   X(8, 2, 8, 1)
 
+// The streaming kernel over row blocks (plain B loads: the row blocks of a column group re-read
+// B from L2): for M too large for one row block but too small for the tiled kernel to give
+// every CU an output tile (e.g. 128 x 4096: 64 tiles of 64x128).  (MR, NBW, waves, unroll).
+#define ROW_SHAPES(X) \
+  X(1, 4, 8, 3)       \
+  X(2, 2, 8, 4)       \
+  X(2, 4, 8, 3)
+
 const Shape kShapes[] = {
 #define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64, false},
     MAIN_SHAPES(MS)
 #undef MS
-#define SS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN "_splitk", FAM_MAIN, BM, BN, WM * WN * 64, true},
-        SPLIT_SHAPES(SS)
-#undef SS
 #define DS(MR, NBW, NW, U) {"decode_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, false},
-            DECODE_SHAPES(DS)
+        DECODE_SHAPES(DS)
 #undef DS
+#define RS(MR, NBW, NW, U) {"rows_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, true},
+            ROW_SHAPES(RS)
+#undef RS
 };
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 #define COUNT(...) +1
-constexpr int kFirstSplit = 0 MAIN_SHAPES(COUNT);
-constexpr int kFirstDecode = kFirstSplit SPLIT_SHAPES(COUNT);
+constexpr int kFirstDecode = 0 MAIN_SHAPES(COUNT);
+constexpr int kFirstRows = kFirstDecode DECODE_SHAPES(COUNT);
 #undef COUNT
+// at most this many 64x128 output tiles: the row-blocked streaming kernel instead (it is 1.7-2x
+// faster at 64 tiles and level at 128: 256x4096x4096 15.9 us against 15.6, 96x8192x8192 33.6
+// against 32.4)
+constexpr long kRowsMaxTiles = 96;
 
-// One row of kernels per (kind, epilogue, output dtype) combination, one column per shape,
-// then the split-K reduce kernel of that combination (index kNumShapes).
+// One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
 struct KernelRow {
   static const KernelFn* get() {
@@ -104,15 +109,14 @@ struct KernelRow {
 #define MS(BM, BN, WM, WN) gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16>,
         MAIN_SHAPES(MS)
 #undef MS
-#define SS(BM, BN, WM, WN) gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16, true>,
-            SPLIT_SHAPES(SS)
-#undef SS
-#define DS(MR, NBW, NW, U) gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI, BF16>,
+#define DS(MR, NBW, NW, U) gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI, BF16, true>,
             DECODE_SHAPES(DS)
 #undef DS
-        splitk_reduce_kernel<KIND, EPI, BF16>,
+#define RS(MR, NBW, NW, U) gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI, BF16, false>,
+                ROW_SHAPES(RS)
+#undef RS
     };
-    static_assert(sizeof(fns) / sizeof(fns[0]) == kNumShapes + 1, "variant table mismatch");
+    static_assert(sizeof(fns) / sizeof(fns[0]) == kNumShapes, "variant table mismatch");
     return fns;
   }
 };
@@ -139,26 +143,29 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
   return nullptr;
 }
 
-// Automatic split count for a split-K variant (measured on MI355X for 32..128 tiles of 64x128
-// and K = 4096..8192): 4 splits, 8 when there are at most 32 tiles, and at least 8 K tiles
-// per split.
-constexpr int kSplitMinK = 8;
-int auto_splits(long ntiles, int nk) {
-  long ks = 256 / (ntiles > 0 ? ntiles : 1);
-  if (ks < 4) ks = 4;
-  if (ks > SPLIT_MAX) ks = SPLIT_MAX;
-  if (ks > nk / kSplitMinK) ks = nk / kSplitMinK;
-  return ks < 1 ? 1 : (int)ks;
+// Row-blocked streaming variant for an output too small for the tiled kernel to occupy the
+// chip.  Every workgroup of (16*MR) x (16*NBW) outputs reads (16*MR + 16*NBW) * K bytes from L2
+// (or HBM), so for 256 workgroups 32x64 blocks move the fewest bytes.  Measured on MI355X
+// (kernel time, graph replay): 128x4096x4096 fp8 8.9 us (64x128 tiles: 15.3, 32x32 blocks:
+// 13.3), the same shape int8/int4/bf16 8.8/8.9/15.9 against 16.0/17.3/30.2, 200x2048x8192 fp8
+// 14.2 against 26.8.  Blockscale and MXFP4 keep MR = 1: their per-tile scales make the 32-row
+// block spill registers (blockscale 256x2112x7168: 16x64 blocks 25.1 us, 32x64 37.1, 64x128
+// tiles 40.6; MXFP4 128x4096x4096: 9.1 against 10.9).
+int select_rows(int kind, int epi) {
+  const int mr = (epi == EPI_BLOCK || kind == KIND_FP4) ? 1 : 2;
+  for (int v = kFirstRows; v < kNumShapes; ++v)
+    if (kShapes[v].bm == 16 * mr && kShapes[v].bn == 64) return v;
+  return -1;
 }
 
 int select_variant(int M, int N, int K, int kind, int epi) {
   // The decode family wins up to 16 rows; above that its per-row A traffic grows and the
-  // 64x128 tile (split-K when few tiles) is faster above 32 rows -- and above 16 rows when N
-  // has at least 200 column tiles of 128, or at least 32 with the blockscale epilogue.
-  // Measured on MI355X for every kind: fp8/int8/int4 (N x K = 28672x8192, 4096x4096, 7168x2048,
-  // 14336x4096, 8192x8192), bf16 and MXFP4 (28672x8192, 8192x8192), blockscale (7168x7168,
-  // 2112x7168); e.g. 64x28672x8192 fp8 43.8 µs against 77.4, bf16 86 against 144,
-  // blockscale 64x7168x7168 18.1 against 33.2.
+  // 64x128 tile is faster above 32 rows -- and above 16 rows when N has at least 200 column
+  // tiles of 128, or at least 32 with the blockscale epilogue.  Measured on MI355X for every
+  // kind: fp8/int8/int4 (N x K = 28672x8192, 4096x4096, 7168x2048, 14336x4096, 8192x8192),
+  // bf16 and MXFP4 (28672x8192, 8192x8192), blockscale (7168x7168, 2112x7168); e.g.
+  // 64x28672x8192 fp8 43.8 us against 77.4, bf16 86 against 144, blockscale 64x7168x7168 18.1
+  // against 33.2.
   const int ncol = (N + 127) / 128;
   const bool tile_small_m = M > 32 || (M > 16 && (ncol >= 200 || (epi == EPI_BLOCK && ncol >= 32)));
   if (M <= 64 && !tile_small_m) {
@@ -167,12 +174,12 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     const int rows = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
     const int nblk = N / 16;
     int best = -1;
-    for (int v = kFirstDecode; v < kNumShapes; ++v) {
+    for (int v = kFirstDecode; v < kFirstRows; ++v) {
       if (kShapes[v].bm != rows) continue;
       const int nbw = kShapes[v].bn / 16;
       if (kind == KIND_FP4 && nbw > 4) continue;  // MXFP4's scale words push 7 blocks past the register file
       // int4 blocks carry half the bytes: 4 blocks per workgroup beat 2 even at 224 workgroups
-      // (16x14336x4096: 7.6 µs against 8.5)
+      // (16x14336x4096: 7.6 us against 8.5)
       const int min_wg = kind == KIND_INT4 ? 200 : 240;
       if (best < 0 || (nblk / nbw >= min_wg && nbw > kShapes[best].bn / 16)) best = v;
     }
@@ -180,7 +187,7 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   }
   // main family: the first tile in a measured preference list that gives enough workgroups
   // to occupy the chip (256 CUs).  Without the blockscale epilogue 256x256 wins from about
-  // 160 tiles (1536x8192x8192: 88 µs against 110 for 128x256; 512x28672x8192: 113 against
+  // 160 tiles (1536x8192x8192: 88 us against 110 for 128x256; 512x28672x8192: 113 against
   // 166), 128x128 when it gives more than one tile per CU (272+: at 256 tiles the 64x128 tile
   // is still 3-25% faster, at 280-512 tiles 128x128 is 4-40% faster), and the 4-wave 64x128
   // tile (two resident per CU) below that.  128x256 was never the fastest in these sweeps.
@@ -189,7 +196,7 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   };
   static const Pref kRowcol[] = {{256, 256, 512, 160}, {128, 128, 256, 272}, {64, 128, 256, 0}};
   // blockscale (measured on M = 128-4096 with N x K = 7168x7168, 2112x7168, 3072x1536,
-  // 24576x1536): 256x256 from 200 tiles (4096x24576x1536: 196 µs against 231 for 256x128),
+  // 24576x1536): 256x256 from 200 tiles (4096x24576x1536: 196 us against 231 for 256x128),
   // 256x128 from 160, 128x128 from 240
   static const Pref kBlock[] = {{256, 256, 512, 200}, {256, 128, 512, 160}, {128, 128, 256, 240}, {64, 128, 256, 0}};
   const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
@@ -197,51 +204,13 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   for (int i = 0; i < n; ++i) {
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg) continue;
-    // the last resort (64x128) leaves CUs idle when there are at most 128 tiles: split K
-    // across workgroups when K has at least 32 K tiles (shorter K gains nothing measurable)
-    const bool split = list[i].min_wg == 0 && wg <= 128 && K / KT >= 32;
-    const int v0 = split ? kFirstSplit : 0, v1 = split ? kFirstDecode : kFirstSplit;
-    for (int v = v0; v < v1; ++v)
+    // the last resort (64x128) leaves CUs idle when there are at most 128 tiles: the
+    // row-blocked streaming kernel spreads the output over every CU instead
+    if (list[i].min_wg == 0 && wg <= kRowsMaxTiles) return select_rows(kind, epi);
+    for (int v = 0; v < kFirstDecode; ++v)
       if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }
   return -1;
-}
-
-// Split-K workspace per (device, stream): the ks partial-sum slices, grown on demand.  Each
-// stream has its own, so launches that run concurrently on different streams never share one;
-// launches on one stream run in order.  A workspace is never freed: kernels still queued, or a
-// graph captured earlier, may reference it, so growing allocates a larger one and keeps the old
-// one until the process ends.  Growing allocates, so it refuses to happen under graph capture.
-int splitk_workspace(hipStream_t stream, size_t bytes, void** ws) {
-  struct Ws {
-    void* mem = nullptr;
-    size_t bytes = 0;
-  };
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, Ws> cache;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return fail(e, "hipGetDevice: %s", hipGetErrorString(e));
-  std::lock_guard<std::mutex> lock(mu);
-  Ws& w = cache[std::make_pair(dev, stream)];
-  if (w.bytes < bytes) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(stream, &cs);
-    if (e != hipSuccess) return fail(e, "hipStreamIsCapturing: %s", hipGetErrorString(e));
-    if (cs != hipStreamCaptureStatusNone)
-      return fail(hipErrorStreamCaptureUnsupported,
-                  "split-K workspace (%zu bytes) must be allocated before graph capture: run the same shape once "
-                  "on this stream outside capture",
-                  bytes);
-    const size_t nb = bytes > ((size_t)16 << 20) ? bytes : ((size_t)16 << 20);
-    void* mem = nullptr;
-    e = hipMalloc(&mem, nb);
-    if (e != hipSuccess) return fail(e, "split-K workspace of %zu bytes: %s", nb, hipGetErrorString(e));
-    w.mem = mem;  // the previous one (if any) stays allocated: see above
-    w.bytes = nb;
-  }
-  *ws = w.mem;
-  return 0;
 }
 
 // Persistent grid for the large-M kernel: as many workgroups as can be resident at once
@@ -281,55 +250,35 @@ int check_common(const void* c, const void* a, const void* b, int M, int N, int 
   if ((long)(M + 256) * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N * 4 >= (1L << 31))
     return fail(hipErrorInvalidValue, "operand too large for 32-bit element offsets (M=%d N=%d K=%d)", M, N, K);
   if (M > 0 && (!c || !a || !b)) return fail(hipErrorInvalidValue, "null tensor pointer");
-  if (variant < -1 || (variant >= 0 && ((variant & 0xFFFF) >= kNumShapes || (variant >> 24) != 0)))
-    return fail(hipErrorInvalidValue, "unknown variant %d", variant);
+  if (variant < -1 || variant >= kNumShapes) return fail(hipErrorInvalidValue, "unknown variant %d", variant);
   return 0;
 }
 
-// variant: -1 = the library's choice (tile and split count), else the variant index in bits
-// 0..15 and, for a split-K variant, the K split count in bits 16..23 (0 = automatic).
-int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args_in, hipStream_t stream) {
-  if (args_in.M == 0) return 0;
-  GemmArgs args = args_in;
-  const int v = variant >= 0 ? (variant & 0xFFFF) : select_variant(args.M, args.N, args.K, kind, epi);
-  const int ks_req = variant >= 0 ? (variant >> 16) & 0xFF : 0;
+// variant: -1 = the library's choice, else the index of a variant in the table.
+int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, hipStream_t stream) {
+  if (args.M == 0) return 0;
+  const int v = variant >= 0 ? variant : select_variant(args.M, args.N, args.K, kind, epi);
+  if (v < 0 || v >= kNumShapes)
+    return fail(hipErrorInvalidValue, "no kernel variant for M=%d N=%d K=%d", args.M, args.N, args.K);
   const Shape& s = kShapes[v];
-  if (s.family == FAM_DECODE && args.M > s.bm)
-    return fail(hipErrorInvalidValue, "variant %s handles M <= %d, got M=%d", s.name, s.bm, args.M);
-  if (!s.split && ks_req > 1) return fail(hipErrorInvalidValue, "variant %s does not split K", s.name);
   const KernelFn* row = kernel_row(kind, epi, out_dtype);
   if (!row) return fail(hipErrorInvalidValue, "unsupported combination kind=%d epilogue=%d", kind, epi);
   dim3 grid;
   if (s.family == FAM_MAIN) {
     const long ntiles = (long)((args.M + s.bm - 1) / s.bm) * ((args.N + s.bn - 1) / s.bn);
-    const int nk = args.K / KT;
-    int ks = 1;
-    if (s.split) {
-      ks = ks_req ? ks_req : auto_splits(ntiles, nk);
-      if (ks > SPLIT_MAX || ks > nk)
-        return fail(hipErrorInvalidValue, "%d K splits: at most %d and at most K/128 = %d", ks, SPLIT_MAX, nk);
-      if (ks > 1) {
-        int rc = splitk_workspace(stream, (size_t)ks * args.M * args.N * 4, &args.ws);
-        if (rc) return rc;
-      }
-    }
-    args.ks = ks;
     int g = 0;
-    int rc = persistent_grid(row[v], s.threads, ntiles * ks, &g);
+    int rc = persistent_grid(row[v], s.threads, ntiles, &g);
     if (rc) return rc;
     grid = dim3(g);
   } else {
-    grid = dim3((args.N + s.bn - 1) / s.bn);
+    // one workgroup per (row block, column group); a decode shape normally has one row block
+    const long nrb = (args.M + s.bm - 1) / s.bm;
+    const long ncg = (args.N / 16 + s.bn / 16 - 1) / (s.bn / 16);
+    grid = dim3((unsigned)(nrb * ncg));
   }
   hipLaunchKernelGGL(row[v], grid, dim3(s.threads), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of %s failed: %s", s.name, hipGetErrorString(e));
-  if (args.ks > 1) {
-    const long quads = ((long)args.M * args.N) / 4;
-    hipLaunchKernelGGL(row[kNumShapes], dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, args);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(e, "launch of the split-K reduction failed: %s", hipGetErrorString(e));
-  }
   return 0;
 }
 

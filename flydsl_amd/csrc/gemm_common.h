@@ -158,10 +158,6 @@ struct GemmArgs {
   const float* sa;    // EPI_ROWCOL: [M]; EPI_BLOCK: [K/128][M]
   const float* sb;    // EPI_ROWCOL: [N]; EPI_BLOCK: [ceil(N/128)][K/128]
   int M, N, K;
-  // split-K kernels only: ks K ranges per output tile and the partial-sum workspace
-  // ws[ks][M][N] (int32 or fp32)
-  int ks;
-  void* ws;
 };
 
 }  // namespace flygemm

@@ -1,24 +1,40 @@
-// Small-M (decode) kernel: B is streamed from HBM straight into MFMA operand registers.
+// Small-M kernel: B is streamed from HBM straight into MFMA operand registers.
 //
-// For M <= 16*MR the whole of A (a few hundred KB at most) is L2-resident, so the kernel is
-// bound by reading B once.  A workgroup owns NBW 16-column blocks and all M rows; its NW
-// waves split K (wave w takes K tiles w, w+NW, ...), each wave keeps UNROLL-1 K tiles of
-// loads in flight ahead of the one it multiplies, and the NW partial accumulators are
-// summed through LDS before the fused epilogue.  The reduction is inside the workgroup: no workspace, no atomics, and
-// the int32 sums stay exact.  Owning several column blocks per workgroup divides the A
-// traffic (one A fragment serves NBW blocks).
+// A workgroup owns NBW 16-column blocks and one block of 16*MR rows.  Its NW waves split K
+// (wave w takes K tiles w, w+NW, ...), each wave keeps UNROLL-1 K tiles of loads in flight
+// ahead of the one it multiplies, and the NW partial accumulators are summed through LDS
+// before the fused epilogue.  The K split is reduced inside the workgroup: no workspace, no
+// atomics, no second launch, and the int32 sums stay exact.
+//
+// Decode (M <= 16*MR): one row block, the whole of A (a few hundred KB at most) stays in L2
+// and the kernel is bound by reading B once; owning several column blocks per workgroup
+// divides the A traffic (one A fragment serves NBW blocks).  Larger M with few output tiles
+// (e.g. 128 x 4096): the grid also runs over row blocks, so 256 workgroups can share an output
+// that a 64x128 tile would cover with 64.  The row blocks of one column group read the same B
+// and are placed on one XCD, next to each other in dispatch order, so B comes from HBM once
+// and is re-read from that XCD's L2.
 //
 // Per K tile a lane loads, for every owned 16-column block, the two 16-byte chunks
 // (lane/16) and (lane/16)+4 of column (lane%16) -- the preshuffled layout makes each
-// wave-wide load one contiguous 1 KB read, issued non-temporal because B is used once --
-// and the matching two chunks of A row (lane%16).  As in the large-M kernel, B is the
-// MFMA's first operand, so a lane ends with row (lane%16) and four consecutive columns.
+// wave-wide load one contiguous 1 KB read, non-temporal when B is read once (NT_B) -- and the
+// matching two chunks of A row (lane%16).  As in the large-M kernel, B is the MFMA's first
+// operand, so a lane ends with row (lane%16) and four consecutive columns.
 #pragma once
 #include "gemm_common.h"
 
 namespace flygemm {
 
-template <int MR, int NBW, int NW, int UNROLL, int KIND, int EPI, bool OUT_BF16>
+// B loads: non-temporal (NT_B) when each B byte is read by one workgroup (decode shapes), plain
+// when the row blocks of a column group re-read it from L2.
+template <bool NT, typename T>
+__device__ __forceinline__ T load_b(const T* p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+template <int MR, int NBW, int NW, int UNROLL, int KIND, int EPI, bool OUT_BF16, bool NT_B = true>
 __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   const int M = p.M, N = p.N, K = p.K;
   const int nk = K / KT;
@@ -32,7 +48,15 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   const int l16 = lane & 15;
   const int lq = lane >> 4;
   const int nblk_max = N / 16 - 1;
-  const int nb0 = blockIdx.x * NBW;
+  // workgroup -> (row block, column group).  With several row blocks, XCD x (workgroups are
+  // dealt to the 8 XCDs round-robin) gets a contiguous range of logical ids, row block
+  // fastest, so the row blocks sharing a column group run together on one XCD.
+  const int nrb = (M + 16 * MR - 1) / (16 * MR);
+  int bid = blockIdx.x;
+  const int G = gridDim.x;
+  if (nrb > 1 && (G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
+  const int m0 = (bid % nrb) * 16 * MR;
+  const int nb0 = (bid / nrb) * NBW;
 
   constexpr int B_BLK = (KIND == KIND_INT4) ? 1024 : 2048;
   constexpr size_t B_PER_K = B_BLK / KT;  // bytes of one 16-col block per K element (16 or 8)
@@ -41,7 +65,6 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   // per-token / per-channel scaling (not applied to 16-bit inputs, whose scale pointers may be
   // null, nor to MXFP4, whose block scales are applied by the MFMA)
   constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_unscaled(KIND);
-  constexpr int MQ = (MR + 1) / 2;
   AccT acc[MR][NBW];
 #pragma unroll
   for (int i = 0; i < MR; ++i)
@@ -50,7 +73,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
 
   const uint8_t* arow[MR];
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) arow[mi] = p.a + (size_t)min(mi * 16 + l16, M - 1) * K + lq * 16;
+  for (int mi = 0; mi < MR; ++mi) arow[mi] = p.a + (size_t)min(m0 + mi * 16 + l16, M - 1) * K + lq * 16;
   const uint8_t* bblk[NBW];
 #pragma unroll
   for (int j = 0; j < NBW; ++j) {
@@ -69,7 +92,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     i32x4 blo[NBW], bhi[NBW];
     i32x2 b4lo[NBW], b4hi[NBW];
     float sa[MR], sb[NBW];  // blockscale: this K tile's A scale per row block, B scale per column block
-    uint32_t fa[MQ], fb[NBW];  // MXFP4: scale words, already shifted to the block's byte pair
+    uint32_t fa[MR], fb[NBW];  // MXFP4: scale words, already shifted to the block's byte pair
   };
   Stage st[UNROLL];
   auto load = [&](Stage& s, int kt) {
@@ -77,11 +100,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     for (int j = 0; j < NBW; ++j) {
       const uint8_t* src = bblk[j] + (size_t)kt * B_BLK;
       if constexpr (KIND == KIND_INT4) {
-        s.b4lo[j] = __builtin_nontemporal_load((const i32x2*)src);
-        s.b4hi[j] = __builtin_nontemporal_load((const i32x2*)(src + 512));
+        s.b4lo[j] = load_b<NT_B>((const i32x2*)src);
+        s.b4hi[j] = load_b<NT_B>((const i32x2*)(src + 512));
       } else {
-        s.blo[j] = __builtin_nontemporal_load((const i32x4*)src);
-        s.bhi[j] = __builtin_nontemporal_load((const i32x4*)(src + 1024));
+        s.blo[j] = load_b<NT_B>((const i32x4*)src);
+        s.bhi[j] = load_b<NT_B>((const i32x4*)(src + 1024));
       }
     }
 #pragma unroll
@@ -94,8 +117,12 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     if constexpr (KIND == KIND_FP4) {
       const uint32_t* wa = (const uint32_t*)p.sa;
       const uint32_t* wb = (const uint32_t*)p.sb;
+      // row block r16 = m0/16 + mi is half (r16 & 1) of 32-row scale group r16 / 2
 #pragma unroll
-      for (int q = 0; q < MQ; ++q) s.fa[q] = wa[((size_t)min(q, (M + 31) / 32 - 1) * nk + kt) * 64 + lane];
+      for (int mi = 0; mi < MR; ++mi) {
+        const int r16 = (m0 >> 4) + mi;
+        s.fa[mi] = wa[((size_t)min(r16 >> 1, (M + 31) / 32 - 1) * nk + kt) * 64 + lane] >> (8 * (r16 & 1));
+      }
 #pragma unroll
       for (int j = 0; j < NBW; ++j) {
         const int nb = min(nb0 + j, nblk_max);
@@ -104,7 +131,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     }
     if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
-      for (int mi = 0; mi < MR; ++mi) s.sa[mi] = p.sa[(size_t)kt * M + min(mi * 16 + l16, M - 1)];
+      for (int mi = 0; mi < MR; ++mi) s.sa[mi] = p.sa[(size_t)kt * M + min(m0 + mi * 16 + l16, M - 1)];
 #pragma unroll
       for (int j = 0; j < NBW; ++j) s.sb[j] = p.sb[(size_t)(min((nb0 + j) * 16, N - 1) >> 7) * nk + kt];
     }
@@ -147,9 +174,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) {
           if constexpr (KIND == KIND_FP4) {
-            const uint32_t saw = s.fa[mi >> 1] >> (8 * (mi & 1));
-            acc[mi][j] = mfma_fp4<0>(bl, s.alo[mi], acc[mi][j], s.fb[j], saw);
-            acc[mi][j] = mfma_fp4<1>(bh, s.ahi[mi], acc[mi][j], s.fb[j], saw);
+            acc[mi][j] = mfma_fp4<0>(bl, s.alo[mi], acc[mi][j], s.fb[j], s.fa[mi]);
+            acc[mi][j] = mfma_fp4<1>(bh, s.ahi[mi], acc[mi][j], s.fb[j], s.fa[mi]);
           } else {
             acc[mi][j] = mfma_k64<KIND>(bl, s.alo[mi], acc[mi][j]);
             acc[mi][j] = mfma_k64<KIND>(bh, s.ahi[mi], acc[mi][j]);
@@ -194,7 +220,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       AccT s = red[0][mi * NBW + j][lane];
 #pragma unroll
       for (int w = 1; w < NW; ++w) s += red[w][mi * NBW + j][lane];
-      const int row = mi * 16 + l16;
+      const int row = m0 + mi * 16 + l16;
       if (row >= M) continue;
       const size_t idx = (size_t)row * N + col;
       if constexpr (EPI == EPI_RAW) {

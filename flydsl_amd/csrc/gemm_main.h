@@ -144,15 +144,7 @@ __device__ __forceinline__ void workgroup_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Split-K (SPLIT): work item (s, tile) covers K tiles [s*nk/ks, (s+1)*nk/ks) of the tile and
-// stores its raw accumulators to slice s of the workspace, ws[s][M][N] (int32 or fp32); the
-// reduce kernel below, launched next on the same stream, adds the ks slices in split order and
-// applies the epilogue.  The kernel boundary orders the partial sums before their reads, so
-// no fence, counter or co-residency assumption is involved, and the sum does not depend on
-// which split finished first.
-constexpr int SPLIT_MAX = 8;
-
-template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16, bool SPLIT = false>
+template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) {
   using C = MainCfg<BM, BN, WM, WN, KIND>;
   constexpr int MR = C::MR, NR = C::NR, NW = C::NW;
@@ -413,38 +405,19 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     }
   };
 
-  // ---- split-K: this item's raw accumulators to its workspace slice, with the epilogue's
-  // store pattern (MR*NR 16-byte buffer stores per lane, those outside C dropped) ----
-  const int ks = SPLIT ? p.ks : 1;
-  auto store_partial = [&](int s, int m0, int n0) {
-    const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc((const uint8_t*)p.ws + (size_t)s * M * N * 4, M * N * 4);
-#pragma unroll
-    for (int mi = 0; mi < MR; ++mi) {
-      const int row = m0 + wm * C::TM + mi * 16 + l16;
-#pragma unroll
-      for (int ni = 0; ni < NR; ++ni) {
-        const int col = n0 + wn * C::TN + ni * 16 + lq * 4;
-        const uint32_t off = (row < M && col < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)col) * 4u : 0x80000000u;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[mi][ni]), rsrc_w, off, 0, 0);
-      }
-    }
-  };
-
-  // ---- persistent loop over this workgroup's work items (a tile, or one K range of a tile
-  // when split), one flattened (item, K tile) pipeline: the DMA of the next step -- the next
-  // K tile, or the first K tile of the next item -- is in flight while the MFMAs of the
-  // current step run, so an item's first loads overlap the previous item's last MFMAs and
-  // its epilogue.
+  // ---- persistent loop over this workgroup's tiles, one flattened (tile, K tile) pipeline:
+  // the DMA of the next step -- the next K tile, or the first K tile of the next tile -- is
+  // in flight while the MFMAs of the current step run, so a tile's first loads overlap the
+  // previous tile's last MFMAs and its epilogue.
   const int G = gridDim.x;
-  const int nitems = ntiles * ks;
-  auto item = [&](int w, int& m0_, int& n0_, int& kb_, int& ke_, int& s_) {
-    s_ = SPLIT ? w / ntiles : 0;
+  const int nitems = ntiles;
+  auto item = [&](int w, int& m0_, int& n0_, int& kb_, int& ke_) {
     int bm, bn;
-    tile_coords(w - s_ * ntiles, ntiles, nbm, bm, bn);
+    tile_coords(w, ntiles, nbm, bm, bn);
     m0_ = bm * BM;
     n0_ = bn * BN;
-    kb_ = SPLIT ? s_ * nk / ks : 0;
-    ke_ = SPLIT ? (s_ + 1) * nk / ks : nk;
+    kb_ = 0;
+    ke_ = nk;
   };
   if constexpr (C::NS == 3) {
     // Three LDS stages, the DMA two steps ahead (the 4-wave tiles, whose steps are short
@@ -456,23 +429,23 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     __shared__ __attribute__((aligned(1024))) uint8_t lds2[STAGE];
     auto ring = [&](int i) -> uint8_t* { return i == 0 ? lds0 : (i == 1 ? lds1 : lds2); };
     int iw = blockIdx.x, ikt = 0, ike = 0;  // the next step to issue: item iw, K tile ikt
-    int im0 = 0, in0 = 0, idummy = 0;
-    if (iw < nitems) item(iw, im0, in0, ikt, ike, idummy);
+    int im0 = 0, in0 = 0;
+    if (iw < nitems) item(iw, im0, in0, ikt, ike);
     int issued = 0;
     auto issue_next = [&](int slot) {
       issue(ring(slot), im0, in0, ikt);
       ++issued;
       if (++ikt == ike) {
         iw += G;
-        if (iw < nitems) item(iw, im0, in0, ikt, ike, idummy);
+        if (iw < nitems) item(iw, im0, in0, ikt, ike);
       }
     };
     if (iw < nitems) issue_next(0);
     if (iw < nitems) issue_next(1);
     int step = 0, slot = 0;
     for (int w = blockIdx.x; w < nitems; w += G) {
-      int m0, n0, kb, ke, s;
-      item(w, m0, n0, kb, ke, s);
+      int m0, n0, kb, ke;
+      item(w, m0, n0, kb, ke);
 #pragma unroll
       for (int i = 0; i < MR; ++i)
 #pragma unroll
@@ -487,31 +460,27 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         compute(ring(slot));
         slot = slot == 2 ? 0 : slot + 1;
       }
-      if (ks > 1)
-        store_partial(s, m0, n0);
-      else
-        epilogue(m0, n0);
+      epilogue(m0, n0);
     }
     return;
   }
   int w = blockIdx.x;
-  int m0, n0, kb, ke, s;
-  item(w, m0, n0, kb, ke, s);
+  int m0, n0, kb, ke;
+  item(w, m0, n0, kb, ke);
   issue(lds0, m0, n0, kb);
   int step = 0;
   for (; w < nitems; w += G) {
     const int wnext = w + G;
-    int nm0 = 0, nn0 = 0, nkb = 0, nke = 0, ns = 0;
-    if (wnext < nitems) item(wnext, nm0, nn0, nkb, nke, ns);
+    int nm0 = 0, nn0 = 0, nkb = 0, nke = 0;
+    if (wnext < nitems) item(wnext, nm0, nn0, nkb, nke);
 #pragma unroll
     for (int i = 0; i < MR; ++i)
 #pragma unroll
       for (int j = 0; j < NR; ++j) acc[i][j] = AccT{0, 0, 0, 0};
     for (int kt = kb; kt < ke; ++kt, ++step) {
-      // wait for this wave's loads of this step; at an item's first step the previous
-      // item's MR*NR epilogue stores were issued after them and may still be in flight
-      // (vector memory operations retire in issue order).  A split item's partial-sum
-      // stores are the same count.
+      // wait for this wave's loads of this step; at a tile's first step the previous
+      // tile's MR*NR epilogue stores were issued after them and may still be in flight
+      // (vector memory operations retire in issue order).
       if (kt == kb && step > 0)
         wait_vmem_leaving<MR * NR>();
       else
@@ -529,53 +498,11 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         issue(nxt, nm0, nn0, nkb);
       compute(cur);
     }
-    if (ks > 1)
-      store_partial(s, m0, n0);
-    else
-      epilogue(m0, n0);
+    epilogue(m0, n0);
     m0 = nm0;
     n0 = nn0;
     kb = nkb;
     ke = nke;
-    s = ns;
-  }
-}
-
-// Split-K epilogue: C = epilogue(sum over s of ws[s]) with the sum taken in split order and the
-// same arithmetic as the main kernel's epilogue.  One thread per 4 consecutive outputs.
-template <int KIND, int EPI, bool OUT_BF16>
-__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p) {
-  typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
-  constexpr bool kScaled = EPI == EPI_ROWCOL && !kind_unscaled(KIND);
-  const int M = p.M, N = p.N;
-  const long i4 = (long)blockIdx.x * 256 + threadIdx.x;
-  if (i4 * 4 >= (long)M * N) return;
-  const size_t idx = (size_t)i4 * 4;
-  const size_t slice = (size_t)M * N;
-  const uint8_t* ws = (const uint8_t*)p.ws + idx * 4;
-  // every slice's load is issued before the first add
-  AccT part[SPLIT_MAX];
-#pragma unroll
-  for (int s = 0; s < SPLIT_MAX; ++s)
-    part[s] = s < p.ks ? __builtin_nontemporal_load((const AccT*)(ws + s * slice * 4)) : AccT{0, 0, 0, 0};
-  AccT sum = part[0];
-#pragma unroll
-  for (int s = 1; s < SPLIT_MAX; ++s)
-    if (s < p.ks) sum += part[s];
-  if constexpr (EPI == EPI_RAW) {
-    *(AccT*)((uint8_t*)p.c + idx * 4) = sum;
-  } else {
-    const int row = (int)(idx / N), col = (int)(idx % N);
-    float v[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = (float)sum[r];
-    if constexpr (kScaled) {
-      const float sa = p.sa[row];
-      const f32x4 sb = *(const f32x4*)(p.sb + col);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = (v[r] * sa) * sb[r];
-    }
-    *(i32x2*)((typename OutT<OUT_BF16>::type*)p.c + idx) = pack_out4<OUT_BF16>(v);
   }
 }
 

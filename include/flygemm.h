@@ -9,14 +9,9 @@
  * Conventions shared by every entry point:
  *  - All pointers are device pointers the caller allocated.  Launches are asynchronous on
  *    `stream` (a hipStream_t, NULL = default stream).  Callers keep buffers alive until the
- *    stream has finished.  Nothing is allocated, freed or synchronized here, with one
- *    exception: a split-K launch (chosen for M > 64 when the output has at most 128 tiles of
- *    64x128, or forced through `variant`) writes ks fp32/int32 partial sums per output to a
- *    workspace that the library allocates the first time a stream needs it (at least 16 MiB,
- *    one per device and stream; a larger call allocates a larger one, and none is ever freed
- *    before the process ends, since queued kernels or captured graphs may still use it), then
- *    launches a second kernel that adds them in split order and applies the epilogue.
- *    Allocating is refused while the stream is being captured into a graph.
+ *    stream has finished.  Nothing is allocated, freed or synchronized here, and every GEMM is
+ *    one kernel launch (a K split over the waves of a workgroup is summed in LDS), so every
+ *    entry point may be captured into a HIP graph on any stream.
  *  - A is row-major [M][K] bytes.  B is the preshuffled [N][K] buffer produced by the
  *    reference's `shuffle_weight(b, layout=(16, 16))` (tests/utils.py:76-96): element
  *    (n, k) at byte (n/16)*16*K + (k/16)*256 + (n%16)*16 + (k%16).  INT4 B is that buffer
@@ -28,9 +23,7 @@
  *  - Return value: 0 on success, otherwise a hipError_t code; flygemm_last_error() gives
  *    the message of the calling thread's last failure.
  *  - `variant`: -1 picks the kernel from the built-in table; 0..flygemm_num_variants()-1
- *    forces one (for tests and tuning).  For a split-K variant (name ending in "_splitk"),
- *    bits 16..23 may add the K split count (1..8, each split at least one 128-deep K tile;
- *    0 = the library's choice).
+ *    forces one (for tests and tuning); every variant accepts every M.
  */
 #ifndef FLYGEMM_H
 #define FLYGEMM_H

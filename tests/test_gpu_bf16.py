@@ -16,7 +16,6 @@ from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
 VARIANTS = _lib.variants()
-DECODE_ROWS = {i: 16 * int(n.split("_m")[1].split("_")[0]) for i, n in enumerate(VARIANTS) if n.startswith("decode_")}
 DT = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
@@ -60,8 +59,6 @@ def test_reference_shapes(gpu, kind, M, N, K):
 def test_variants_ragged(gpu, kind, variant):
     for (M, N, K) in [(1, 64, 64), (7, 2112, 256), (16, 1024, 2048), (33, 1040, 384), (100, 272, 192),
                       (300, 528, 640)]:
-        if variant in DECODE_ROWS and M > DECODE_ROWS[variant]:
-            continue
         _say(f"variant {VARIANTS[variant]} {kind} {M}x{N}x{K}")
         ops = workloads.make_operands(workloads.custom(kind, M, N, K, seed=M * 3 + N + K))
         out = H.launch(ops, gpu, variant=variant)

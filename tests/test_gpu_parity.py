@@ -18,8 +18,6 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 VARIANTS = _lib.variants()
 MAIN = [i for i, n in enumerate(VARIANTS) if n.startswith("main_")]
-DECODE = [i for i, n in enumerate(VARIANTS) if n.startswith("decode_")]
-DECODE_ROWS = {i: 16 * int(VARIANTS[i].split("_m")[1].split("_")[0]) for i in DECODE}
 
 
 def _say(msg):
@@ -47,7 +45,7 @@ def test_golden_fixture(gpu, kind):
     sa = torch.from_numpy(z["sa"]).to(gpu)
     sb = torch.from_numpy(z["sb"]).to(gpu)
     from oracle import gemm as og, numerics as on
-    for v in [-1] + MAIN + [d for d in DECODE if DECODE_ROWS[d] >= M]:
+    for v in [-1] + list(range(len(VARIANTS))):
         c = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
         if kind == "fp8_block":
             rc = _lib.load().flygemm_blockscale(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(),
@@ -102,14 +100,13 @@ def test_config_T_sampled_rows(gpu):
 
 # ---------------------------------------------------------------- every variant, ragged shapes
 SHAPES = [(1, 64, 128), (7, 2112, 256), (16, 1024, 2048), (33, 1040, 384), (100, 272, 384), (300, 528, 640)]
+# every variant handles any M: the decode and rows variants add row blocks past 16*MR rows
 
 
 @pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "fp8_block"])
 @pytest.mark.parametrize("variant", list(range(len(VARIANTS))))
 def test_variants_ragged(gpu, kind, variant):
     for (M, N, K) in SHAPES:
-        if variant in DECODE and M > DECODE_ROWS[variant]:
-            continue
         w = workloads.custom(kind, M, N, K, seed=M + N + K, b_std=0.02 if kind == "int4" else 1.0)
         ops = workloads.make_operands(w)
         _say(f"variant {VARIANTS[variant]} {kind} {M}x{N}x{K}")
@@ -120,84 +117,73 @@ def test_variants_ragged(gpu, kind, variant):
             assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
 
 
-# ---------------------------------------------------------------- split-K
-SPLIT = [i for i, n in enumerate(VARIANTS) if n.endswith("_splitk")]
+# ---------------------------------------------------------------- row-blocked streaming kernel
+ROWS = [i for i, n in enumerate(VARIANTS) if n.startswith("rows_")]
 
 
 @pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "fp8_block", "bf16"])
-@pytest.mark.parametrize("variant", SPLIT)
-@pytest.mark.parametrize("ks", [2, 3, 4, 8])
-def test_split_k_forced(gpu, kind, variant, ks):
-    """Forced K splits (bits 16..23 of the variant) on ragged shapes, including K ranges of
-    unequal length (ks not dividing K/128) and a split per K tile: int paths bit-exact (raw
-    accumulators and bf16 output), the rest within the bar.  Repeating the call gives the
-    same bits: the partial sums are added in split order whichever split finishes last."""
-    for (M, N, K) in [(100, 272, 1024), (130, 528, 2176), (7, 2112, 512)]:
-        if ks > K // 128:
-            continue
-        w = workloads.custom(kind, M, N, K, seed=M + N + K + ks, b_std=0.02 if kind == "int4" else 1.0)
+@pytest.mark.parametrize("variant", ROWS)
+def test_rows_variants(gpu, kind, variant):
+    """The row-blocked kernel (several row blocks per column group, K split over the waves
+    and summed in LDS) on ragged shapes: a partial last row block, N not a multiple of the
+    column group, K tiles not a multiple of the wave count.  Int paths bit-exact (raw
+    accumulators and bf16 output), the rest within the bar; a repeated call gives the same
+    bits (the LDS sum has a fixed order)."""
+    for (M, N, K) in [(100, 272, 1024), (130, 528, 2176), (300, 96, 640)]:
+        w = workloads.custom(kind, M, N, K, seed=M + N + K, b_std=0.02 if kind == "int4" else 1.0)
         ops = workloads.make_operands(w)
-        v = variant | (ks << 16)
-        _say(f"split-K {VARIANTS[variant]} ks={ks} {kind} {M}x{N}x{K}")
-        out = H.launch(ops, gpu, variant=v)
-        again = H.launch(ops, gpu, variant=v)
+        _say(f"rows {VARIANTS[variant]} {kind} {M}x{N}x{K}")
+        out = H.launch(ops, gpu, variant=variant)
+        again = H.launch(ops, gpu, variant=variant)
         torch.cuda.synchronize()
         assert torch.equal(out, again)
         ref = H.check(ops, out)
         if kind in ("int8", "int4"):
-            assert np.array_equal(H.raw_acc(ops, gpu, v).cpu().numpy(), ref)
+            assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
 
 
-def test_split_k_two_streams_and_graph(gpu):
-    """Split-K launches on two streams at once (each stream has its own workspace), then the
-    same launch captured in a HIP graph after a warm-up outside capture: every replay, with
-    eager work in between, equals the eager result."""
-    names = VARIANTS
-    assert names[_lib.load().flygemm_select_variant(128, 4096, 4096, 0, 0)].endswith("_splitk")
-    opsA = workloads.make_operands(workloads.custom("int8", 128, 2048, 4096, seed=41))
-    opsB = workloads.make_operands(workloads.custom("int8", 128, 2048, 4096, seed=42))
-    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
-    _say("split-K two streams")
-    outs = []
+@pytest.mark.parametrize("kind,M,N,K", [("fp8", 128, 4096, 4096), ("fp8_block", 33, 2112, 7168),
+                                        ("fp8_block", 64, 2112, 7168), ("fp8_block", 256, 2112, 7168),
+                                        ("int8", 128, 2048, 4096)])
+def test_graph_capture_reference_pattern(gpu, kind, M, N, K):
+    """The reference harness's graph path (tests/test_common.py:79-89 with the launcher of
+    test_blockscale_preshuffle_gemm.py:199-213): eager launches on the current stream, then
+    ``torch.cuda.graph(g)`` on torch's own capture stream, which has never run the shape.
+    Every replay, with eager work of the same shape in between, equals the eager result."""
+    ops = workloads.make_operands(workloads.custom(kind, M, N, K, seed=M + N))
+    _say(f"graph capture {kind} {M}x{N}x{K} variant="
+          f"{VARIANTS[_lib.load().flygemm_select_variant(M, N, K, 0 if kind == 'fp8_block' else _lib.FLYGEMM_IN[kind], int(kind == 'fp8_block'))]}")
+    a = H.dev_flat(ops["a"], gpu)
+    b = H.dev_flat(ops["b_dev"], gpu)
+    sa = (ops["sa_t"] if kind == "fp8_block" else ops["sa"]).to(gpu).contiguous().view(-1)
+    sb = ops["sb"].to(gpu).contiguous().view(-1)
+    c = torch.zeros(M, N, dtype=torch.bfloat16, device=gpu)
+    if kind == "fp8_block":
+        from flydsl_amd.kernels.blockscale_preshuffle_gemm import compile_blockscale_preshuffle_gemm
+        fn = compile_blockscale_preshuffle_gemm(M=M, N=N, K=K, tile_m=64, tile_n=128, tile_k=128, out_dtype="bf16")
+    else:
+        from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
+        fn = compile_preshuffle_gemm_a8(K=K, tile_m=64, tile_n=128, tile_k=128, in_dtype=kind, out_dtype="bf16")
+
+    def launch_kernel():
+        fn(c.view(-1), a, b, sa, sb, M, N, torch.cuda.current_stream())
+
     for _ in range(3):
-        with torch.cuda.stream(s1):
-            oa = H.launch(opsA, gpu, stream=s1)
-        with torch.cuda.stream(s2):
-            ob = H.launch(opsB, gpu, stream=s2)
-        outs.append((oa, ob))
+        launch_kernel()
     torch.cuda.synchronize()
-    for oa, ob in outs:
-        H.check(opsA, oa)
-        H.check(opsB, ob)
-
-    _say("split-K graph replay")
-    ops = workloads.make_operands(workloads.custom("fp8", 128, 4096, 4096, seed=43))
-    eager = H.launch(ops, gpu)
-    torch.cuda.synchronize()
+    eager = c.clone()
     H.check(ops, eager)
-    a = ops["a"].to(gpu).view(torch.int8).view(-1)
-    b = ops["b_dev"].to(gpu).view(torch.int8).view(-1)
-    sa, sb = ops["sa"].to(gpu).view(-1), ops["sb"].to(gpu).view(-1)
-    c = torch.empty(128, 4096, dtype=torch.bfloat16, device=gpu)
-    from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
-    fn = compile_preshuffle_gemm_a8(K=4096, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        fn(c.view(-1), a, b, sa, sb, 128, 4096, s)  # allocates this stream's workspace
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    assert torch.equal(c, eager)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
-        fn(c.view(-1), a, b, sa, sb, 128, 4096, s)
+    with torch.cuda.graph(g):
+        launch_kernel()
     for i in range(3):
-        c.fill_(0)
-        H.launch(ops, gpu)  # eager split-K work on another stream between replays
+        c.zero_()
+        other = H.launch(ops, gpu)  # eager work of the same shape between replays
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(c, eager), f"replay {i}"
+        assert torch.equal(other, eager)
 
 
 @pytest.mark.parametrize("kind", ["fp8", "int8"])

@@ -38,20 +38,20 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 0, 0)].startswith("decode_m1")
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
     # every shape gets a variant, and the five configurations get the tiles measured fastest
-    expect = {(128, 4096, 4096, 0, 0): "main_64x128_w1x4_splitk", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
+    expect = {(128, 4096, 4096, 0, 0): "rows_m2_nb4_w8_u3", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
               (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_256x128_w2x4",
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
     # 17-64 rows: decode only up to 32 rows (16 for very wide N, or blockscale with 32+ column
-    # tiles); the 64x128 tile (split-K when few tiles) above
+    # tiles); the 64x128 tile above, or the row-blocked kernel when that gives few tiles
     assert names[lib.flygemm_select_variant(64, 28672, 8192, 0, 0)] == "main_64x128_w1x4"
     assert names[lib.flygemm_select_variant(32, 28672, 8192, 0, 0)] == "main_64x128_w1x4"
     assert names[lib.flygemm_select_variant(32, 8192, 8192, 1, 0)].startswith("decode_m2")
-    assert names[lib.flygemm_select_variant(48, 8192, 8192, 1, 0)] == "main_64x128_w1x4_splitk"
-    assert names[lib.flygemm_select_variant(64, 7168, 2048, 2, 0)] == "main_64x128_w1x4"
-    assert names[lib.flygemm_select_variant(64, 8192, 8192, 3, 0)] == "main_64x128_w1x4_splitk"
-    assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "main_64x128_w1x4_splitk"
+    assert names[lib.flygemm_select_variant(48, 8192, 8192, 1, 0)] == "rows_m2_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(64, 7168, 2048, 2, 0)] == "rows_m2_nb4_w8_u3"  # 56 tiles
+    assert names[lib.flygemm_select_variant(64, 8192, 8192, 3, 0)] == "rows_m2_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(32, 2112, 7168, 0, 1)].startswith("decode_m2")
     assert names[lib.flygemm_select_variant(16, 7168, 7168, 0, 1)].startswith("decode_m1")
     # blockscale: 256x256 from 200 tiles, 256x128 from 160
@@ -64,12 +64,17 @@ def test_variant_table():
     # 128x128 once it gives more than one tile per CU
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x128_w2x2"
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
-    # split K only where the 64x128 tiles leave CUs idle and K has at least 32 K tiles
-    assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 0)] == "main_64x128_w1x4_splitk"
-    assert names[lib.flygemm_select_variant(128, 4096, 2048, 0, 0)] == "main_64x128_w1x4"
+    # the row-blocked kernel where the 64x128 tiles leave CUs idle (at most 96 tiles), with
+    # 16-row blocks for blockscale and MXFP4
+    assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 0)] == "rows_m2_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(128, 4096, 1024, 1, 0)] == "rows_m2_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(256, 8192, 4096, 0, 0)] == "main_64x128_w1x4"
-    assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 1)] == "main_64x128_w1x4_splitk"
-    assert names[lib.flygemm_select_variant(128, 4096, 2048, 3, 0)] == "main_64x128_w1x4_splitk"  # 2 bytes/elt
+    assert names[lib.flygemm_select_variant(256, 4096, 4096, 0, 0)] == "main_64x128_w1x4"  # 128 tiles
+    assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 1)] == "rows_m1_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(256, 2112, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(33, 2112, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(128, 4096, 4096, 5, 0)] == "rows_m1_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(128, 4096, 2048, 3, 0)] == "rows_m2_nb4_w8_u3"  # 2 bytes/elt
     # int4 decode takes more column blocks per workgroup (half-size blocks)
     assert names[lib.flygemm_select_variant(16, 14336, 4096, 2, 0)] == "decode_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(16, 14336, 4096, 1, 0)] == "decode_m1_nb2_w8_u4"
@@ -96,16 +101,12 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc != 0 and b"in_dtype" in lib.flygemm_last_error()
     rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 256, 0, 0, 99, None)
     assert rc != 0 and b"variant" in lib.flygemm_last_error()
-    # split counts ride in bits 16..23 of the variant, for split-K variants only
+    # a variant index past the table (including the old split-count bits) is rejected
     names = _lib.variants()
-    sk, plain = names.index("main_64x128_w1x4_splitk"), names.index("main_64x128_w1x4")
+    plain = names.index("main_64x128_w1x4")
     rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 1024, 0, 0, plain | (2 << 16), None)
-    assert rc != 0 and b"does not split K" in lib.flygemm_last_error()
-    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 2048, 0, 0, sk | (9 << 16), None)
-    assert rc != 0 and b"K splits" in lib.flygemm_last_error()
-    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 256, 0, 0, sk | (3 << 16), None)
-    assert rc != 0 and b"K splits" in lib.flygemm_last_error()
-    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 1024, 0, 0, sk | (1 << 24), None)
+    assert rc != 0 and b"unknown variant" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 100, 128, 1024, 0, 0, -2, None)
     assert rc != 0 and b"unknown variant" in lib.flygemm_last_error()
     rc = lib.flygemm_blockscale(p, p, p, p, p, 16, 128, 256, 64, 0, -1, None)
     assert rc != 0 and b"scale_block_k" in lib.flygemm_last_error()
