@@ -294,20 +294,31 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         const i32x4 hi = *(const i32x4*)(sB + off + 1024);
         bf[ni] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
+    // blockscale: the 128-deep MFMA of row mi goes into a zeroed partial, and the partial is
+    // added to the accumulator scaled by sa * sb one row later, after the next row's MFMAs
+    // have been issued, so the FMAs never wait on the MFMA that produced their operand.  Two
+    // partial sets alternate between rows.
+    f32x4 part[2][NR];
+    auto scale_row = [&](int mi) {
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni) {
+        const f32x4 pv = part[mi & 1][ni];
+        const float s = sa_t[mi] * sb_t[ni];
+        acc[mi][ni].x = __builtin_fmaf(pv.x, s, acc[mi][ni].x);
+        acc[mi][ni].y = __builtin_fmaf(pv.y, s, acc[mi][ni].y);
+        acc[mi][ni].z = __builtin_fmaf(pv.z, s, acc[mi][ni].z);
+        acc[mi][ni].w = __builtin_fmaf(pv.w, s, acc[mi][ni].w);
+      }
+    };
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) {
         const i32x8 af = i32x8{alo.x, alo.y, alo.z, alo.w, ahi.x, ahi.y, ahi.z, ahi.w};
         if (mi + 1 < MR) load_a(sA, mi + 1, alo, ahi);
         if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
-          for (int ni = 0; ni < NR; ++ni) {
-            const f32x4 part = mfma_fp8(bf[ni], af, f32x4{0.f, 0.f, 0.f, 0.f});
-            const float s = sa_t[mi] * sb_t[ni];
-            acc[mi][ni].x = __builtin_fmaf(part.x, s, acc[mi][ni].x);
-            acc[mi][ni].y = __builtin_fmaf(part.y, s, acc[mi][ni].y);
-            acc[mi][ni].z = __builtin_fmaf(part.z, s, acc[mi][ni].z);
-            acc[mi][ni].w = __builtin_fmaf(part.w, s, acc[mi][ni].w);
-          }
+          for (int ni = 0; ni < NR; ++ni) part[mi & 1][ni] = mfma_fp8(bf[ni], af, f32x4{0.f, 0.f, 0.f, 0.f});
+          if (mi > 0) scale_row(mi - 1);
+          if (mi + 1 == MR) scale_row(mi);
         } else {
 #if FLY_SCHED
           // the next row's A reads stay ahead of this row's MFMAs
