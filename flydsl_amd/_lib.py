@@ -10,7 +10,7 @@ import os
 
 from .build import OUT as LIB_PATH
 
-FLYGEMM_IN = {"fp8": 0, "int8": 1, "int4": 2, "bf16": 3, "fp16": 4, "fp4": 5}
+FLYGEMM_IN = {"fp8": 0, "int8": 1, "int4": 2, "bf16": 3, "fp16": 4, "fp4": 5, "int4_bf16": 6, "int8smooth": 7}
 FLYGEMM_OUT = {"bf16": 0, "fp16": 1, "fp32": 2}
 QUANT_IN = {"fp16": 0, "bf16": 1, "fp32": 2}
 QUANT_OUT = {"fp8": 0, "int8": 1}
@@ -26,8 +26,8 @@ SIGNATURES = [
     ("flygemm_accumulators", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     ("flygemm_quant_rows", ctypes.c_int, [_P, _F, _P, _I, _I, _I, _I, _I, _P]),
     ("flygemm_mxfp4", ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
-    ("flygemm_moe_gemm1", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 11 + [_P]),
-    ("flygemm_moe_gemm2", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 12 + [_P]),
+    ("flygemm_moe_gemm1", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 12 + [_P]),
+    ("flygemm_moe_gemm2", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 13 + [_P]),
     ("flygemm_moe_reduce", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _P]),
     ("flygemm_moe_blockscale_gemm1", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 11 + [_P]),
     ("flygemm_moe_blockscale_gemm2", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 12 + [_P]),

@@ -24,7 +24,10 @@ typedef int   i32x4 __attribute__((ext_vector_type(4)));
 typedef int   i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIND_F16 = 4, KIND_FP4 = 5 };
+enum Kind : int {
+  KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIND_F16 = 4, KIND_FP4 = 5,
+  KIND_W4A16 = 6,  // MoE only: bf16 activations, int4 weights converted to bf16 in registers
+};
 
 // 16-bit inputs (bf16 / fp16) run through the same kernels in bytes: K counts bytes (two per
 // element), the preshuffled B layout is the 1-byte layout applied to each row's bytes
@@ -33,7 +36,7 @@ enum Kind : int { KIND_FP8 = 0, KIND_INT8 = 1, KIND_INT4 = 2, KIND_BF16 = 3, KIN
 // lane as the int8 16x16x64 instruction.  They are not scaled (kernels/preshuffle_gemm.py:
 // 804-806, 874-877).
 constexpr bool kind_is_16bit(int k) { return k == KIND_BF16 || k == KIND_F16; }
-constexpr bool kind_float_acc(int k) { return k == KIND_FP8 || kind_is_16bit(k) || k == KIND_FP4; }
+constexpr bool kind_float_acc(int k) { return k == KIND_FP8 || kind_is_16bit(k) || k == KIND_FP4 || k == KIND_W4A16; }
 // kinds whose epilogue applies no per-token / per-channel scale (MXFP4 scales live inside the MFMA)
 constexpr bool kind_unscaled(int k) { return kind_is_16bit(k) || k == KIND_FP4; }
 

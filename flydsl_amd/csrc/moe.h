@@ -17,6 +17,14 @@
 //                 (* sorted_weights[i] if doweight), with global atomics.
 // 16-bit inputs carry no scales (the factors are 1).
 //
+// Input kinds (reference in_dtype): fp8, int8, bf16, fp16; int8 with slot-major activations
+// ("int8smooth": stage-1 x is [topk*tokens][K] with row s*tokens + t and one scale per such row,
+// moe_gemm_2stage.py:466-476); int4 weights with int8 activations (W4A8, KIND_INT4: the packed
+// preshuffled bytes of the dense int4 path, unpacked to int8 in registers); int4 weights with
+// bf16 activations (W4A16, KIND_W4A16: the nibbles converted to bf16 in registers, times a
+// per-(32-deep K group, weight row) scale when group scales are given, else the per-row scale
+// in the epilogue, as for int8; mfma_preshuffle_pipeline.py:148-222).
+//
 // W1 and W2 are preshuffled like every B operand here.  A rows are gathered by the LDS-DMA:
 // each lane's buffer offset names its own row, and padding rows get an offset past the buffer,
 // which reads zeros.  One workgroup (4 waves) per (TN-column block, sorted block of TM rows);
@@ -45,7 +53,33 @@ struct MoeArgs {
   int nsplit;                  // column ranges per run (workgroups per run)
   int out_mode;                // MoeOut
   uint32_t out_bytes;          // size of out (buffer bounds of the epilogue stores)
+  int a_token_slot;            // stage 1: x rows (and sa) per route, slot-major s*tokens + t
+  int wgroup;                  // W4A16: 32 = sw holds group scales [E][K/32][rows of W], 0 = per row
 };
+
+// Formats of the MoE input kinds.
+constexpr bool moe_w_int4(int k) { return k == KIND_INT4 || k == KIND_W4A16; }
+constexpr bool moe_a_16bit(int k) { return kind_is_16bit(k) || k == KIND_W4A16; }
+// bytes of one 16-column weight block per 128-byte K tile of the activations
+constexpr int moe_b_blk(int k) { return k == KIND_W4A16 ? 512 : (k == KIND_INT4 ? 1024 : 2048); }
+
+// Eight packed int4 weights of one 32-bit word (byte j holds element j in its low nibble and
+// element j + 4 in its high nibble, the dense int4 packing) -> eight bf16 in element order,
+// each times `s` when `scaled` (rounded to nearest even).
+__device__ __forceinline__ i32x4 int4x8_to_bf16(uint32_t p, float s, bool scaled) {
+  float f[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int off = k < 4 ? 8 * k : 8 * (k - 4) + 4;
+    const int v = ((int)(p << (28 - off))) >> 28;   // sign-extended nibble
+    f[k] = scaled ? (float)v * s : (float)v;
+  }
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  bf16x8 o;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = (__bf16)f[k];
+  return __builtin_bit_cast(i32x4, o);
+}
 
 // Stage-2 outputs: F16/BF16/F32 accumulate into out[token] with atomics; *_ROWS store each
 // route's row out[token*topk + slot] with plain stores (the reduce mode, summed by
@@ -76,23 +110,27 @@ struct MoeCfg {
   static constexpr int NR = TN / (16 * WN);           // 16-column blocks per wave and weight half
   static constexpr int NB = STAGE == 1 ? 2 : 1;       // weight halves: gate and up in stage 1
   static constexpr int A_BYTES = TME * KT;            // A part of one LDS slot
-  static constexpr int B_BYTES = NB * (TN / 16) * 2048;  // B part: NB x TN columns x 128 bytes
-  static constexpr int SLOT = A_BYTES + B_BYTES;
+  static constexpr int B_BYTES = NB * (TN / 16) * moe_b_blk(KIND);  // B part: NB x TN columns, one K tile
   static constexpr int A_DMA = A_BYTES / 1024;        // 1 KB DMA instructions per K tile
   static constexpr int AQ = (A_DMA + NW - 1) / NW;    // per wave
-  static constexpr int BQ = B_BYTES / 1024 / NW;      // per wave
+  static constexpr int B_DMA = B_BYTES / 1024;        // 1 KB DMA instructions per K tile
+  static constexpr int BQ = (B_DMA + NW - 1) / NW;    // per wave (some waves one fewer)
   static constexpr int ESZ = F32 ? 4 : 2;
   // epilogue tile row: TN values, then 16 bytes holding the row's destination (the padding also
   // spreads the rows over the LDS banks)
   static constexpr int RS = TN * ESZ + 16;
+  // one ring slot: a K step's A and B tiles, and at least 16 rows of the atomic epilogue's
+  // staging, which reuses the slot (int4 weights leave the data part small)
+  static constexpr int SLOT = A_BYTES + B_BYTES > 16 * RS ? A_BYTES + B_BYTES : 16 * RS;
   static constexpr int CH = (SLOT / RS) / 16 * 16 < TME ? (SLOT / RS) / 16 * 16 : TME;  // rows per chunk
   static constexpr int NCH = (TME + CH - 1) / CH;
   static constexpr int NST = MR * NR;                 // direct row stores per thread per column tile
   static_assert(TM % 16 == 0 && NR >= 1 && TN % (16 * WN) == 0 && TMW % 16 == 0 && A_BYTES % 1024 == 0,
                 "tile shape");
-  static_assert(B_BYTES % (1024 * NW) == 0, "B DMA split over the waves");
+  static_assert(B_BYTES % 1024 == 0, "B DMA in whole instructions");
   static_assert(CH >= 16 && NS * SLOT <= 160 * 1024, "LDS budget");
-  static_assert(NS == 2 || (NS == 3 && A_DMA % NW == 0), "a 3-slot ring counts equal DMA issues per wave");
+  static_assert(NS == 2 || (NS == 3 && A_DMA % NW == 0 && B_DMA % NW == 0),
+                "a 3-slot ring counts equal DMA issues per wave");
   static constexpr int DMA_PER_STEP = (NS == 3 ? A_DMA / NW : 0) + BQ;  // per wave (3-slot ring)
 };
 
@@ -118,7 +156,8 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   constexpr int NW = C::NW, TMW = C::TMW;
   static_assert(!BS || KIND == KIND_FP8, "blockscale is fp8");
   static_assert(STAGE == 2 || !F32, "stage 1 writes 2-byte outputs");
-  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "MoE input kinds");
+  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND) || moe_w_int4(KIND), "MoE input kinds");
+  static_assert(KIND != KIND_W4A16 || NS == 2, "W4A16 group scales ride the two-slot pipeline");
   constexpr int MR = C::MR, NR = C::NR, NB = C::NB, TME = C::TME, NT = NW * 64;
   const int mode = p.out_mode;
   const bool rows = STAGE == 1 || mode == MOE_OUT_F16_ROWS || mode == MOE_OUT_BF16_ROWS;
@@ -156,8 +195,12 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   const int wm = wave / WN, wn = wave % WN;
   const int rw0 = wm * TMW;    // this wave's first row
   const int l16 = lane & 15, lq = lane >> 4;
-  const int a_rows = STAGE == 1 ? p.tokens : p.tokens * p.topk;
-  constexpr bool kScaled = !kind_is_16bit(KIND) && !BS;  // per-token / per-row scales in the epilogue
+  const bool a_ts = STAGE == 1 && p.a_token_slot;
+  const int a_rows = STAGE == 1 && !a_ts ? p.tokens : p.tokens * p.topk;
+  // per-token activation scales and per-row weight scales in the epilogue: not for 16-bit
+  // activations (W4A16 keeps the weight scale unless it has group scales) nor blockscale
+  constexpr bool kScaledA = !moe_a_16bit(KIND) && !BS;
+  const bool scaled_w = (!kind_is_16bit(KIND) && !BS) && !(KIND == KIND_W4A16 && p.wgroup);
 
   // ---- per-row facts, fixed for the workgroup's life ----
   // Every load below is unconditional (indices clamped into range, the result masked after), so
@@ -177,7 +220,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     const int id = ida[j];
     const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
     const bool ok = rloc < rows_valid && t < p.tokens && s < p.topk;
-    const int row = STAGE == 1 ? t : t * p.topk + s;
+    const int row = STAGE == 1 ? (a_ts ? s * p.tokens + t : t) : t * p.topk + s;
     const int c = (lane & 7) ^ ((rloc >> 1) & 7);
     va[j] = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
   }
@@ -191,9 +234,9 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
     const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
     dst_r[mi] = !ok ? -1 : (rows ? t * p.topk + s : t);
-    const int arow = ok ? (STAGE == 1 ? t : t * p.topk + s) : 0;
+    const int arow = ok ? (STAGE == 1 ? (a_ts ? s * p.tokens + t : t) : t * p.topk + s) : 0;
     arow_r[mi] = arow;
-    const float sxv = kScaled ? p.sa[arow] : 1.f;
+    const float sxv = kScaledA ? p.sa[arow] : 1.f;
     const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
     sx_r[mi] = ok ? sxv : 0.f;  // 0 keeps padding rows finite; 1 for unscaled kinds
     rw_r[mi] = ok ? rwv : 0.f;
@@ -202,8 +245,13 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
   // this expert's weight rows only (the whole array may exceed 32-bit offsets)
   const int wrows = STAGE == 1 ? 2 * p.N : p.N;
-  const sgpr4 rsrc_w = buf_desc(p.w + (size_t)e * (size_t)wrows * (size_t)K, (uint32_t)wrows * (uint32_t)K);
+  // bytes per weight row: K for 1-byte weights of 1-byte activations and 2-byte of 2-byte ones,
+  // K/2 for int4 weights of int8 activations, K/4 for int4 weights of bf16 activations
+  const uint32_t wrb = KIND == KIND_W4A16 ? (uint32_t)K / 4u : (KIND == KIND_INT4 ? (uint32_t)K / 2u : (uint32_t)K);
+  const sgpr4 rsrc_w = buf_desc(p.w + (size_t)e * (size_t)wrows * wrb, (uint32_t)wrows * wrb);
   const uint32_t vb = (uint32_t)lane * 16u;
+  // W4A16: one DMA instruction brings two adjacent 16-column blocks, 512 bytes each
+  const uint32_t vb_w4 = (uint32_t)(lane & 31) * 16u + (uint32_t)(lane >> 5) * 16u * wrb;
 
   // DMA of step (column tile jt, K tile kt) into ring slot `slot`: A rows, then the B blocks
   // (local 16-column block lb: gate -- or W2 -- for lb < TN/16, up after), each 2 KB per K tile
@@ -218,11 +266,20 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     const int n0 = jt * TN;
 #pragma unroll
     for (int j = 0; j < C::BQ; ++j) {
-      const int q = wave + j * NW;           // 1 KB piece q: local block q/2, half q%2
-      const int lb = q >> 1;
-      const int nb = lb < TN / 16 ? n0 / 16 + lb : (p.N + n0) / 16 + (lb - TN / 16);
-      const uint32_t so = (uint32_t)nb * 16u * (uint32_t)K + (uint32_t)kt * 2048u + (uint32_t)(q & 1) * 1024u;
-      dma16(rsrc_w, st + C::A_BYTES + q * 1024, vb, __builtin_amdgcn_readfirstlane(so));
+      const int q = wave + j * NW;
+      if (q >= C::B_DMA) continue;           // wave-uniform
+      // local 16-column block lb (gate -- or W2 -- for lb < TN/16, up after) -> global block
+      auto gblk = [&](int lb) { return lb < TN / 16 ? n0 / 16 + lb : (p.N + n0) / 16 + (lb - TN / 16); };
+      uint32_t so, vo = vb;
+      if constexpr (KIND == KIND_W4A16) {     // piece q: blocks 2q and 2q+1 (TN/16 is even)
+        so = (uint32_t)gblk(2 * q) * 16u * wrb + (uint32_t)kt * 512u;
+        vo = vb_w4;
+      } else if constexpr (KIND == KIND_INT4) {  // piece q: block q
+        so = (uint32_t)gblk(q) * 16u * wrb + (uint32_t)kt * 1024u;
+      } else {                                // piece q: block q/2, half q%2
+        so = (uint32_t)gblk(q >> 1) * 16u * wrb + (uint32_t)kt * 2048u + (uint32_t)(q & 1) * 1024u;
+      }
+      dma16(rsrc_w, st + C::A_BYTES + q * 1024, vo, __builtin_amdgcn_readfirstlane(so));
     }
   };
 
@@ -247,6 +304,24 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     }
   };
 
+  // W4A16 group scales of the current step and of the next (as the blockscale factors): for
+  // each of this lane's weight columns, the scales of the two 32-deep K groups of the step
+  float gs_c[NB][NR][2], gs_n[NB][NR][2];
+  const int kgroups = K / 64;   // 32-element groups per weight row (K counts bf16 bytes)
+  auto load_gs = [&](int jt, int kt) {
+    if constexpr (KIND == KIND_W4A16) {
+      if (!p.wgroup) return;
+#pragma unroll
+      for (int h = 0; h < NB; ++h)
+#pragma unroll
+        for (int ni = 0; ni < NR; ++ni) {
+          const int n = (h ? p.N : 0) + jt * TN + (wn * NR + ni) * 16 + l16;
+#pragma unroll
+          for (int g = 0; g < 2; ++g) gs_n[h][ni][g] = p.sw[((size_t)e * kgroups + 2 * kt + g) * wrows + n];
+        }
+    }
+  };
+
   // One K tile: this wave's B fragments read once, then row block by row block, the next row's
   // A fragment read ahead of this row's MFMAs.  B is the MFMA's first operand, so each
   // accumulator tile holds its 16x16 output block transposed.
@@ -263,9 +338,23 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     for (int h = 0; h < NB; ++h)
 #pragma unroll
       for (int ni = 0; ni < NR; ++ni) {
-        const int off = (h * (TN / 16) + wn * NR + ni) * 2048 + lq * 256 + l16 * 16;
-        bl[h][ni] = *(const i32x4*)(sB + off);
-        bh[h][ni] = *(const i32x4*)(sB + off + 1024);
+        const int blk = h * (TN / 16) + wn * NR + ni;
+        if constexpr (KIND == KIND_W4A16) {
+          // MFMA half j takes elements 32j + 8lq .. +7 of the 64-element step: 4 bytes of
+          // 16-element chunk 2j + lq/2 of this column
+          const int off = blk * 512 + (lq >> 1) * 128 + l16 * 8 + (lq & 1) * 4;
+          const bool gsc = p.wgroup != 0;
+          bl[h][ni] = int4x8_to_bf16(*(const uint32_t*)(sB + off), gsc ? gs_c[h][ni][0] : 1.f, gsc);
+          bh[h][ni] = int4x8_to_bf16(*(const uint32_t*)(sB + off + 256), gsc ? gs_c[h][ni][1] : 1.f, gsc);
+        } else if constexpr (KIND == KIND_INT4) {
+          const int off = blk * 1024 + lq * 128 + l16 * 8;
+          bl[h][ni] = unpack_int4x16(*(const i32x2*)(sB + off));
+          bh[h][ni] = unpack_int4x16(*(const i32x2*)(sB + off + 512));
+        } else {
+          const int off = blk * 2048 + lq * 256 + l16 * 16;
+          bl[h][ni] = *(const i32x4*)(sB + off);
+          bh[h][ni] = *(const i32x4*)(sB + off + 1024);
+        }
       }
     i32x4 alo, ahi;
     load_a(0, alo, ahi);
@@ -290,8 +379,9 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
             acc[h][mi][ni] = mfma_fp8(__builtin_shufflevector(bl[h][ni], bh[h][ni], 0, 1, 2, 3, 4, 5, 6, 7),
                                       __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[h][mi][ni]);
           } else {
-            acc[h][mi][ni] = mfma_k64<KIND>(bl[h][ni], lo, acc[h][mi][ni]);
-            acc[h][mi][ni] = mfma_k64<KIND>(bh[h][ni], hi, acc[h][mi][ni]);
+            constexpr int MK = KIND == KIND_W4A16 ? KIND_BF16 : KIND;   // int4 weights: int8 or bf16 MFMA
+            acc[h][mi][ni] = mfma_k64<MK>(bl[h][ni], lo, acc[h][mi][ni]);
+            acc[h][mi][ni] = mfma_k64<MK>(bh[h][ni], hi, acc[h][mi][ni]);
           }
         }
     }
@@ -299,7 +389,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
 
   auto col_scale = [&](int jt, int h, int ni) -> f32x4 {
     const int n = jt * TN + (wn * NR + ni) * 16 + lq * 4;
-    return kScaled ? *(const f32x4*)(p.sw + (size_t)e * wrows + (h ? p.N : 0) + n) : f32x4{1.f, 1.f, 1.f, 1.f};
+    return scaled_w ? *(const f32x4*)(p.sw + (size_t)e * wrows + (h ? p.N : 0) + n) : f32x4{1.f, 1.f, 1.f, 1.f};
   };
 
   // Epilogue of column tile jt.  Lane (l16, lq) holds row mi*16 + l16, columns 4*lq .. 4*lq+3
@@ -448,6 +538,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   int slot = 0;
   bool keep_stores = false;
   load_bs(j0, 0);
+  load_gs(j0, 0);
   issue(j0, 0, 0);
   for (int jt = j0; jt < j1; ++jt) {
 #pragma unroll
@@ -463,6 +554,21 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
         wait_dma();
       keep_stores = false;
       workgroup_barrier();
+      if constexpr (KIND == KIND_W4A16) {
+        if (p.wgroup) {
+#pragma unroll
+          for (int h = 0; h < NB; ++h)
+#pragma unroll
+            for (int ni = 0; ni < NR; ++ni) {
+              gs_c[h][ni][0] = gs_n[h][ni][0];
+              gs_c[h][ni][1] = gs_n[h][ni][1];
+            }
+          if (kt + 1 < nk)
+            load_gs(jt, kt + 1);
+          else if (jt + 1 < j1)
+            load_gs(jt + 1, 0);
+        }
+      }
       if constexpr (BS) {
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) bsa_c[mi] = bsa_n[mi];

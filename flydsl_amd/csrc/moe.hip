@@ -25,7 +25,9 @@ MoeFn moe_stage1_tile(int tm, int r, int tn) {
   T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
   T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)
   T(64, 1, 256, 1, 4, 2)
-  if constexpr (!BS) {  // the blockscale partials and factors do not fit next to the run tiles
+  // run tiles: not for blockscale (its partials and factors do not fit next to them) nor W4A16
+  // (its group scales ride the two-slot pipeline)
+  if constexpr (!BS && KIND != KIND_W4A16) {
     T(16, 8, 128, 2, 4, 3) T(32, 4, 128, 2, 4, 3) T(64, 2, 128, 2, 4, 3)
   }
 #undef T
@@ -37,6 +39,8 @@ MoeFn moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
   switch (kind) {
     case KIND_FP8: return moe_stage1_tile<KIND_FP8, false>(tm, r, tn);
     case KIND_INT8: return moe_stage1_tile<KIND_INT8, false>(tm, r, tn);
+    case KIND_INT4: return moe_stage1_tile<KIND_INT4, false>(tm, r, tn);
+    case KIND_W4A16: return moe_stage1_tile<KIND_W4A16, false>(tm, r, tn);
     case KIND_BF16: return moe_stage1_tile<KIND_BF16, false>(tm, r, tn);
     case KIND_F16: return moe_stage1_tile<KIND_F16, false>(tm, r, tn);
     default: return nullptr;
@@ -61,7 +65,7 @@ int pick_tile_n(int N, long runs) {
 int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
                const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
                const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
-               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, bool bs,
+               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, bool bs, int group_size,
                hipStream_t stream) {
   const char* what = bs ? (stage == 1 ? "moe_blockscale_gemm1" : "moe_blockscale_gemm2")
                         : (stage == 1 ? "moe_gemm1" : "moe_gemm2");
@@ -80,10 +84,27 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   // Runs of several routing blocks when experts hold two or more blocks on average, on 2 x 4
   // waves: stage 1 128 rows x 128 output columns (128 gate + 128 up weight rows) with a 3-slot
   // DMA ring; stage 2 256 rows x 256 columns with 2 slots.  The caller's tile_n is then overridden: tiling does not change results.
+  int kind;
+  bool token_slot = false;
+  switch (in_dtype) {
+    case FLYGEMM_IN_FP8: kind = KIND_FP8; break;
+    case FLYGEMM_IN_INT8: kind = KIND_INT8; break;
+    case FLYGEMM_IN_INT8_SMOOTH: kind = KIND_INT8; token_slot = stage == 1; break;
+    case FLYGEMM_IN_INT4: kind = KIND_INT4; break;
+    case FLYGEMM_IN_INT4_BF16: kind = KIND_W4A16; break;
+    case FLYGEMM_IN_BF16: kind = KIND_BF16; break;
+    case FLYGEMM_IN_FP16: kind = KIND_F16; break;
+    default: return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
+  }
+  if (bs && kind != KIND_FP8) return fail(hipErrorInvalidValue, "%s: blockscale takes fp8", what);
+  // group scales: W4A16 only, 32-element groups along K (reference tests/utils.py:99-120)
+  if (group_size > 0 && (kind != KIND_W4A16 || group_size != 32))
+    return fail(hipErrorInvalidValue, "%s: group_size=%d: group scales are for int4_bf16 with group_size 32", what,
+                group_size);
   const long routes = (long)tokens * topk;
   int R = 1;
   const int run_tn = stage == 1 ? 128 : 256;
-  if (!bs && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
+  if (!bs && kind != KIND_W4A16 && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
     R = (stage == 1 ? 128 : 256) / tile_m;   // stage 1: 128 rows, three LDS slots
     tile_n = run_tn;
   }
@@ -105,21 +126,14 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (tile_n != 64 && tile_n != 128 && tile_n != 256)
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
   if (N % tile_n != 0) return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
-  int kind;
-  switch (in_dtype) {
-    case FLYGEMM_IN_FP8: kind = KIND_FP8; break;
-    case FLYGEMM_IN_INT8: kind = KIND_INT8; break;
-    case FLYGEMM_IN_BF16: kind = KIND_BF16; break;
-    case FLYGEMM_IN_FP16: kind = KIND_F16; break;
-    default: return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
-  }
-  const bool is16 = kind_is_16bit(kind);
-  const long kb = is16 ? 2L * K : (long)K;
+  const bool is16 = moe_a_16bit(kind);      // 2-byte activations (bf16, fp16, W4A16)
+  const long kb = is16 ? 2L * K : (long)K;  // activation bytes per row
   if (kb % 128 != 0)
     return fail(hipErrorInvalidValue, "%s: K=%d must be a multiple of %d (128-byte K tile)", what, K, is16 ? 64 : 128);
-  const long a_rows = stage == 1 ? tokens : (long)tokens * topk;
+  const long a_rows = stage == 1 && !token_slot ? tokens : (long)tokens * topk;
   const long w_rows = stage == 1 ? 2L * N : (long)N;
-  if (a_rows * kb >= (1L << 31) || w_rows * kb >= (1L << 31))
+  const long wb = moe_w_int4(kind) ? K / 2 : kb;  // weight bytes per row
+  if (a_rows * kb >= (1L << 31) || w_rows * wb >= (1L << 31))
     return fail(hipErrorInvalidValue, "%s: activation or per-expert weight above 2^31 bytes", what);
   int mout;
   const bool rows = stage == 2 && !accumulate;
@@ -131,7 +145,8 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (tokens == 0 || blocks == 0) return 0;
   if (!out || !a || !w || !sorted_ids || !expert_ids || !num_valid)
     return fail(hipErrorInvalidValue, "%s: null tensor pointer", what);
-  if (!is16 && (!sa || !sw)) return fail(hipErrorInvalidValue, "%s: null scale pointer", what);
+  const bool need_sa = !is16, need_sw = !kind_is_16bit(kind);
+  if ((need_sa && !sa) || (need_sw && !sw)) return fail(hipErrorInvalidValue, "%s: null scale pointer", what);
   if (doweight && !sorted_w) return fail(hipErrorInvalidValue, "%s: null sorted_weights with doweight", what);
 
   const long out_bytes = (stage == 1 || !accumulate) ? (long)tokens * topk * N * 2
@@ -152,7 +167,8 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   nsplit = nsplit < 1 ? 1 : (nsplit > ntn ? ntn : nsplit);
   MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
                sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
-               doweight ? 1 : 0, blocks, (int)nsplit, mout, (uint32_t)out_bytes};
+               doweight ? 1 : 0, blocks, (int)nsplit, mout, (uint32_t)out_bytes, token_slot ? 1 : 0,
+               group_size > 0 ? group_size : 0};
   // grid (N / tile_n, blocks) in the reference; here one dimension over (block, column range),
   // rounded up to a multiple of 8 for the kernel's XCD-aware order (the extra workgroups and
   // those that do not start a run exit at once)
@@ -173,10 +189,11 @@ int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scal
                       const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
                       const int32_t* num_valid_ids, int32_t tokens, int32_t inter_dim, int32_t model_dim,
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
-                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream) {
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, int32_t group_size,
+                      void* stream) {
   return moe_launch(1, out, x, w, scale_x, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights, num_valid_ids,
                     tokens, inter_dim, model_dim, size_expert_ids, experts, topk, tile_m, tile_n, in_dtype, out_dtype,
-                    doweight_stage1, 1, false, (hipStream_t)stream);
+                    doweight_stage1, 1, false, group_size, (hipStream_t)stream);
 }
 
 int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* scale_a2, const float* scale_w,
@@ -184,10 +201,10 @@ int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* sca
                       const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
                       int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, int32_t accumulate,
-                      void* stream) {
+                      int32_t group_size, void* stream) {
   return moe_launch(2, out, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
                     num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
-                    in_dtype, out_dtype, doweight_stage2, accumulate, false, (hipStream_t)stream);
+                    in_dtype, out_dtype, doweight_stage2, accumulate, false, group_size, (hipStream_t)stream);
 }
 
 int flygemm_moe_blockscale_gemm1(void* out, const void* x, const void* w, const float* x_scale_t,
@@ -201,7 +218,7 @@ int flygemm_moe_blockscale_gemm1(void* out, const void* x, const void* w, const 
     return fail(hipErrorInvalidValue, "moe_blockscale_gemm1: scale_block_k=%d: only 128 is supported", scale_block_k);
   return moe_launch(1, out, x, w, x_scale_t, w_scale, sorted_token_ids, sorted_expert_ids, sorted_weights,
                     num_valid_ids, tokens, inter_dim, model_dim, size_expert_ids, experts, topk, tile_m, tile_n,
-                    FLYGEMM_IN_FP8, out_dtype, doweight_stage1, 1, true, (hipStream_t)stream);
+                    FLYGEMM_IN_FP8, out_dtype, doweight_stage1, 1, true, -1, (hipStream_t)stream);
 }
 
 int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const float* a2_scale_t,
@@ -215,7 +232,7 @@ int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const
     return fail(hipErrorInvalidValue, "moe_blockscale_gemm2: scale_block_k=%d: only 128 is supported", scale_block_k);
   return moe_launch(2, out, a2, w, a2_scale_t, w_scale, sorted_token_ids, sorted_expert_ids, sorted_weights,
                     num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
-                    FLYGEMM_IN_FP8, out_dtype, doweight_stage2, accumulate, true, (hipStream_t)stream);
+                    FLYGEMM_IN_FP8, out_dtype, doweight_stage2, accumulate, true, -1, (hipStream_t)stream);
 }
 
 int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t tokens, int32_t topk,

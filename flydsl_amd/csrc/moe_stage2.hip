@@ -13,7 +13,9 @@ MoeFn stage2_tile(int tm, int r, int tn) {
   if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, WM_, WN_, F32, BS>;
   T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(16, 1, 256, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4)
   T(32, 1, 256, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4) T(64, 1, 256, 1, 4)
-  if constexpr (!BS) {  // the blockscale partials and factors do not fit next to the run tiles
+  // run tiles: not for blockscale (its partials and factors do not fit next to them) nor W4A16
+  // (its group scales ride the two-slot pipeline)
+  if constexpr (!BS && KIND != KIND_W4A16) {
     T(16, 16, 256, 2, 4) T(32, 8, 256, 2, 4) T(64, 4, 256, 2, 4)
   }
 #undef T
@@ -34,6 +36,8 @@ MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs) {
   switch (kind) {
     case KIND_FP8: return stage2_kind<KIND_FP8>(tm, r, tn, f32);
     case KIND_INT8: return stage2_kind<KIND_INT8>(tm, r, tn, f32);
+    case KIND_INT4: return stage2_kind<KIND_INT4>(tm, r, tn, f32);
+    case KIND_W4A16: return stage2_kind<KIND_W4A16>(tm, r, tn, f32);
     case KIND_BF16: return stage2_kind<KIND_BF16>(tm, r, tn, f32);
     case KIND_F16: return stage2_kind<KIND_F16>(tm, r, tn, f32);
     default: return nullptr;

@@ -21,9 +21,14 @@ produces with ``block_size == tile_m``.
 Behind the launchers: ``flygemm_moe_gemm1`` / ``flygemm_moe_gemm2`` of ``include/flygemm.h``,
 hand-written gfx950 kernels; no JIT and no host fallback.
 
-Built: ``in_dtype`` fp8, int8 (per-token x scale, per-row weight scale), fp16, bf16 (unscaled);
-``group_size=-1``; ``tile_m`` 16/32/64; ``tile_n`` 64/128/256.  ``int8smooth``, ``int4``,
-``int4_bf16`` and group-wise scales raise ``NotImplementedError``.  Stage 2 also has the
+Built: every ``in_dtype`` of the reference -- fp8, int8 (per-token x scale, per-row weight scale),
+fp16, bf16 (unscaled), ``int8smooth`` (stage-1 x given per route, slot-major rows
+``s*tokens + t`` with their own scales; stage 2 as int8), ``int4`` (W4A8: int8 x, packed int4
+weights), ``int4_bf16`` (W4A16: bf16 x, packed int4 weights with per-row scales, or with
+``group_size=32`` group scales ``[E, K/32, rows]``, reference ``tests/utils.py:99-120``);
+``tile_m`` 16/32/64; ``tile_n`` 64/128/256.  ``group_size > 0`` with another in_dtype raises
+``ValueError`` (the reference accepts and ignores it; its harness skips those cases,
+``tests/kernels/test_moe_gemm.py:1230-1231``).  Stage 2 also has the
 reference's reduce mode (``accumulate=False`` + ``compile_moe_reduction``, or
 ``compile_moe_gemm2_ex(mode=MoeGemm2Mode.REDUCE)``): per-route rows with plain stores, then a
 reduction over the top-k slots -- about three times faster than atomics on MI355X, whose atomic
@@ -38,8 +43,8 @@ from .. import _lib
 from ._launch import device_ptr, stream_handle
 
 _ALL_IN = ("fp8", "fp16", "bf16", "int8", "int8smooth", "int4", "int4_bf16")
-_BUILT_IN = {"fp8": "fp8", "int8": "int8", "bf16": "bf16", "fp16": "fp16"}
-_T16 = {"bf16": torch.bfloat16, "fp16": torch.float16}
+_T16 = {"bf16": torch.bfloat16, "fp16": torch.float16, "int4_bf16": torch.bfloat16}   # 2-byte activations
+_W4 = ("int4", "int4_bf16")   # packed int4 weights
 _OUT = {"f16": ("fp16", torch.float16), "bf16": ("bf16", torch.bfloat16), "f32": ("fp32", torch.float32)}
 # stage 2 spellings the reference accepts (moe_gemm_2stage.py:1315-1316)
 _OUT_ALIAS = {"fp16": "f16", "half": "f16", "bfloat16": "bf16", "fp32": "f32", "float": "f32"}
@@ -53,10 +58,9 @@ def _check_common(in_dtype, group_size, tile_m, tile_n, tile_k):
         raise ValueError(f"tile_k_bytes must be divisible by 64, got tile_k={tile_k} (elem_bytes={elem})")
     if (int(tile_m) * int(tile_k) * elem) % 256:
         raise ValueError(f"tile_m*tile_k*elem_bytes must be divisible by 256: tile_m={tile_m}, tile_k={tile_k}")
-    if in_dtype not in _BUILT_IN:
-        raise NotImplementedError(f"in_dtype={in_dtype!r} has no MI355X MoE kernel in this build")
-    if int(group_size) > 0:
-        raise NotImplementedError("group-wise weight scales (group_size > 0) are not built")
+    if int(group_size) > 0 and (in_dtype != "int4_bf16" or int(group_size) != 32):
+        raise ValueError(f"group_size={group_size}: group-wise weight scales are built for in_dtype='int4_bf16' "
+                         f"with group_size=32")
     if int(tile_m) not in (16, 32, 64):
         raise ValueError(f"tile_m={tile_m}: the MI355X kernels take routing blocks of 16, 32 or 64 rows")
     if int(tile_n) not in (64, 128, 256):
@@ -66,7 +70,7 @@ def _check_common(in_dtype, group_size, tile_m, tile_n, tile_k):
 
 class _MoeStage:
     def __init__(self, stage, *, model_dim, inter_dim, experts, topk, tile_m, tile_n, tile_k, doweight, in_dtype,
-                 out_dtype, elem, accumulate=True, blockscale=False):
+                 out_dtype, elem, accumulate=True, blockscale=False, group_size=-1):
         self.stage = stage
         self.model_dim, self.inter_dim = int(model_dim), int(inter_dim)
         self.experts, self.topk = int(experts), int(topk)
@@ -76,6 +80,7 @@ class _MoeStage:
         self.elem = elem
         self.accumulate = bool(accumulate)
         self.blockscale = bool(blockscale)   # fp8 with 1x128 / 128x128 block scales
+        self.group_size = int(group_size) if int(group_size) > 0 else -1
 
     def __call__(self, arg_out, arg_x, arg_w, arg_scale_x, arg_scale_w, arg_sorted_token_ids, arg_expert_ids,
                  arg_sorted_weights, arg_num_valid_ids, tokens, n_in, k_in, size_expert_ids, stream=None):
@@ -91,18 +96,27 @@ class _MoeStage:
         if K % self.tile_k:
             raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
         E, topk = self.experts, self.topk
-        a_rows = tokens if self.stage == 1 else tokens * topk
+        # int8smooth stage 1 takes x per route (slot-major rows s*tokens + t)
+        per_route = self.stage == 2 or self.in_dtype == "int8smooth"
+        a_rows = tokens * topk if per_route else tokens
         w_rows = E * 2 * N if self.stage == 1 else E * N
+        w_bytes = w_rows * K // 2 if self.in_dtype in _W4 else w_rows * K
         out_name, out_t = _OUT[self.out_dtype]
         out_elems = tokens * topk * N if (self.stage == 1 or not self.accumulate) else tokens * N
         o = device_ptr(arg_out, "arg_out", out_elems, dtypes=(out_t,))
         if self.in_dtype in _T16:
             x = device_ptr(arg_x, "arg_x", a_rows * K, dtypes=(_T16[self.in_dtype],))
-            w = device_ptr(arg_w, "arg_w", w_rows * K, dtypes=(_T16[self.in_dtype],))
-            sx = sw = 0  # unscaled; the reference passes empty tensors
+            sx = 0  # unscaled activations; the reference passes empty tensors
+            if self.in_dtype == "int4_bf16":
+                w = device_ptr(arg_w, "arg_w", w_bytes, elem_bytes=1)
+                nsw = w_rows * (K // self.group_size) if self.group_size > 0 else w_rows
+                sw = device_ptr(arg_scale_w, "arg_scale_w", nsw, dtypes=(torch.float32,))
+            else:
+                w = device_ptr(arg_w, "arg_w", w_rows * K, dtypes=(_T16[self.in_dtype],))
+                sw = 0
         else:
             x = device_ptr(arg_x, "arg_x", a_rows * K, elem_bytes=1)
-            w = device_ptr(arg_w, "arg_w", w_rows * K, elem_bytes=1)
+            w = device_ptr(arg_w, "arg_w", w_bytes, elem_bytes=1)
             nsx, nsw = (a_rows * (K // 128), w_rows // 128 * (K // 128)) if self.blockscale else (a_rows, w_rows)
             sx = device_ptr(arg_scale_x, "arg_scale_x", nsx, dtypes=(torch.float32,))
             sw = device_ptr(arg_scale_w, "arg_scale_w", nsw, dtypes=(torch.float32,))
@@ -115,12 +129,16 @@ class _MoeStage:
                if self.doweight else 0)
         nv = device_ptr(arg_num_valid_ids, "arg_num_valid_ids", 1, dtypes=(torch.int32,))
         lib = _lib.load()
-        dt = 128 if self.blockscale else _lib.FLYGEMM_IN[_BUILT_IN[self.in_dtype]]   # scale_block_k / in_dtype
+        dt = 128 if self.blockscale else _lib.FLYGEMM_IN[self.in_dtype]   # scale_block_k / in_dtype
         args = (o, x, w, sx, sw, ids, eids, sws, nv, tokens, N, K, blocks, E, topk, self.tile_m, self.tile_n, dt,
                 _lib.FLYGEMM_OUT[out_name], int(self.doweight))
         name = f"flygemm_moe_{'blockscale_' if self.blockscale else ''}gemm{self.stage}"
         fn = getattr(lib, name)
-        rc = fn(*args, h_stream) if self.stage == 1 else fn(*args, int(self.accumulate), h_stream)
+        tail = () if self.blockscale else (self.group_size,)
+        if self.stage == 1:
+            rc = fn(*args, *tail, h_stream)
+        else:
+            rc = fn(*args, int(self.accumulate), *tail, h_stream)
         _lib.check(rc, name)
 
 
@@ -135,14 +153,14 @@ def compile_moe_gemm1(*, model_dim: int, inter_dim: int, experts: int, topk: int
         raise ValueError(f"inter_dim={inter_dim} % tile_n={tile_n} and model_dim={model_dim} % tile_k={tile_k} must be 0")
     return _MoeStage(1, model_dim=model_dim, inter_dim=inter_dim, experts=experts, topk=topk, tile_m=tile_m,
                      tile_n=tile_n, tile_k=tile_k, doweight=doweight_stage1, in_dtype=in_dtype, out_dtype=out_dtype,
-                     elem=elem)
+                     elem=elem, group_size=group_size)
 
 
 def compile_moe_gemm2(*, model_dim: int, inter_dim: int, experts: int, topk: int, tile_m: int, tile_n: int,
                       tile_k: int, doweight_stage2: bool, in_dtype: str = "fp8", group_size: int = -1,
                       out_dtype: str = "f16", use_cshuffle_epilog=None, accumulate: bool = True):
     """Stage 2 (down GEMM accumulated over the top-k slots); validates like reference
-    ``moe_gemm_2stage.py:1300-1430``.  ``accumulate=False`` (the reduce mode) is not built."""
+    ``moe_gemm_2stage.py:1300-1430``.  ``accumulate=False`` writes per-route rows (reduce mode)."""
     elem = _check_common(in_dtype, group_size, tile_m, tile_n, tile_k)
     out_dtype = _OUT_ALIAS.get(str(out_dtype).strip().lower(), out_dtype)
     if out_dtype not in ("f16", "bf16", "f32"):
@@ -153,7 +171,7 @@ def compile_moe_gemm2(*, model_dim: int, inter_dim: int, experts: int, topk: int
         raise ValueError(f"model_dim={model_dim} % tile_n={tile_n} and inter_dim={inter_dim} % tile_k={tile_k} must be 0")
     return _MoeStage(2, model_dim=model_dim, inter_dim=inter_dim, experts=experts, topk=topk, tile_m=tile_m,
                      tile_n=tile_n, tile_k=tile_k, doweight=doweight_stage2, in_dtype=in_dtype, out_dtype=out_dtype,
-                     elem=elem, accumulate=accumulate)
+                     elem=elem, accumulate=accumulate, group_size=group_size)
 
 
 _RED_DT = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}

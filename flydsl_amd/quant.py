@@ -2,11 +2,11 @@
 
 Mirrors the reference's helpers in ``tests/utils.py``:
 
-* ``pertoken_quant``  (``tests/utils.py:29-73``): per-row symmetric quantization,
-  ``scale = amax / dtypeMax`` (zero rows -> 1), ``q = cast(x / scale)``.  The reference's
-  int8 cast truncates toward zero (``.to(torch.int8)``); here int8/int4 round half to
-  even and clamp (``rounding="nearest"``, the rule the measured workloads specify);
-  ``rounding="trunc"`` reproduces the reference's cast.
+* ``pertoken_quant``  (``tests/utils.py:29-73``, same arguments): per-row symmetric
+  quantization of ``x * x_scale`` (smooth quant), ``scale = amax / dtypeMax`` (zero rows -> 1)
+  unless given, ``q = cast(x / scale)``.  The reference's int8 cast truncates toward zero
+  (``.to(torch.int8)``); here int8/int4 round half to even and clamp (``rounding="nearest"``,
+  the rule the measured workloads specify); ``rounding="trunc"`` reproduces the reference's cast.
 * ``shuffle_weight``  (``tests/utils.py:76-96``, 1-byte elements, ``layout=(16, 16)``):
   the B preshuffle, byte (n, k) -> ``[n//16][k//16][n%16][k%16]``.
 * ``pack_int4``       (``tests/kernels/test_preshuffle_gemm.py:165-174``): two int4 per byte
@@ -22,23 +22,34 @@ FP8 = torch.float8_e4m3fn  # OCP e4m3: the gfx950 MFMA fp8 format
 _QMAX = {torch.int8: 127.0, FP8: 448.0}
 
 
-def pertoken_quant(x: torch.Tensor, quant_dtype=torch.int8, dtypeMax=None, rounding: str = "nearest"):
-    """Returns (q [rows, cols] of quant_dtype, scale [rows, 1] fp32)."""
+def pertoken_quant(x: torch.Tensor, scale=None, x_scale=None, scale_dtype=torch.float32, quant_dtype=torch.int8,
+                   dtypeMax=None, *, rounding: str = "nearest"):
+    """Per-row quantization with the reference's arguments (``tests/utils.py:29-73``).
+
+    ``x_scale`` (smooth quant): the rows are multiplied by it first (broadcast, e.g. a per-column
+    ``[1, cols]`` smoothing factor).  ``scale``: use these per-row scales instead of
+    ``amax / dtypeMax``.  Non-finite inputs are scrubbed (NaN -> 0, +-inf -> +-dtypeMax) and
+    non-finite scales become 1, as in the reference.  ``scale_dtype``: dtype of the returned
+    scales.  Returns (q [rows, cols] of quant_dtype, scale [rows, 1])."""
     x = x.to(torch.float32)
+    hidden = x if x_scale is None else x * torch.as_tensor(x_scale, dtype=torch.float32, device=x.device)
     if dtypeMax is None:
         dtypeMax = _QMAX[quant_dtype]
-    x = torch.nan_to_num(x, nan=0.0, posinf=float(dtypeMax), neginf=-float(dtypeMax))
-    amax = torch.maximum(torch.amax(x, dim=-1, keepdim=True), -torch.amin(x, dim=-1, keepdim=True))
-    scale = amax / dtypeMax
-    scale[scale == 0] = 1
-    scale = torch.nan_to_num(scale, nan=1.0, posinf=1.0, neginf=1.0)
-    y = x / scale
+    hidden = torch.nan_to_num(hidden, nan=0.0, posinf=float(dtypeMax), neginf=-float(dtypeMax))
+    if scale is None:
+        amax = torch.maximum(torch.amax(hidden, dim=-1, keepdim=True), -torch.amin(hidden, dim=-1, keepdim=True))
+        per_row = amax / dtypeMax
+        per_row[per_row == 0] = 1
+    else:
+        per_row = torch.as_tensor(scale, device=x.device).to(torch.float32)
+    per_row = torch.nan_to_num(per_row, nan=1.0, posinf=1.0, neginf=1.0)
+    y = hidden / per_row
     if quant_dtype == torch.int8:
         if rounding == "nearest":
             y = torch.round(y).clamp_(-dtypeMax, dtypeMax)
         elif rounding != "trunc":
             raise ValueError(f"rounding must be 'nearest' or 'trunc', got {rounding!r}")
-    return y.to(quant_dtype), scale.to(torch.float32)
+    return y.to(quant_dtype), per_row.to(scale_dtype)
 
 
 def blockscale_quant(x: torch.Tensor, block_rows: int, block_cols: int = 128, dtypeMax: float = 448.0):

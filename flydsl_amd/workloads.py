@@ -131,7 +131,7 @@ class MoeWorkload:
     tile_m: int
     tile_n1: int
     tile_n2: int
-    kind: str = "fp8"     # "fp8" | "int8" | "bf16" | "fp16" | "fp8_block" (1x128 / 128x128 block scales)
+    kind: str = "fp8"     # "fp8" | "int8" | "int8smooth" | "int4" | "int4_bf16" | "bf16" | "fp16" | "fp8_block"
     seed: int = 0
     note: str = ""
 
@@ -173,11 +173,11 @@ def _moe_quant(x: torch.Tensor, kind: str, weight: bool = False):
         return x.to(_MOE_T16[kind]), None
     if kind == "fp8_block":
         return quant.blockscale_quant(x, 128 if weight else 1, 128)
-    q, s = quant.pertoken_quant(x.reshape(-1, x.shape[-1]), quant.FP8 if kind == "fp8" else torch.int8)
+    q, s = quant.pertoken_quant(x.reshape(-1, x.shape[-1]), quant_dtype=quant.FP8 if kind == "fp8" else torch.int8)
     return q.reshape(x.shape), s.reshape(-1)
 
 
-def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
+def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True, group_size: int = -1) -> dict:
     """Synthetic operands drawn as the reference's 2-stage test draws them
     (``test_moe_gemm.py:1236-1262``: x ~ 0.2 N(0,1), W1 ~ 0.2 N(0,1), W2 ~ 0.2/sqrt(I) N(0,1),
     routing = softmax over the top-k of uniform scores), generated on ``device`` from
@@ -185,7 +185,16 @@ def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
     metadata from ``flydsl_amd.moe.moe_sorting`` with ``block_size = tile_m``.
 
     The stage-2 input ``a2`` [tokens*topk, inter_dim] is drawn directly (0.2 N(0,1), quantized
-    per row) so stage 2 can be measured and tested on its own."""
+    per row) so stage 2 can be measured and tested on its own.
+
+    Kinds beyond fp8/int8/bf16/fp16/fp8_block follow the reference harness's preparation
+    (``test_moe_gemm.py:414-450,471-491``): ``int8smooth`` -- a per-expert smoothing factor
+    0.75 + 0.5 U(0,1) per column, x expanded per route and quantized per route, passed
+    slot-major (``x`` [topk*tokens, D], ``sx`` [topk*tokens]; ``x_route`` / ``sx_route`` keep
+    [tokens, topk, ...]); ``int4`` -- int8 x, weights quantized per row to [-7, 7] and packed two
+    per byte after the shuffle; ``int4_bf16`` -- bf16 x and the same int4 weights, with
+    ``group_size = 32`` group scales 0.005 + 0.05 U(0,1) of shape [E, K/32, rows] (``w1_groups``,
+    ``w2_groups``; ``sw1`` / ``sw2`` then hold them flat) in place of the per-row scales."""
     from .moe import moe_sorting
 
     g = torch.Generator(device=device).manual_seed(w.seed)
@@ -196,19 +205,47 @@ def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
     score = torch.rand(T, E, generator=g, device=device)
     vals, topk_ids = torch.topk(score, k=k, dim=1)
     topk_w = torch.softmax(vals, dim=1).float()
-    xq, sx = _moe_quant(x, w.kind)
-    w1q, sw1 = _moe_quant(w1, w.kind, weight=True)
-    w2q, sw2 = _moe_quant(w2, w.kind, weight=True)
+    kind = w.kind
+    extra = {}
+    if kind in ("int4", "int4_bf16"):
+        xq, sx = _moe_quant(x, "int8" if kind == "int4" else "bf16")
+        w1q, sw1 = quant.pertoken_quant(w1, quant_dtype=torch.int8, dtypeMax=7)
+        w2q, sw2 = quant.pertoken_quant(w2, quant_dtype=torch.int8, dtypeMax=7)
+        sw1, sw2 = sw1.reshape(-1), sw2.reshape(-1)
+        if kind == "int4_bf16" and group_size > 0:
+            w1g = torch.rand(E, D // group_size, 2 * I, generator=g, device=device) * 0.05 + 0.005
+            w2g = torch.rand(E, I // group_size, D, generator=g, device=device) * 0.05 + 0.005
+            extra.update(w1_groups=w1g, w2_groups=w2g)
+            sw1, sw2 = w1g.contiguous().view(-1), w2g.contiguous().view(-1)
+        w1_dev = quant.pack_int4(quant.shuffle_weight(w1q))
+        w2_dev = quant.pack_int4(quant.shuffle_weight(w2q))
+    else:
+        if kind == "int8smooth":
+            smooth = 0.75 + 0.5 * torch.rand(E, D, generator=g, device=device)
+            x_route = x[:, None, :] * smooth[topk_ids.long()]               # [T, k, D]
+            q, sr = quant.pertoken_quant(x_route.reshape(T * k, D), quant_dtype=torch.int8)
+            q, sr = q.view(T, k, D), sr.view(T, k)
+            extra.update(x_route=q, sx_route=sr, smooth=smooth)
+            xq = q.permute(1, 0, 2).contiguous().view(k * T, D)          # slot-major rows s*T + t
+            sx = sr.t().contiguous().view(-1)
+            wk = "int8"
+        else:
+            xq, sx = _moe_quant(x, kind)
+            wk = kind
+        w1q, sw1 = _moe_quant(w1, wk, weight=True)
+        w2q, sw2 = _moe_quant(w2, wk, weight=True)
+        w1_dev, w2_dev = quant.shuffle_weight(w1q), quant.shuffle_weight(w2q)
     del w1, w2
     sid, sw, eid, post = moe_sorting(topk_ids.to(torch.int32), topk_w, E, w.tile_m)
-    out = dict(workload=w, x=xq, sx=sx, w1=w1q, sw1=sw1, w1_shuf=quant.shuffle_weight(w1q), w2=w2q, sw2=sw2,
-               w2_shuf=quant.shuffle_weight(w2q), topk_ids=topk_ids.to(torch.int32), topk_weights=topk_w,
+    out = dict(workload=w, x=xq, sx=sx, w1=w1q, sw1=sw1, w1_shuf=w1_dev, w2=w2q, sw2=sw2,
+               w2_shuf=w2_dev, topk_ids=topk_ids.to(torch.int32), topk_weights=topk_w,
                sorted_ids=sid, sorted_weights=sw, sorted_expert_ids=eid, num_valid_ids=post[:1].contiguous(),
-               blocks=int(eid.numel()))
+               blocks=int(eid.numel()), group_size=group_size, **extra)
     if with_stage2_input:
         a2 = torch.randn(T * k, I, generator=g, device=device) * s
-        out["a2"], out["sa2"] = _moe_quant(a2, w.kind)
-    if w.kind == "fp8_block":
+        a2_kind = {"int8smooth": "int8", "int4": "int8", "int4_bf16": "bf16"}.get(kind, kind)
+        out["a2"], out["sa2"] = _moe_quant(a2, a2_kind)
+    if kind == "fp8_block":
         # the kernels take activation block scales K-block major ([K/128, rows], the reference's
         # transpose_scale layout) and weight block scales flat; *_blocks keep [rows, K/128]
         out["sx_blocks"], out["sx"] = sx, sx.t().contiguous().view(-1)
@@ -219,15 +256,27 @@ def moe_problem(w: MoeWorkload, device, with_stage2_input: bool = True) -> dict:
     return out
 
 
-def moe_bytes(w: MoeWorkload, stage: int, active_experts: int) -> int:
+def moe_bytes(w: MoeWorkload, stage: int, active_experts: int, group_size: int = -1) -> float:
     """Algorithmic HBM bytes of one stage: each active expert's weights and every activation,
-    scale and output element once (index/weight metadata included)."""
-    eb = 2 if w.kind in _MOE_T16 else 1
+    scale and output element once (index/weight metadata included).  Packed int4 weights count
+    half a byte; ``int8smooth`` reads stage-1 activations per route; group scales (int4_bf16,
+    ``group_size`` > 0) are one float per weight row and K group."""
+    eb = 2 if w.kind in _MOE_T16 or w.kind == "int4_bf16" else 1     # activation bytes
+    wb = 0.5 if w.kind in ("int4", "int4_bf16") else eb               # weight bytes
     T, D, I, k = w.tokens, w.model_dim, w.inter_dim, w.topk
     meta = 4 * (T * k + w.experts * w.tile_m) * 2
     bs = w.kind == "fp8_block"   # block scales: per (row, 128 K) for activations, 128 x 128 for weights
+    a_scaled = w.kind != "int4_bf16" and w.kind not in _MOE_T16
     if stage == 1:
-        sc = (T * (D // 128) + active_experts * (2 * I // 128) * (D // 128)) if bs else (T + active_experts * 2 * I)
-        return active_experts * 2 * I * D * eb + T * D * eb + T * k * I * 2 + sc * 4 + meta
-    sc = (T * k * (I // 128) + active_experts * (D // 128) * (I // 128)) if bs else (T * k + active_experts * D)
-    return active_experts * D * I * eb + T * k * I * eb + T * D * 2 + sc * 4 + meta
+        x_rows = T * k if w.kind == "int8smooth" else T
+        if bs:
+            sc = T * (D // 128) + active_experts * (2 * I // 128) * (D // 128)
+        else:
+            wsc = active_experts * 2 * I * (D // group_size if group_size > 0 else 1)
+            sc = (x_rows if a_scaled else 0) + wsc
+        return active_experts * 2 * I * D * wb + x_rows * D * eb + T * k * I * 2 + sc * 4 + meta
+    if bs:
+        sc = T * k * (I // 128) + active_experts * (D // 128) * (I // 128)
+    else:
+        sc = (T * k if a_scaled else 0) + active_experts * D * (I // group_size if group_size > 0 else 1)
+    return active_experts * D * I * wb + T * k * I * eb + T * D * 2 + sc * 4 + meta

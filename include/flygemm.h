@@ -40,7 +40,9 @@ enum {
   FLYGEMM_IN_INT4 = 2, /* int8 A, packed signed int4 B */
   FLYGEMM_IN_BF16 = 3, /* bf16 A and B, no scaling (scale pointers ignored) */
   FLYGEMM_IN_FP16 = 4, /* fp16 A and B, no scaling (scale pointers ignored) */
-  FLYGEMM_IN_FP4 = 5   /* MXFP4: flygemm_mxfp4 only (and flygemm_select_variant) */
+  FLYGEMM_IN_FP4 = 5,  /* MXFP4: flygemm_mxfp4 only (and flygemm_select_variant) */
+  FLYGEMM_IN_INT4_BF16 = 6,  /* MoE only: bf16 activations, packed int4 weights (W4A16) */
+  FLYGEMM_IN_INT8_SMOOTH = 7 /* MoE only: int8, stage-1 activations per route, slot-major */
 };
 enum { FLYGEMM_OUT_BF16 = 0, FLYGEMM_OUT_FP16 = 1, FLYGEMM_OUT_F32 = 2 /* flygemm_mxfp4 only */ };
 
@@ -107,8 +109,20 @@ int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int3
  *   sorted_expert_ids int32 [size_expert_ids]: the expert of each tile_m-row block (-1: none);
  *   sorted_weights fp32, aligned with sorted_token_ids (read only when doweight != 0);
  *   num_valid_ids int32 [1]: padded row count; blocks at or past it do nothing.
- * in_dtype FLYGEMM_IN_FP8 / _INT8 (per-token scale_x, per-row scale_w) or _BF16 / _FP16
- * (unscaled; scale pointers ignored).  Weights preshuffled as B everywhere here.
+ * in_dtype (the reference's in_dtype strings, kernels/moe_gemm_2stage.py:110-121):
+ *   FLYGEMM_IN_FP8 / _INT8: per-token scale_x, per-row scale_w;
+ *   FLYGEMM_IN_INT8_SMOOTH ("int8smooth"): int8 whose stage-1 activations are given per route,
+ *     x [topk*tokens][model_dim] with row s*tokens + t (slot-major) and scale_x [topk*tokens] in
+ *     the same order; stage 2 is plain int8;
+ *   FLYGEMM_IN_INT4 ("int4", W4A8): int8 activations, weights packed two int4 per byte exactly as
+ *     the dense int4 B (the preshuffled int8 bytes, then packed), per-row scale_w;
+ *   FLYGEMM_IN_INT4_BF16 ("int4_bf16", W4A16): bf16 activations (no scale_x), the same packed int4
+ *     weights, converted to bf16 in registers; scale_w per weight row when group_size <= 0, or
+ *     group scales [experts][K/32][rows of the expert's weight] (w[n][k] * scale[e][k/32][n],
+ *     tests/kernels/test_ref.py:44-50,117-123) when group_size == 32;
+ *   FLYGEMM_IN_BF16 / _FP16: unscaled (scale pointers ignored).
+ * group_size: -1 (or 0) for per-row weight scales; 32 only with FLYGEMM_IN_INT4_BF16.
+ * Weights preshuffled as B everywhere here.
  * tile_m (16, 32, 64) is the routing block size the metadata was built with; tile_n (64, 128,
  * 256, or 0 to choose) must divide the output width.  K % 128 == 0 (K % 64 for 16-bit).
  *
@@ -122,7 +136,8 @@ int flygemm_moe_gemm1(void* out, const void* x, const void* w, const float* scal
                       const int32_t* sorted_token_ids, const int32_t* sorted_expert_ids, const float* sorted_weights,
                       const int32_t* num_valid_ids, int32_t tokens, int32_t inter_dim, int32_t model_dim,
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
-                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, void* stream);
+                      int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage1, int32_t group_size,
+                      void* stream);
 
 /* Stage 2, per route r = (t, s) of expert e: y_r[n] = (a2[t*topk+s].W2[e*D+n]) * sa[t*topk+s]
  *   * sw[e*D+n] (* sorted_weights if doweight_stage2); a2 [tokens*topk][inter_dim], W2
@@ -139,7 +154,7 @@ int flygemm_moe_gemm2(void* out, const void* a2, const void* w, const float* sca
                       const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim, int32_t inter_dim,
                       int32_t size_expert_ids, int32_t experts, int32_t topk, int32_t tile_m, int32_t tile_n,
                       int32_t in_dtype, int32_t out_dtype, int32_t doweight_stage2, int32_t accumulate,
-                      void* stream);
+                      int32_t group_size, void* stream);
 
 /* Blockscale MoE (fp8, per-block scales, ScaleBlockM = 1, N = K = 128): each 128-deep K block's
  * partial product is scaled before it is accumulated,

@@ -19,7 +19,14 @@ grouped GEMMs, restated in numpy.
                     pins the metadata interpretation (slot/token packing, padding, expert per block).
 
 Activations and weights arrive as quantized bytes (fp8 e4m3fn, int8) with fp32 per-row scales,
-or as bf16/fp16 bit patterns without scales; the products are evaluated in float64.
+or as bf16/fp16 bit patterns without scales; the products are evaluated in float64.  The
+reference's other input kinds map onto these: ``int4`` (W4A8) is int8 activations with int4
+weight values (kind "int8", values in [-7, 7]); ``int4_bf16`` (W4A16) is bf16 activations
+(``kind="bf16"``) with int4 weight values (``w_kind="int8"``), scaled per row or, with
+``w_groups`` [E, K/g, rows], per (K group, row): ``w[e,n,k] * w_groups[e, k // g, n]``
+(``tests/kernels/test_ref.py:44-50,117-123``); ``int8smooth`` gives stage 1 its activations
+per route, ``x_q`` [tokens, topk, K] with ``sx`` [tokens, topk] (the reference oracle's 3-D
+``x_fp8``, ``:26-34``).
 
 * ``gemm1_blockscale`` / ``gemm2_blockscale``  ``torch_stage1_blockscale_ref`` /
                     ``torch_stage2_blockscale_ref`` (``tests/kernels/test_moe_blockscale.py:64-133``):
@@ -75,9 +82,22 @@ def silu(x: np.ndarray) -> np.ndarray:
     return x / (1.0 + np.exp(-x))
 
 
-def _expert_w(wq, sw, kind, rows: int, e: int) -> np.ndarray:
-    """Dequantized float64 weight rows [e*rows, (e+1)*rows) (one expert, on demand)."""
+def _expert_w(wq, sw, kind, rows: int, e: int, w_groups=None, w_round=None) -> np.ndarray:
+    """Dequantized float64 weight rows [e*rows, (e+1)*rows) (one expert, on demand); with
+    ``w_groups`` [E, K/g, rows] each (row, K group) has its own scale instead of ``sw``;
+    ``w_round="bf16"`` rounds those dequantized weights to bf16 (nearest even), the operand a
+    bf16 matrix instruction can take."""
     lo, hi = e * rows, (e + 1) * rows
+    if w_groups is not None:
+        # the reference multiplies in float32 (an fp32 weight tensor scaled in place)
+        v = np.asarray(wq)[lo:hi].view(np.int8).astype(np.float32)
+        gs = np.asarray(w_groups, dtype=np.float32)[e]            # [K/g, rows]
+        g = v.shape[1] // gs.shape[0]
+        wd = (v * np.repeat(gs.T, g, axis=1)).astype(np.float32)
+        if w_round == "bf16":
+            from .numerics import bf16_rne, bf16_to_f32
+            wd = bf16_to_f32(bf16_rne(wd))
+        return wd.astype(np.float64)
     return dequant_rows(np.asarray(wq)[lo:hi], None if sw is None else np.asarray(sw).reshape(-1)[lo:hi], kind,
                         np.float64)
 
@@ -88,21 +108,32 @@ def _selected(T, tokens_subset):
     return sel
 
 
+def _act(x_q, sx, kind):
+    """Dequantized float64 activations: [tokens, K], or [tokens, topk, K] given per route."""
+    q = np.asarray(x_q)
+    flat = q.reshape(-1, q.shape[-1])
+    x = dequant_rows(flat, None if sx is None else np.asarray(sx).reshape(-1), kind, np.float64)
+    return x.reshape(q.shape)
+
+
 def gemm1(x_q, w1_q, sx, sw1, topk_ids, topk_weights, inter_dim: int, doweight: bool, kind: str,
-          tokens_subset=None) -> np.ndarray:
+          tokens_subset=None, w_kind=None, w_groups=None, w_round=None) -> np.ndarray:
     """[tokens, topk, inter_dim] float64 (rows of tokens outside ``tokens_subset`` are 0).
-    x_q [tokens, K]; w1_q [E*2I, K] unshuffled; sx [tokens]; sw1 [E*2I]."""
+    x_q [tokens, K] (or [tokens, topk, K] per route, sx then [tokens, topk]); w1_q [E*2I, K]
+    unshuffled; sx [tokens]; sw1 [E*2I]; ``w_kind`` the weights' kind when it differs from the
+    activations'; ``w_groups`` [E, K/g, 2I] group scales in place of sw1."""
     ids = np.asarray(topk_ids).astype(np.int64)
     T, topk = ids.shape
     E = np.asarray(w1_q).shape[0] // (2 * inter_dim)
-    x = dequant_rows(x_q, None if sx is None else np.asarray(sx).reshape(-1), kind, np.float64)
+    x = _act(x_q, sx, kind)
     out = np.zeros((T, topk, inter_dim))
     sel = _selected(T, tokens_subset)
     for e in range(E):
         t_idx, s_idx = np.nonzero((ids == e) & sel[:, None])
         if len(t_idx) == 0:
             continue
-        y = x[t_idx] @ _expert_w(w1_q, sw1, kind, 2 * inter_dim, e).T
+        x_in = x[t_idx, s_idx] if x.ndim == 3 else x[t_idx]
+        y = x_in @ _expert_w(w1_q, sw1, w_kind or kind, 2 * inter_dim, e, w_groups, w_round).T
         v = silu(y[:, :inter_dim]) * y[:, inter_dim:]
         if doweight:
             v = v * np.asarray(topk_weights, np.float64)[t_idx, s_idx][:, None]
@@ -111,9 +142,9 @@ def gemm1(x_q, w1_q, sx, sw1, topk_ids, topk_weights, inter_dim: int, doweight: 
 
 
 def gemm2(a2_q, w2_q, sa2, sw2, topk_ids, topk_weights, model_dim: int, doweight: bool, kind: str,
-          tokens_subset=None) -> np.ndarray:
+          tokens_subset=None, w_kind=None, w_groups=None, w_round=None) -> np.ndarray:
     """[tokens, model_dim] float64.  a2_q [tokens*topk, K] (row t*topk + s); w2_q [E*D, K]
-    unshuffled; sa2 [tokens*topk]; sw2 [E*D]."""
+    unshuffled; sa2 [tokens*topk]; sw2 [E*D]; ``w_kind`` / ``w_groups`` [E, K/g, D] as in gemm1."""
     ids = np.asarray(topk_ids).astype(np.int64)
     T, topk = ids.shape
     E = np.asarray(w2_q).shape[0] // model_dim
@@ -127,7 +158,7 @@ def gemm2(a2_q, w2_q, sa2, sw2, topk_ids, topk_weights, model_dim: int, doweight
         t_idx, s_idx = np.nonzero((ids == e) & sel[:, None])
         if len(t_idx) == 0:
             continue
-        y = a2[t_idx * topk + s_idx] @ _expert_w(w2_q, sw2, kind, model_dim, e).T
+        y = a2[t_idx * topk + s_idx] @ _expert_w(w2_q, sw2, w_kind or kind, model_dim, e, w_groups, w_round).T
         if doweight:
             y = y * np.asarray(topk_weights, np.float64)[t_idx, s_idx][:, None]
         np.add.at(out, t_idx, y)

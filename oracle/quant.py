@@ -14,7 +14,7 @@ fp8 uses the e4m3fn round-to-nearest-even cast, as the reference does.
 ``:193-198``), then ``fptosi(x * (1/scale))`` -- a float32 reciprocal, a float32 product,
 truncation toward zero (``:208-238``).
 
-Pins (``tests/test_oracle.py``): invariants ``|q| <= qmax``, ``|q*scale - x| <=
+Pins (``tests/test_oracle.py``): smooth-quant and given-scale known answers; invariants ``|q| <= qmax``, ``|q*scale - x| <=
 scale/2`` (int) or half an fp8 ulp (fp8), all-zero rows get scale 1, the row amax
 maps to exactly +-qmax; agreement with the product's torch quantizer; the block
 quantizer reduces to the row quantizer when the block covers the whole row.
@@ -45,15 +45,24 @@ def _cast(y: np.ndarray, kind: str, rounding: str = "nearest") -> np.ndarray:
     return np.clip(np.rint(y), -qmax, qmax).astype(np.int8)
 
 
-def quant_rows(x: np.ndarray, kind: str, rounding: str = "nearest"):
+def quant_rows(x: np.ndarray, kind: str, rounding: str = "nearest", x_scale=None, scale=None):
     """Per-row quantization: returns (q, scale[rows]) with q uint8 codes (fp8) or int8.
     ``rounding`` ("nearest" or "truncate") applies to the integer kinds; fp8 always rounds
-    to nearest even."""
+    to nearest even.  ``x_scale`` (smooth quant) multiplies the rows first, in float32
+    (``tests/utils.py:41-44``); ``scale`` replaces the computed per-row scales (non-finite ones
+    become 1, ``:66-68``)."""
     qmax = QMAX[kind]
-    x32 = np.nan_to_num(np.asarray(x, dtype=np.float32), nan=0.0, posinf=qmax, neginf=-qmax)
-    scale = _row_scale(x32, qmax)
-    q = _cast((x32 / scale).astype(np.float32), kind, rounding)
-    return q, scale.reshape(-1)
+    x32 = np.asarray(x, dtype=np.float32)
+    if x_scale is not None:
+        x32 = (x32 * np.asarray(x_scale, dtype=np.float32)).astype(np.float32)
+    x32 = np.nan_to_num(x32, nan=0.0, posinf=qmax, neginf=-qmax)
+    if scale is None:
+        sc = _row_scale(x32, qmax)
+    else:
+        sc = np.array(scale, dtype=np.float32).reshape(-1, 1)
+        sc[~np.isfinite(sc)] = np.float32(1.0)
+    q = _cast((x32 / sc).astype(np.float32), kind, rounding)
+    return q, sc.reshape(-1)
 
 
 def quant_rows_recip(x: np.ndarray):

@@ -46,7 +46,8 @@ def run_stage1(p, dev, out_dtype="f16", doweight=False, tile_n=None):
     w = p["workload"]
     fn = compile_moe_gemm1(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
                            tile_m=w.tile_m, tile_n=tile_n or w.tile_n1, tile_k=_tile_k(w.kind),
-                           doweight_stage1=doweight, in_dtype=w.kind, out_dtype=out_dtype)
+                           doweight_stage1=doweight, in_dtype=w.kind, out_dtype=out_dtype,
+                           group_size=p.get("group_size", -1))
     out = torch.full((w.tokens, w.topk, w.inter_dim), float("nan"), dtype=OUT_T[out_dtype], device=dev)
     empty = torch.empty(0, dtype=torch.float32, device=dev)
     fn(out, H.dev_flat(p["x"], dev), H.dev_flat(p["w1_shuf"], dev),
@@ -60,7 +61,8 @@ def run_stage2(p, dev, out_dtype="f16", doweight=True, tile_n=None, out=None, a2
     w = p["workload"]
     fn = compile_moe_gemm2(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
                            tile_m=w.tile_m, tile_n=tile_n or w.tile_n2, tile_k=_tile_k(w.kind),
-                           doweight_stage2=doweight, in_dtype=w.kind, out_dtype=out_dtype)
+                           doweight_stage2=doweight, in_dtype=w.kind, out_dtype=out_dtype,
+                           group_size=p.get("group_size", -1))
     if out is None:
         out = torch.zeros((w.tokens, w.model_dim), dtype=OUT_T[out_dtype], device=dev)
     a2 = p["a2"] if a2 is None else a2
@@ -72,18 +74,60 @@ def run_stage2(p, dev, out_dtype="f16", doweight=True, tile_n=None, out=None, a2
     return out
 
 
-def ref_stage1(p, doweight, subset=None):
-    w = p["workload"]
-    return omoe.gemm1(_host(p["x"]), _host(p["w1"]), _np(p["sx"]), _np(p["sw1"]), _np(p["topk_ids"]),
-                      _np(p["topk_weights"]), w.inter_dim, doweight, w.kind, tokens_subset=subset)
+# the oracle's view of each input kind: (activation kind, weight kind); int4 weights are int8
+# values in [-7, 7], int8smooth activations are given per route
+_ORACLE_KIND = {"int8smooth": ("int8", "int8"), "int4": ("int8", "int8"), "int4_bf16": ("bf16", "int8")}
 
 
-def ref_stage2(p, doweight, subset=None, a2=None, sa2=None):
+def _kinds(w):
+    return _ORACLE_KIND.get(w.kind, (w.kind, w.kind))
+
+
+def ref_stage1(p, doweight, subset=None, w_round=None):
     w = p["workload"]
+    ak, wk = _kinds(w)
+    x, sx = (p["x_route"], p["sx_route"]) if w.kind == "int8smooth" else (p["x"], p["sx"])
+    groups = p.get("w1_groups")
+    return omoe.gemm1(_host(x), _host(p["w1"]), _np(sx), None if groups is not None else _np(p["sw1"]),
+                      _np(p["topk_ids"]), _np(p["topk_weights"]), w.inter_dim, doweight, ak, tokens_subset=subset,
+                      w_kind=wk, w_groups=_np(groups), w_round=w_round)
+
+
+def ref_stage2(p, doweight, subset=None, a2=None, sa2=None, w_round=None):
+    w = p["workload"]
+    ak, wk = _kinds(w)
     a2 = p["a2"] if a2 is None else a2
     sa2 = p["sa2"] if sa2 is None else sa2
-    return omoe.gemm2(_host(a2), _host(p["w2"]), _np(sa2), _np(p["sw2"]), _np(p["topk_ids"]),
-                      _np(p["topk_weights"]), w.model_dim, doweight, w.kind, tokens_subset=subset)
+    groups = p.get("w2_groups")
+    return omoe.gemm2(_host(a2), _host(p["w2"]), _np(sa2), None if groups is not None else _np(p["sw2"]),
+                      _np(p["topk_ids"]), _np(p["topk_weights"]), w.model_dim, doweight, ak, tokens_subset=subset,
+                      w_kind=wk, w_groups=_np(groups), w_round=w_round)
+
+
+# W4A16 with group scales: the bf16 matrix instruction takes the dequantized weights rounded to
+# bf16 (the reference kernel truncates them, mfma_preshuffle_pipeline.py:111-141; here they round
+# to nearest even), so those cases are judged twice: at the standard bar against the oracle with
+# that rounding, and against the exact fp32 dequantization at GROUP_EXACT_ATOL of the RMS (each
+# weight moves by up to 2^-9 of itself, and stage 1's silu(gate) * up doubles the error of its
+# largest outputs).  The reference's own check of these cases is rtol = atol = 0.5
+# (tests/kernels/test_moe_gemm.py:587-589).
+GROUP_EXACT_ATOL = 4e-2
+
+
+def check_stage1(p, out, doweight, subset=None, rows=None, what=""):
+    if p.get("w1_groups") is not None:
+        _check(out, ref_stage1(p, doweight, subset, w_round="bf16"), rows, what=what + " (bf16 weights)")
+        return _check(out, ref_stage1(p, doweight, subset), rows, what=what + " (exact)", atol_rms=GROUP_EXACT_ATOL)
+    return _check(out, ref_stage1(p, doweight, subset), rows, what=what)
+
+
+def check_stage2(p, out, doweight, subset=None, rows=None, what="", atol_rms=1e-2):
+    if p.get("w2_groups") is not None:
+        _check(out, ref_stage2(p, doweight, subset, w_round="bf16"), rows, what=what + " (bf16 weights)",
+               atol_rms=atol_rms)
+        return _check(out, ref_stage2(p, doweight, subset), rows, what=what + " (exact)",
+                      atol_rms=max(atol_rms, GROUP_EXACT_ATOL))
+    return _check(out, ref_stage2(p, doweight, subset), rows, what=what, atol_rms=atol_rms)
 
 
 # bf16 outputs accumulated with atomics: every one of the top-k additions rounds the running sum
@@ -102,11 +146,11 @@ def _check(out, ref, rows=None, what="", atol_rms=1e-2):
     return worst
 
 
-def _problem(name_or_w, kind, dev, seed=None):
+def _problem(name_or_w, kind, dev, seed=None, group_size=-1):
     w = W.MOE_WORKLOADS[name_or_w] if isinstance(name_or_w, str) else name_or_w
     w = W.MoeWorkload(w.name, w.tokens, w.model_dim, w.inter_dim, w.experts, w.topk, w.tile_m, w.tile_n1, w.tile_n2,
                       kind, w.seed if seed is None else seed)
-    return W.moe_problem(w, dev)
+    return W.moe_problem(w, dev, group_size=group_size)
 
 
 def test_sorting_on_device_matches_oracle(gpu):
@@ -197,7 +241,7 @@ def test_two_stage_chain(gpu):
     w = p["workload"]
     _say("chain MM fp8")
     o1 = run_stage1(p, gpu, "f16", doweight=False)
-    a2, sa2 = pertoken_quant(o1.float().view(w.tokens * w.topk, w.inter_dim), FP8)
+    a2, sa2 = pertoken_quant(o1.float().view(w.tokens * w.topk, w.inter_dim), quant_dtype=FP8)
     sa2 = sa2.view(-1).contiguous()
     o2 = run_stage2(p, gpu, "f16", doweight=True, a2=a2, sa2=sa2)
     torch.cuda.synchronize()
@@ -246,9 +290,13 @@ def test_blocks_past_num_valid_and_empty_routing(gpu):
 def test_launcher_checks(gpu):
     p = _problem("MS", "fp8", gpu)
     w = p["workload"]
-    with pytest.raises(NotImplementedError):
+    # group scales are built for int4_bf16 with 32-element groups only
+    with pytest.raises(ValueError, match="group"):
         compile_moe_gemm1(model_dim=256, inter_dim=128, experts=4, topk=2, tile_m=16, tile_n=64, tile_k=128,
-                          doweight_stage1=False, in_dtype="int4")
+                          doweight_stage1=False, in_dtype="int8", group_size=32)
+    with pytest.raises(ValueError, match="group"):
+        compile_moe_gemm2(model_dim=256, inter_dim=128, experts=4, topk=2, tile_m=16, tile_n=64, tile_k=128,
+                          doweight_stage2=False, in_dtype="int4_bf16", group_size=64)
     fn = compile_moe_gemm1(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
                            tile_m=w.tile_m, tile_n=w.tile_n1, tile_k=128, doweight_stage1=False)
     out = torch.empty(w.tokens, w.topk, w.inter_dim, dtype=torch.float16, device=gpu)
@@ -420,3 +468,120 @@ def test_blockscale_tiles_outputs_modes(gpu, tile_m, tile_n, out_dtype, mode):
     _check(o1, ref_bs1(p, True), what="blockscale stage1")
     _check(o2, ref_bs2(p, False), what="blockscale stage2",
            atol_rms=BF16_ATOMIC_ATOL if (out_dtype == "bf16" and mode == "atomic") else 1e-2)
+
+
+# ---- the reference's other input kinds: int8smooth, int4 (W4A8), int4_bf16 (W4A16) -----------
+NEW_KINDS = [("int8smooth", -1), ("int4", -1), ("int4_bf16", -1), ("int4_bf16", 32)]
+NEW_IDS = ["int8smooth", "int4", "int4_bf16", "int4_bf16-g32"]
+
+
+@pytest.mark.parametrize("kind,group", NEW_KINDS, ids=NEW_IDS)
+@pytest.mark.parametrize("shape", ["MS", "MM"])
+@pytest.mark.parametrize("doweight", [False, True])
+def test_new_kinds_stage1(gpu, kind, group, shape, doweight):
+    """The reference harness's S and M shapes (test_moe_gemm.py:1173-1192) for the kinds of
+    test_moe_gemm.py:414-450, stage 1 with and without routing weights."""
+    _say(f"stage1 {shape} {kind} g={group} doweight={doweight}")
+    p = _problem(shape, kind, gpu, seed=11, group_size=group)
+    out = run_stage1(p, gpu, "f16", doweight)
+    torch.cuda.synchronize()
+    check_stage1(p, out, doweight, what=f"stage1 {shape} {kind} g={group}")
+
+
+@pytest.mark.parametrize("kind,group", NEW_KINDS, ids=NEW_IDS)
+@pytest.mark.parametrize("shape", ["MS", "MM"])
+@pytest.mark.parametrize("mode,out_dtype", [("atomic", "f16"), ("atomic", "f32"), ("reduce", "f16"),
+                                            ("reduce", "bf16")])
+def test_new_kinds_stage2(gpu, kind, group, shape, mode, out_dtype):
+    """Stage 2 in atomic and reduce modes (test_moe_gemm.py:1187)."""
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+
+    p = _problem(shape, kind, gpu, seed=12, group_size=group)
+    w = p["workload"]
+    _say(f"stage2 {shape} {kind} g={group} {mode} {out_dtype}")
+    if mode == "atomic":
+        out = run_stage2(p, gpu, out_dtype, doweight=True)
+    else:
+        fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                                  tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=128, doweight_stage2=True,
+                                  in_dtype=kind, group_size=group, out_dtype=out_dtype, mode=MoeGemm2Mode.REDUCE)
+        out = torch.full((w.tokens, w.model_dim), float("nan"), dtype=OUT_T[out_dtype], device=gpu)
+        empty = torch.empty(0, dtype=torch.float32, device=gpu)
+        fn(out, H.dev_flat(p["a2"], gpu), H.dev_flat(p["w2_shuf"], gpu), empty if p["sa2"] is None else p["sa2"],
+           p["sw2"], p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"], p["num_valid_ids"], w.tokens,
+           w.model_dim, w.inter_dim, p["blocks"])
+    torch.cuda.synchronize()
+    check_stage2(p, out, True, what=f"stage2 {shape} {kind} g={group} {mode} {out_dtype}")
+
+
+@pytest.mark.parametrize("kind,group", NEW_KINDS, ids=NEW_IDS)
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+@pytest.mark.parametrize("tile_n", [64, 128, 256])
+def test_new_kinds_every_tile(gpu, kind, group, tile_m, tile_n):
+    """Every single-block tile (a 64-column tile of W4A16 weights is 2 KB per K step: two DMA
+    instructions for four waves)."""
+    w = W.moe_custom(100, 512, 256, 6, 3, tile_m, tile_n, tile_n, kind, seed=tile_m + tile_n)
+    p = W.moe_problem(w, gpu, group_size=group)
+    _say(f"tile {kind} g={group} {tile_m}x{tile_n}")
+    o1 = run_stage1(p, gpu, "bf16", doweight=True)
+    o2 = run_stage2(p, gpu, "f32", doweight=False)
+    torch.cuda.synchronize()
+    check_stage1(p, o1, True, what=f"stage1 {kind} tile {tile_m}x{tile_n}")
+    check_stage2(p, o2, False, what=f"stage2 {kind} tile {tile_m}x{tile_n}")
+
+
+@pytest.mark.parametrize("kind", ["int4", "int8smooth"])
+@pytest.mark.parametrize("tile_m", [16, 64])
+def test_new_kinds_runs_of_blocks(gpu, kind, tile_m):
+    """Experts with many routing blocks take the 8-wave run tiles (W4A16 keeps single blocks)."""
+    w = W.moe_custom(600, 512, 256, 5, 2, tile_m, 128, 256, kind, seed=tile_m * 3)
+    p = W.moe_problem(w, gpu)
+    rows = np.unique(np.r_[np.arange(0, 600, 7), 599])
+    _say(f"runs {kind} tile_m {tile_m}")
+    o1 = run_stage1(p, gpu, "f16", doweight=True)
+    o2 = run_stage2(p, gpu, "bf16", doweight=False)
+    torch.cuda.synchronize()
+    _check(o1, ref_stage1(p, True, rows), rows, what=f"runs stage1 {kind}")
+    _check(o2, ref_stage2(p, False, rows), rows, what=f"runs stage2 {kind}", atol_rms=BF16_ATOMIC_ATOL)
+
+
+@pytest.mark.parametrize("kind,group", NEW_KINDS, ids=NEW_IDS)
+def test_new_kinds_graph_capture(gpu, kind, group):
+    """Both stages captured with torch.cuda.graph on torch's capture stream after eager runs
+    (the reference harness's graph path, tests/test_common.py:79-89); every replay, with eager
+    work in between, equals the eager result."""
+    p = _problem("MM", kind, gpu, seed=13, group_size=group)
+    w = p["workload"]
+    _say(f"graph {kind} g={group}")
+    o1 = run_stage1(p, gpu, "f16", doweight=False)
+    o2 = run_stage2(p, gpu, "f32", doweight=True)
+    torch.cuda.synchronize()
+    e1, e2 = o1.clone(), o2.clone()
+    check_stage1(p, e1, False, what=f"graph eager stage1 {kind}")
+    check_stage2(p, e2, True, what=f"graph eager stage2 {kind}")
+    f1 = compile_moe_gemm1(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                           tile_m=w.tile_m, tile_n=w.tile_n1, tile_k=128, doweight_stage1=False, in_dtype=kind,
+                           out_dtype="f16", group_size=group)
+    f2 = compile_moe_gemm2(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                           tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=128, doweight_stage2=True, in_dtype=kind,
+                           out_dtype="f32", group_size=group)
+    x, w1, a2, w2 = (H.dev_flat(p[k], gpu) for k in ("x", "w1_shuf", "a2", "w2_shuf"))
+    empty = torch.empty(0, dtype=torch.float32, device=gpu)
+    sx = empty if p["sx"] is None else p["sx"]
+    sa2 = empty if p["sa2"] is None else p["sa2"]
+    meta = (p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"], p["num_valid_ids"])
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream()
+        o1.zero_()
+        o2.zero_()
+        f1(o1, x, w1, sx, p["sw1"], *meta, w.tokens, w.inter_dim, w.model_dim, p["blocks"], s)
+        f2(o2, a2, w2, sa2, p["sw2"], *meta, w.tokens, w.model_dim, w.inter_dim, p["blocks"], s)
+    for i in range(3):
+        o1.fill_(7)
+        run_stage1(p, gpu, "f16", doweight=False)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o1, e1), f"replay {i} stage1"
+        check_stage2(p, o2, True, what=f"graph replay {i} stage2 {kind}")

@@ -227,11 +227,11 @@ def test_moe_abi_rejects_bad_arguments_before_launch():
 
     def s1(**kw):
         a = dict(tokens=64, inter=128, model=256, blocks=12, experts=4, topk=2, tile_m=16, tile_n=64, in_dtype=0,
-                 out_dtype=1, doweight=0)
+                 out_dtype=1, doweight=0, group=-1, sw=p)
         a.update(kw)
-        return lib.flygemm_moe_gemm1(p, p, p, p, p, p, p, p, p, a["tokens"], a["inter"], a["model"], a["blocks"],
+        return lib.flygemm_moe_gemm1(p, p, p, p, a["sw"], p, p, p, p, a["tokens"], a["inter"], a["model"], a["blocks"],
                                      a["experts"], a["topk"], a["tile_m"], a["tile_n"], a["in_dtype"], a["out_dtype"],
-                                     a["doweight"], None)
+                                     a["doweight"], a["group"], None)
 
     def err():
         return lib.flygemm_last_error()
@@ -241,20 +241,26 @@ def test_moe_abi_rejects_bad_arguments_before_launch():
     assert s1(inter=192, tile_n=128) != 0 and b"multiple of tile_n" in err()
     assert s1(model=200) != 0 and b"128-byte K tile" in err()
     assert s1(in_dtype=3, model=96) != 0 and b"multiple of 64" in err()
-    assert s1(in_dtype=2) != 0 and b"in_dtype" in err()
+    assert s1(in_dtype=9) != 0 and b"in_dtype" in err()
+    # group scales: int4_bf16 (W4A16) with 32-element groups only; W4A16 needs its weight scales
+    assert s1(group=32) != 0 and b"group" in err()
+    assert s1(in_dtype=6, group=64) != 0 and b"group" in err()
+    assert s1(in_dtype=6, sw=None) != 0 and b"null scale" in err()
+    assert s1(in_dtype=6, model=96) != 0 and b"multiple of 64" in err()
     assert s1(out_dtype=2) != 0 and b"out_dtype" in err()       # stage 1 has no fp32 output
     assert s1(topk=0) != 0 and b"topk" in err()
     assert s1(tokens=1 << 24) != 0 and b"2^24" in err()
     assert s1(tokens=0) == 0 and s1(blocks=0) == 0                # nothing to do
-    rc = lib.flygemm_moe_gemm2(p, p, p, None, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 1, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, None, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 1, -1, None)
     assert rc != 0 and b"null scale" in err()
-    rc = lib.flygemm_moe_gemm2(p, p, p, None, None, p, p, None, p, 64, 256, 128, 12, 4, 2, 16, 64, 3, 2, 1, 1, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, None, None, p, p, None, p, 64, 256, 128, 12, 4, 2, 16, 64, 3, 2, 1, 1, -1,
+                               None)
     assert rc != 0 and b"sorted_weights" in err()
     # reduce mode (accumulate == 0) writes fp16/bf16 rows only
-    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 0, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 0, -1, None)
     assert rc != 0 and b"without accumulation" in err()
     # a per-expert weight slab above 2^31 bytes is refused
-    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 8, 65536, 65536, 12, 4, 2, 16, 256, 0, 2, 0, 1, None)
+    rc = lib.flygemm_moe_gemm2(p, p, p, p, p, p, p, p, p, 8, 65536, 65536, 12, 4, 2, 16, 256, 0, 2, 0, 1, -1, None)
     assert rc != 0 and b"2^31" in err()
     # the reduction
     assert lib.flygemm_moe_reduce(p, p, None, 4, 2, 100, 1, None) != 0 and b"multiple of 8" in err()
@@ -273,9 +279,11 @@ def test_moe_launchers_validate_like_reference():
         compile_moe_gemm1(**kw, doweight_stage1=False, out_dtype="f32")
     with pytest.raises(ValueError):
         compile_moe_gemm1(**{**kw, "tile_k": 32}, doweight_stage1=False)       # 32 bytes per K tile
-    with pytest.raises(NotImplementedError):
-        compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype="int4_bf16")
-    with pytest.raises(NotImplementedError):
+    # every reference in_dtype compiles; group scales only for int4_bf16 with 32-element groups
+    for dt in ("fp8", "fp16", "bf16", "int8", "int8smooth", "int4", "int4_bf16"):
+        assert compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype=dt).in_dtype == dt
+    assert compile_moe_gemm2(**kw, doweight_stage2=True, in_dtype="int4_bf16", group_size=32).group_size == 32
+    with pytest.raises(ValueError, match="group"):
         compile_moe_gemm1(**kw, doweight_stage1=False, in_dtype="bf16", group_size=32)
     with pytest.raises(ValueError):
         compile_moe_gemm2(**kw, doweight_stage2=True, out_dtype="f32", accumulate=False)

@@ -774,3 +774,111 @@ def test_moe_blockscale_stage2_one_expert_and_uniform_scales():
     got_u = omoe.gemm2_blockscale(a2q, w2q, a2s_u, w2s_u, ids, w, D, True)
     row_u = omoe.gemm2(a2q, w2q, a2s_u[:, 0], np.repeat(w2s_u[:, 0], 128), ids, w, D, True, "fp8")
     assert np.allclose(got_u, row_u, rtol=1e-5, atol=1e-6)   # dequant_rows rounds to float32
+
+
+# ---- quantizer arguments of the reference's pertoken_quant (smooth quant, given scales) ------
+def test_quant_rows_smooth_and_given_scale_known_answers():
+    """tests/utils.py:29-73: x_scale multiplies the rows before the scale is taken; a given
+    scale replaces amax/qmax; non-finite given scales become 1."""
+    x = np.array([[1.0, -2.0, 4.0], [0.5, 0.25, -1.0]], np.float32)
+    q, s = oq.quant_rows(x, "int8", x_scale=np.array([4.0, 2.0, 1.0], np.float32))
+    assert q[0].tolist() == [127, -127, 127]                 # row 0 becomes [4, -4, 4]
+    assert np.float32(s[0]) == np.float32(4.0) / np.float32(127.0)
+    # row 1 becomes [2, 0.5, -1]: scale 2/127, codes 127, 31.75 -> 32, -63.5 -> -64 (half to even)
+    assert q[1].tolist() == [127, 32, -64]
+    q1, s1 = oq.quant_rows(x, "int8", x_scale=np.ones(3, np.float32))
+    q0, s0 = oq.quant_rows(x, "int8")
+    assert np.array_equal(q1, q0) and np.array_equal(s1, s0)
+    # the computed scale given back reproduces the codes; a doubled scale halves them (rounded)
+    qg, sg = oq.quant_rows(x, "int8", scale=s0)
+    assert np.array_equal(qg, q0) and np.array_equal(sg, s0)
+    qd, _ = oq.quant_rows(x, "int8", scale=2 * s0)
+    assert np.array_equal(qd, np.rint((x / (2 * s0)[:, None]).astype(np.float32)).astype(np.int8))
+    qn, sn = oq.quant_rows(x, "int8", scale=np.array([np.nan, np.inf], np.float32))
+    assert sn.tolist() == [1.0, 1.0] and qn[0].tolist() == [1, -2, 4]
+
+
+@pytest.mark.parametrize("qd,kind", [(torch.int8, "int8"), (torch.float8_e4m3fn, "fp8")])
+def test_pertoken_quant_smooth_and_given_scale_match_oracle(qd, kind):
+    """The product's pertoken_quant with the reference's x_scale / scale / scale_dtype arguments
+    against the oracle's restatement, byte for byte."""
+    from flydsl_amd import quant as pq
+
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(33, 200, generator=g) * 3
+    xs = 0.5 + torch.rand(1, 200, generator=g)
+    q, s = pq.pertoken_quant(x, x_scale=xs, quant_dtype=qd)
+    oq_q, oq_s = oq.quant_rows(x.numpy(), kind, x_scale=xs.numpy())
+    assert np.array_equal(q.view(torch.uint8).numpy() if kind == "fp8" else q.numpy(), oq_q)
+    assert np.array_equal(s.numpy().reshape(-1), oq_s)
+    given = torch.rand(33, 1, generator=g) * 0.05 + 0.01
+    q2, s2 = pq.pertoken_quant(x, scale=given, quant_dtype=qd)
+    o2_q, o2_s = oq.quant_rows(x.numpy(), kind, scale=given.numpy())
+    assert np.array_equal(q2.view(torch.uint8).numpy() if kind == "fp8" else q2.numpy(), o2_q)
+    assert torch.equal(s2, given)
+    _, s3 = pq.pertoken_quant(x, quant_dtype=qd, scale_dtype=torch.bfloat16)
+    assert s3.dtype == torch.bfloat16
+
+
+# ---- MoE oracle: per-route activations, mixed kinds, group-wise weight scales --------------
+def test_moe_per_route_activations_reduce_to_per_token():
+    """int8smooth gives stage 1 one activation row per route; when every slot of a token holds
+    the token's row and scale, the per-route form is the per-token one."""
+    T, D, I, E, k = 6, 64, 32, 4, 2
+    ids, w, xq, sx, w1q, sw1 = _moe_case(21, T, D, I, E, k, "int8")
+    x3 = np.repeat(xq[:, None, :], k, axis=1)
+    sx3 = np.repeat(sx[:, None], k, axis=1)
+    a = omoe.gemm1(xq, w1q, sx, sw1, ids, w, I, True, "int8")
+    b = omoe.gemm1(x3, w1q, sx3, sw1, ids, w, I, True, "int8")
+    assert np.allclose(a, b, rtol=1e-12, atol=1e-12)
+    # a route's own row is used: doubling one route's scale doubles only its gate and up
+    sx4 = sx3.copy()
+    sx4[2, 1] *= 2
+    c = omoe.gemm1(x3, w1q, sx4, sw1, ids, w, I, False, "int8")
+    ref = omoe.gemm1(x3, w1q, sx3, sw1, ids, w, I, False, "int8")
+    diff = np.abs(c - ref).sum(axis=-1)
+    assert diff[2, 1] > 0 and np.count_nonzero(diff) == 1
+
+
+def test_moe_group_scales_brute_force_and_per_row_reduction():
+    """W4A16 group scales: w[e,n,k] * G[e, k // 32, n] (tests/kernels/test_ref.py:44-50,117-123),
+    checked by an explicit loop over (token, slot, n, k) on a tiny case, and reducing to the
+    per-row form when every group of a row has that row's scale.  Activations are bf16 and the
+    weights int4 values (w_kind int8)."""
+    from oracle import numerics as on
+
+    g = np.random.default_rng(4)
+    T, I, D, E, k, grp = 3, 64, 16, 2, 2, 32
+    ids = np.stack([g.permutation(E)[:k] for _ in range(T)])
+    tw = g.random((T, k)).astype(np.float32)
+    a2 = on.bf16_rne(g.standard_normal((T * k, I)).astype(np.float32))
+    w2 = g.integers(-7, 8, size=(E * D, I)).astype(np.int8)
+    G = (g.random((E, I // grp, D)) * 0.05 + 0.005).astype(np.float32)
+    got = omoe.gemm2(a2, w2, None, None, ids, tw, D, True, "bf16", w_kind="int8", w_groups=G)
+    af = on.bf16_to_f32(a2).astype(np.float64)
+    want = np.zeros((T, D))
+    for t in range(T):
+        for s in range(k):
+            e = ids[t, s]
+            for n in range(D):
+                acc = 0.0
+                for kk in range(I):
+                    wv = float(np.float32(np.float32(w2[e * D + n, kk]) * G[e, kk // grp, n]))   # fp32 dequant
+                    acc += af[t * k + s, kk] * wv
+                want[t, n] += acc * float(tw[t, s])
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+    # constant over the groups of a row: the per-row scale path
+    sw = (g.random(E * D) * 0.05 + 0.005).astype(np.float32)
+    Gc = np.repeat(sw.reshape(E, 1, D), I // grp, axis=1)
+    a = omoe.gemm2(a2, w2, None, None, ids, tw, D, True, "bf16", w_kind="int8", w_groups=Gc)
+    b = omoe.gemm2(a2, w2, None, sw, ids, tw, D, True, "bf16", w_kind="int8")
+    assert np.allclose(a, b, rtol=1e-12, atol=1e-12)
+    # stage 1 the same way (gate and up rows of one expert; K = model_dim = 64)
+    D1 = 64
+    x = on.bf16_rne(g.standard_normal((T, D1)).astype(np.float32))
+    w1 = g.integers(-7, 8, size=(E * 2 * I, D1)).astype(np.int8)
+    sw1 = (g.random(E * 2 * I) * 0.05 + 0.005).astype(np.float32)
+    G1 = np.repeat(sw1.reshape(E, 1, 2 * I), D1 // grp, axis=1)
+    c = omoe.gemm1(x, w1, None, None, ids, tw, I, False, "bf16", w_kind="int8", w_groups=G1)
+    d = omoe.gemm1(x, w1, None, sw1, ids, tw, I, False, "bf16", w_kind="int8")
+    assert np.allclose(c, d, rtol=1e-12, atol=1e-12)
