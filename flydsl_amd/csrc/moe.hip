@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/flygemm.h"
 #include "abi_error.h"
 #include "moe.h"
@@ -181,6 +183,42 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   return 0;
 }
 
+// Per-route rows of flygemm_moe_gemm2_reduce_noalloc: a device array of the library's own, so
+// that entry point allocates nothing.  Each GPU holds one copy at its own address until the
+// process ends, shared by every call on that GPU (calls that overlap on one GPU race).  In host
+// code the name is a stand-in, not a device address: kernels and fills get the address
+// hipGetSymbolAddress returns for the current device.
+constexpr long kNoAllocScratchBytes = FLYGEMM_MOE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, resolved once per device.
+int noalloc_scratch(void** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(e, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(hipErrorInvalidDevice, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "%s: hipGetSymbolAddress of the scratch failed: %s",
+                  what, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+// Zero fill in place of hipMemsetAsync, so the call can be captured in a graph.
+__global__ void __launch_bounds__(256) zero_fill_kernel(uint4* p, long n) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = uint4{0, 0, 0, 0};
+}
+
 }  // namespace
 
 extern "C" {
@@ -260,6 +298,44 @@ int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t t
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of moe_reduce failed: %s", hipGetErrorString(e));
   return 0;
+}
+
+int flygemm_moe_gemm2_reduce_noalloc(void* out, const void* a2, const void* w, const float* scale_a2,
+                                     const float* scale_w, const int32_t* sorted_token_ids,
+                                     const int32_t* sorted_expert_ids, const float* sorted_weights,
+                                     const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim,
+                                     int32_t inter_dim, int32_t size_expert_ids, int32_t experts, int32_t topk,
+                                     int32_t tile_m, int32_t tile_n, int32_t in_dtype, int32_t out_dtype,
+                                     int32_t doweight_stage2, int32_t group_size, const void* valid_mask,
+                                     int32_t zero_intermediate, void* stream) {
+  const char* what = "moe_gemm2_reduce_noalloc";
+  if (out_dtype != FLYGEMM_OUT_FP16 && out_dtype != FLYGEMM_OUT_BF16)
+    return fail(hipErrorInvalidValue, "%s: out_dtype %d not supported (fp16 or bf16)", what, out_dtype);
+  if (tokens < 0 || topk < 1 || model_dim <= 0)
+    return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d topk=%d model_dim=%d", what, tokens, topk,
+                model_dim);
+  if (model_dim % 8 != 0)
+    return fail(hipErrorInvalidValue, "%s: model_dim=%d must be a multiple of 8", what, model_dim);
+  const long need = (long)tokens * topk * model_dim * 2;
+  if (need > kNoAllocScratchBytes)
+    return fail(hipErrorInvalidValue, "%s: tokens*topk*model_dim*2 = %ld bytes exceeds the static scratch of %ld bytes",
+                what, need, kNoAllocScratchBytes);
+  if (tokens == 0) return 0;
+  void* inter = nullptr;
+  if (int rc = noalloc_scratch(&inter, what)) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  if (zero_intermediate && !valid_mask) {
+    const long n = need / 16;
+    const long g = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)g), dim3(256), 0, s, (uint4*)inter, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(e, "%s: launch of the zero fill failed: %s", what, hipGetErrorString(e));
+  }
+  if (int rc = moe_launch(2, inter, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
+                          num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
+                          in_dtype, out_dtype, doweight_stage2, 0, false, group_size, s))
+    return rc;
+  return flygemm_moe_reduce(out, inter, valid_mask, tokens, topk, model_dim, out_dtype, stream);
 }
 
 }  // extern "C"

@@ -190,6 +190,27 @@ int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const
 int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t tokens, int32_t topk,
                        int32_t model_dim, int32_t dtype, void* stream);
 
+/* Stage 2 in reduce mode in one call that allocates nothing: flygemm_moe_gemm2 with
+ * accumulate = 0 into per-route rows [tokens*topk][model_dim] (fp16 or bf16), zeroed first when
+ * zero_intermediate != 0 and valid_mask is NULL, then flygemm_moe_reduce of those rows into out
+ * [tokens][model_dim]; the arguments mean what they mean there, and out equals what those two
+ * calls give.  No counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc), where the
+ * reference's reduce mode takes its rows from torch's allocator.  The rows live in a static
+ * device array of FLYGEMM_MOE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends);
+ * larger tokens*topk*model_dim*2 is rejected.  Every call on one GPU shares that array: calls
+ * that overlap on one GPU (other streams, other threads) race.  The first call on each device
+ * resolves the array's address and must not run under graph capture. */
+#define FLYGEMM_MOE_NOALLOC_SCRATCH_BYTES (64L << 20)
+int flygemm_moe_gemm2_reduce_noalloc(void* out, const void* a2, const void* w, const float* scale_a2,
+                                     const float* scale_w, const int32_t* sorted_token_ids,
+                                     const int32_t* sorted_expert_ids, const float* sorted_weights,
+                                     const int32_t* num_valid_ids, int32_t tokens, int32_t model_dim,
+                                     int32_t inter_dim, int32_t size_expert_ids, int32_t experts, int32_t topk,
+                                     int32_t tile_m, int32_t tile_n, int32_t in_dtype, int32_t out_dtype,
+                                     int32_t doweight_stage2, int32_t group_size, const void* valid_mask,
+                                     int32_t zero_intermediate, void* stream);
+
 /* Kernel variant table (replaces the reference's per-call tile kwargs,
  * kernels/preshuffle_gemm.py:39-53, with a static table). */
 int32_t flygemm_num_variants(void);
