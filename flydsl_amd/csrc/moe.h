@@ -98,8 +98,6 @@ __device__ __forceinline__ float silu_f(float x) {
 
 // F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
 // bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
-// F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
-// bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
 template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, int NS_ = 2>
 struct MoeCfg {
   static constexpr int NS = NS_;                      // LDS ring slots: the DMA runs NS-1 steps ahead

@@ -88,31 +88,27 @@ class PreshuffleGemm:
                                     _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
         _lib.check(rc, "flygemm_preshuffle")
 
-
-def _fp4_call(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):
-    """MXFP4: packed e2m1 A [M, K/2] and preshuffled B [N, K/2] bytes, shuffled E8M0 scales
-    [round_up(M, 32), K/32] and [N, K/32] bytes (``flydsl_amd.fp4``; reference harness
-    ``tests/kernels/test_preshuffle_gemm.py:315-358``)."""
-    M, N, K = int(M), int(N), self.K
-    h_stream = stream_handle(stream)
-    if M < 0 or N <= 0:
-        raise ValueError(f"invalid M={M}, N={N}")
-    if N % 32:
-        raise ValueError(f"N={N} must be a multiple of 32 for MXFP4 (scale groups)")
-    if K % 256:
-        raise ValueError(f"K={K} must be a multiple of 256 for MXFP4")
-    if K % self.tile_k:
-        raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
-    c = device_ptr(arg_c, "arg_c", M * N, dtypes=(_OUT_TORCH[self.out_dtype],))
-    a = device_ptr(arg_a, "arg_a", M * K // 2, elem_bytes=1)
-    b = device_ptr(arg_b, "arg_b", N * K // 2, elem_bytes=1)
-    sa = device_ptr(arg_scale_a, "arg_scale_a", (M + 31) // 32 * 32 * (K // 32), elem_bytes=1)
-    sb = device_ptr(arg_scale_b, "arg_scale_b", N * (K // 32), elem_bytes=1)
-    rc = _lib.load().flygemm_mxfp4(c, a, b, sa, sb, M, N, K, _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
-    _lib.check(rc, "flygemm_mxfp4")
-
-
-PreshuffleGemm._call_fp4 = _fp4_call
+    def _call_fp4(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):
+        """MXFP4: packed e2m1 A [M, K/2] and preshuffled B [N, K/2] bytes, shuffled E8M0 scales
+        [round_up(M, 32), K/32] and [N, K/32] bytes (``flydsl_amd.fp4``; reference harness
+        ``tests/kernels/test_preshuffle_gemm.py:315-358``)."""
+        M, N, K = int(M), int(N), self.K
+        h_stream = stream_handle(stream)
+        if M < 0 or N <= 0:
+            raise ValueError(f"invalid M={M}, N={N}")
+        if N % 32:
+            raise ValueError(f"N={N} must be a multiple of 32 for MXFP4 (scale groups)")
+        if K % 256:
+            raise ValueError(f"K={K} must be a multiple of 256 for MXFP4")
+        if K % self.tile_k:
+            raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
+        c = device_ptr(arg_c, "arg_c", M * N, dtypes=(_OUT_TORCH[self.out_dtype],))
+        a = device_ptr(arg_a, "arg_a", M * K // 2, elem_bytes=1)
+        b = device_ptr(arg_b, "arg_b", N * K // 2, elem_bytes=1)
+        sa = device_ptr(arg_scale_a, "arg_scale_a", (M + 31) // 32 * 32 * (K // 32), elem_bytes=1)
+        sb = device_ptr(arg_scale_b, "arg_scale_b", N * (K // 32), elem_bytes=1)
+        rc = _lib.load().flygemm_mxfp4(c, a, b, sa, sb, M, N, K, _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
+        _lib.check(rc, "flygemm_mxfp4")
 
 
 def compile_preshuffle_gemm_a8(
