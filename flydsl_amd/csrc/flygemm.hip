@@ -186,24 +186,39 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     return best;
   }
   // main family: the first tile in a measured preference list that gives enough workgroups
-  // to occupy the chip (256 CUs).  Without the blockscale epilogue 256x256 wins from about
-  // 160 tiles (1536x8192x8192: 88 us against 110 for 128x256; 512x28672x8192: 113 against
-  // 166), 128x128 when it gives more than one tile per CU (272+: at 256 tiles the 64x128 tile
-  // is still 3-25% faster, at 280-512 tiles 128x128 is 4-40% faster), and the 4-wave 64x128
-  // tile (two resident per CU) below that.  128x256 was never the fastest in these sweeps.
+  // to occupy the chip (256 CUs) and not too many.  Without the blockscale epilogue 256x256
+  // wins from about 160 tiles (1536x8192x8192: 88 us against 110 for 128x256; 512x28672x8192:
+  // 113 against 166), the three-stage 128x256 tile with 200-256 tiles (1024x7168x7168: fp8
+  // 58.3 us against 62.3 for 128x128, int8 59.1 against 62.4, bf16 107.7 against 118.0, MXFP4
+  // 34.7 against 36.1; 1024x8192x8192 fp8 69.8 against 74.0) except for int4 (two stages
+  // there), 128x128 when it gives more than one tile per CU (272+: at 256 tiles the 64x128
+  // tile is still 3-25% faster, at 280-512 tiles 128x128 is 4-40% faster), and the 4-wave
+  // 64x128 tile (two resident per CU) below that.
   struct Pref {
-    int bm, bn, threads, min_wg;
+    int bm, bn, threads, min_wg, max_wg;
+    bool int4;  // also for int4 weights
   };
-  static const Pref kRowcol[] = {{256, 256, 512, 160}, {128, 128, 256, 272}, {64, 128, 256, 0}};
+  static const Pref kRowcol[] = {{256, 256, 512, 160, 1 << 30, true},
+                                 {128, 256, 512, 200, 256, false},
+                                 {128, 128, 256, 272, 1 << 30, true},
+                                 {64, 128, 256, 0, 1 << 30, true}};
   // blockscale (measured on M = 128-4096 with N x K = 7168x7168, 2112x7168, 3072x1536,
-  // 24576x1536): 256x256 from 200 tiles (4096x24576x1536: 196 us against 231 for 256x128),
-  // 256x128 from 160, 128x128 from 240
-  static const Pref kBlock[] = {{256, 256, 512, 200}, {256, 128, 512, 160}, {128, 128, 256, 240}, {64, 128, 256, 0}};
+  // 24576x1536): 256x256 from 160 tiles (4096x24576x1536: 196 us against 231 for 256x128;
+  // 1536x7168x7168, 168 tiles: 107 against 110 for 128x128 and 121 for 128x256), then with
+  // 160-256 tiles the three-stage 128x256 when N is a multiple of 256 (1024x7168x7168: 66.2 us
+  // against 70.2 for 256x128; 2048x3072x1536: 19.4 against 20.4), else 256x128, 128x128 from 240
+  static const Pref kBlock[] = {{256, 256, 512, 160, 1 << 30, true},
+                                {128, 256, 512, 160, 256, true},
+                                {256, 128, 512, 160, 1 << 30, true},
+                                {128, 128, 256, 240, 1 << 30, true},
+                                {64, 128, 256, 0, 1 << 30, true}};
   const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
-  const int n = epi == EPI_BLOCK ? 4 : 3;
+  const int n = epi == EPI_BLOCK ? 5 : 4;
   for (int i = 0; i < n; ++i) {
+    if (kind == KIND_INT4 && !list[i].int4) continue;
+    if (epi == EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && N % 256 != 0) continue;
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
-    if (wg < list[i].min_wg) continue;
+    if (wg < list[i].min_wg || wg > list[i].max_wg) continue;
     // the last resort (64x128) leaves CUs idle when there are at most 128 tiles: the
     // row-blocked streaming kernel spreads the output over every CU instead
     if (list[i].min_wg == 0 && wg <= kRowsMaxTiles) return select_rows(kind, epi);

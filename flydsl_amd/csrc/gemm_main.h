@@ -53,11 +53,15 @@ struct MainCfg {
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB DMA instructions per wave per tile
   static constexpr int B_DMA = B_BYTES / 1024 / NW;
-  // LDS stages: three for the 4-wave tiles of at most 64x128 outputs (short steps), else two.
-  // Measured on MI355X: the third stage saves 4-18% on fp8/int8 shapes from 128x4096x4096 to
-  // 1024x7168x7168, but costs 12% on W4A8 256x14336x4096, whose half-size B steps are not
-  // waiting on their DMA.
-  static constexpr int NS = (NW == 4 && BM * BN <= 64 * 128 && KIND != KIND_INT4) ? 3 : 2;
+  // LDS stages: three for the 4-wave tiles of at most 64x128 outputs (short steps) and for the
+  // 8-wave 128x256 / 256x128 tiles (3 x 48 KB plus scales fits the 160 KB), else two.
+  // Measured on MI355X: the third stage saves 4-18% on the 4-wave tiles for fp8/int8 shapes
+  // from 128x4096x4096 to 1024x7168x7168 and 10-25% on the 8-wave ones for fp8, int8, bf16,
+  // MXFP4 and blockscale (1024x7168x7168 fp8 with 128x256 tiles: 58.3 us against 70.9), but
+  // costs 12-15% on int4 (W4A8 256x14336x4096 with 64x128 tiles, 1024x14336x4096 with
+  // 256x128), whose half-size B steps are not waiting on their DMA.
+  static constexpr int NS =
+      (KIND != KIND_INT4 && ((NW == 4 && BM * BN <= 64 * 128) || (NW == 8 && BM * BN == 256 * 128))) ? 3 : 2;
   static constexpr int DMA_PER_STEP = A_DMA + B_DMA;  // per wave, scale DMAs not counted
   static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile must be a multiple of 16");
   static_assert(A_BYTES % (1024 * NW) == 0 && B_BYTES % (1024 * NW) == 0, "tile not divisible into wave DMAs");
@@ -237,8 +241,9 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
             dma16(rsrc_sb, sc + SA_BYTES + qb * 1024, ((uint32_t)c1 * (uint32_t)nk * 64u) * 4u + (b & 255u),
                   (uint32_t)kt * 256u);
           } else {
-            // lane l: w_scale[n0/128 + l][kt]
-            const int nb = min(n0 / 128 + lane, (N - 1) / 128);
+            // lane l < BN/128: w_scale[n0/128 + l][kt]; the other lanes repeat lane 0's
+            // address (one cache line for the wave instead of 64 scattered ones)
+            const int nb = min(n0 / 128 + (lane < (BN + 127) / 128 ? lane : 0), (N - 1) / 128);
             dma4(rsrc_sb, sc + SA_BYTES, ((uint32_t)nb * (uint32_t)nk + (uint32_t)kt) * 4u, 0);
           }
         }
@@ -260,10 +265,31 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
   };
 
+  // Blockscale: the 128-deep MFMA of row mi goes into a zeroed partial, which is added to the
+  // accumulator scaled by sa * sb one row later, after the next row's MFMAs have been issued,
+  // so the FMAs never wait on the MFMA that produced their operand.  Two partial sets
+  // alternate between rows (MR is even).  The last row's partial waits for the next K tile:
+  // it is added after that tile's first MFMAs (with the factors pend_s kept from its own
+  // tile), or before the epilogue, so the end of a step never waits on its last MFMAs.
+  static_assert(EPI != EPI_BLOCK || MR % 2 == 0, "blockscale alternates two partial sets over an even MR");
+  f32x4 part[2][NR];
+  float pend_s[NR];
+  auto flush_pending = [&]() {
+#pragma unroll
+    for (int ni = 0; ni < NR; ++ni) {
+      const f32x4 pv = part[(MR - 1) & 1][ni];
+      acc[MR - 1][ni].x = __builtin_fmaf(pv.x, pend_s[ni], acc[MR - 1][ni].x);
+      acc[MR - 1][ni].y = __builtin_fmaf(pv.y, pend_s[ni], acc[MR - 1][ni].y);
+      acc[MR - 1][ni].z = __builtin_fmaf(pv.z, pend_s[ni], acc[MR - 1][ni].z);
+      acc[MR - 1][ni].w = __builtin_fmaf(pv.w, pend_s[ni], acc[MR - 1][ni].w);
+    }
+  };
+
   // One K tile.  The A fragment of row mi+1 is requested before the MFMAs of row mi are
   // issued, so its LDS latency hides behind NR MFMAs.  B is the MFMA's first operand, so
-  // each accumulator tile holds C transposed (see the epilogue).
-  auto compute = [&](const uint8_t* sA) {
+  // each accumulator tile holds C transposed (see the epilogue).  `pending`: the previous K
+  // tile of this output tile left its last blockscale row to add.
+  auto compute = [&](const uint8_t* sA, bool pending) {
     const uint8_t* sB = sA + C::A_BYTES;
     const uint8_t* sS = sA + C::STAGE;  // this K tile's scales
     // blockscale: this lane's row scale per row block, the column-block scale per tile column;
@@ -294,11 +320,6 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         const i32x4 hi = *(const i32x4*)(sB + off + 1024);
         bf[ni] = i32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
-    // blockscale: the 128-deep MFMA of row mi goes into a zeroed partial, and the partial is
-    // added to the accumulator scaled by sa * sb one row later, after the next row's MFMAs
-    // have been issued, so the FMAs never wait on the MFMA that produced their operand.  Two
-    // partial sets alternate between rows.
-    f32x4 part[2][NR];
     auto scale_row = [&](int mi) {
 #pragma unroll
       for (int ni = 0; ni < NR; ++ni) {
@@ -317,8 +338,14 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         if constexpr (EPI == EPI_BLOCK) {
 #pragma unroll
           for (int ni = 0; ni < NR; ++ni) part[mi & 1][ni] = mfma_fp8(bf[ni], af, f32x4{0.f, 0.f, 0.f, 0.f});
-          if (mi > 0) scale_row(mi - 1);
-          if (mi + 1 == MR) scale_row(mi);
+          if (mi > 0)
+            scale_row(mi - 1);
+          else if (pending)
+            flush_pending();
+          if (mi + 1 == MR) {
+#pragma unroll
+            for (int ni = 0; ni < NR; ++ni) pend_s[ni] = sa_t[mi] * sb_t[ni];
+          }
         } else {
 #if FLY_SCHED
           // the next row's A reads stay ahead of this row's MFMAs
@@ -468,9 +495,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
           wait_dma();
         workgroup_barrier();  // step's stage is published; every wave is done with step-1's
         if (iw < nitems) issue_next(slot == 0 ? 2 : slot - 1);  // the stage step-1 used
-        compute(ring(slot));
+        compute(ring(slot), kt != kb);
         slot = slot == 2 ? 0 : slot + 1;
       }
+      if constexpr (EPI == EPI_BLOCK) flush_pending();
       epilogue(m0, n0);
     }
     return;
@@ -507,8 +535,9 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         issue(nxt, m0, n0, kt + 1);
       else if (wnext < nitems)
         issue(nxt, nm0, nn0, nkb);
-      compute(cur);
+      compute(cur, kt != kb);
     }
+    if constexpr (EPI == EPI_BLOCK) flush_pending();
     epilogue(m0, n0);
     m0 = nm0;
     n0 = nn0;

@@ -39,7 +39,7 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
     # every shape gets a variant, and the five configurations get the tiles measured fastest
     expect = {(128, 4096, 4096, 0, 0): "rows_m2_nb4_w8_u3", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
-              (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_256x128_w2x4",
+              (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_128x256_w2x4",
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
@@ -56,13 +56,17 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(16, 7168, 7168, 0, 1)].startswith("decode_m1")
     # blockscale: 256x256 from 200 tiles, 256x128 from 160
     assert names[lib.flygemm_select_variant(2048, 7168, 7168, 0, 1)] == "main_256x256_w2x4"
-    assert names[lib.flygemm_select_variant(2048, 3072, 1536, 0, 1)] == "main_256x128_w2x4"
+    assert names[lib.flygemm_select_variant(2048, 3072, 1536, 0, 1)] == "main_128x256_w2x4"
+    assert names[lib.flygemm_select_variant(1024, 2112, 7168, 0, 1)] == "main_64x128_w1x4"  # N % 256 != 0
+    assert names[lib.flygemm_select_variant(1536, 7168, 7168, 0, 1)] == "main_256x256_w2x4"  # 168 tiles
     # 256x256 from about 160 tiles, then 128x128 from 272
     assert names[lib.flygemm_select_variant(1536, 8192, 8192, 0, 0)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(512, 28672, 8192, 0, 0)] == "main_256x256_w2x4"
-    assert names[lib.flygemm_select_variant(1024, 8192, 8192, 0, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 8192, 8192, 0, 0)] == "main_128x256_w2x4"
     # 128x128 once it gives more than one tile per CU
-    assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x256_w2x4"
+    assert names[lib.flygemm_select_variant(1024, 7168, 7168, 2, 0)] == "main_128x128_w2x2"  # int4: no 128x256
+    assert names[lib.flygemm_select_variant(1280, 7168, 7168, 0, 0)] == "main_128x128_w2x2"  # 280 tiles of 128x256
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
     # the row-blocked kernel where the 64x128 tiles leave CUs idle (at most 96 tiles), with
     # 16-row blocks for blockscale and MXFP4
