@@ -261,7 +261,7 @@ int persistent_grid(KernelFn fn, int threads, long ntiles, int* grid) {
 int check_common(const void* c, const void* a, const void* b, int M, int N, int K, int variant) {
   if (M < 0 || N <= 0 || K <= 0) return fail(hipErrorInvalidValue, "invalid sizes M=%d N=%d K=%d", M, N, K);
   if (N % 16 != 0) return fail(hipErrorInvalidValue, "N=%d must be a multiple of 16 (preshuffle block)", N);
-  if (K % 128 != 0) return fail(hipErrorInvalidValue, "K=%d must be a multiple of 128 (K tile)", K);
+  if (K % 64 != 0) return fail(hipErrorInvalidValue, "K=%d bytes must be a multiple of 64 (half K tile)", K);
   if ((long)(M + 256) * K >= (1L << 31) || (long)N * K >= (1L << 31) || (long)M * N * 4 >= (1L << 31))
     return fail(hipErrorInvalidValue, "operand too large for 32-bit element offsets (M=%d N=%d K=%d)", M, N, K);
   if (M > 0 && (!c || !a || !b)) return fail(hipErrorInvalidValue, "null tensor pointer");
@@ -319,15 +319,21 @@ QuantFn quant_fn_in(int out_dtype, int mode, int nslices) {
   return nullptr;
 }
 
-// K in bytes for the kernels: 16-bit inputs have two bytes per element and need K % 64 == 0
-// (one 128-byte K tile); returns -1 after setting the error for a bad K.
+// K in bytes for the kernels, which take K tiles of 128 bytes and a last tile of 64 bytes
+// (the reference's tile_k * elem_bytes % 64 == 0, kernels/preshuffle_gemm.py:89-93): 16-bit
+// inputs have two bytes per element and need K % 32 == 0; returns -1 after setting the error
+// for a bad K.
 int k_bytes(int in_dtype, int K) {
   if (in_dtype == FLYGEMM_IN_BF16 || in_dtype == FLYGEMM_IN_FP16) {
-    if (K <= 0 || K % 64 != 0) {
-      fail(hipErrorInvalidValue, "K=%d must be a multiple of 64 for 16-bit inputs (128-byte K tile)", K);
+    if (K <= 0 || K % 32 != 0) {
+      fail(hipErrorInvalidValue, "K=%d must be a multiple of 32 for 16-bit inputs (64-byte K tile)", K);
       return -1;
     }
     return 2 * K;
+  }
+  if (K <= 0 || K % 64 != 0) {
+    fail(hipErrorInvalidValue, "K=%d must be a multiple of 64 (64-byte K tile)", K);
+    return -1;
   }
   return K;
 }
@@ -357,9 +363,11 @@ int flygemm_preshuffle(void* c, const void* a, const void* b, const float* scale
 int flygemm_blockscale(void* c, const void* a, const void* b, const float* x_scale_t, const float* w_scale,
                        int32_t M, int32_t N, int32_t K, int32_t scale_block_k, int32_t out_dtype,
                        int32_t variant, void* stream) {
+  if (scale_block_k != 128) return fail(hipErrorInvalidValue, "scale_block_k=%d: only 128 is supported", scale_block_k);
+  if (K <= 0 || K % 128 != 0)
+    return fail(hipErrorInvalidValue, "K=%d must be a multiple of scale_block_k=128", K);
   int rc = check_common(c, a, b, M, N, K, variant);
   if (rc) return rc;
-  if (scale_block_k != 128) return fail(hipErrorInvalidValue, "scale_block_k=%d: only 128 is supported", scale_block_k);
   if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16)
     return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
   if (M > 0 && (!x_scale_t || !w_scale)) return fail(hipErrorInvalidValue, "null scale pointer");

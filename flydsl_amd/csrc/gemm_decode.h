@@ -37,7 +37,10 @@ __device__ __forceinline__ T load_b(const T* p) {
 template <int MR, int NBW, int NW, int UNROLL, int KIND, int EPI, bool OUT_BF16, bool NT_B = true>
 __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   const int M = p.M, N = p.N, K = p.K;
+  // full 128-byte K tiles; K (bytes) is a multiple of 64, and when K % 128 == 64 the last 64
+  // bytes form a half tile, taken after the pipeline (see below)
   const int nk = K / KT;
+  const bool half_k = (K % KT) != 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   // Wave-uniform (SGPR) wave index: every branch that guards an MFMA below depends only
@@ -185,6 +188,33 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     }
   };
 
+  // The half K tile (index nk), taken first by the wave whose K tiles it continues (nk % NW),
+  // before the pipeline's registers are in use: its lower 64 bytes (A chunks 0-3, B chunks 0-3)
+  // are loaded and the upper halves are zeros, so the second 64-deep MFMA (and the upper half
+  // of the 128-deep fp8 one) adds nothing; nothing past K is read.  Blockscale and MXFP4 take
+  // whole K tiles only.
+  if constexpr (EPI != EPI_BLOCK && KIND != KIND_FP4) {
+    if (half_k && wave == nk % NW) {
+      Stage& s = st[0];
+#pragma unroll
+      for (int j = 0; j < NBW; ++j) {
+        const uint8_t* src = bblk[j] + (size_t)nk * B_BLK;
+        if constexpr (KIND == KIND_INT4) {
+          s.b4lo[j] = load_b<NT_B>((const i32x2*)src);
+          s.b4hi[j] = i32x2{0, 0};
+        } else {
+          s.blo[j] = load_b<NT_B>((const i32x4*)src);
+          s.bhi[j] = i32x4{0, 0, 0, 0};
+        }
+      }
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) {
+        s.alo[mi] = *(const i32x4*)(arow[mi] + (size_t)nk * KT);
+        s.ahi[mi] = i32x4{0, 0, 0, 0};
+      }
+      compute(s, nk);
+    }
+  }
 #pragma unroll
   for (int u = 0; u < UNROLL - 1; ++u)
     if (wave + u * NW < nk) load(st[u], wave + u * NW);

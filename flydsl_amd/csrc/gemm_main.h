@@ -168,7 +168,11 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   const int nbm = (M + BM - 1) / BM;
   const int nbn = (N + BN - 1) / BN;
   const int ntiles = nbm * nbn;
-  const int nk = K / KT;
+  // K (bytes) is a multiple of 64: the last K tile holds half a tile when K % 128 == 64
+  // (never for blockscale and MXFP4, whose scale blocks span whole K tiles)
+  constexpr bool kHalfOk = KIND != KIND_FP4 && EPI != EPI_BLOCK;
+  const int nk = (K + KT - 1) / KT;
+  const bool half_k = kHalfOk && (K % KT) != 0;
   const int nblk_max = N / 16 - 1;
 
   const int tid = threadIdx.x;
@@ -185,15 +189,22 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   // chunk depends only on the row inside the tile (tile rows start at multiples of 16).
   // B: one resource over the whole buffer; the 16-column block offset is wave-uniform
   // (SGPR soffset), column blocks past N are clamped to the last one.
-  uint32_t va0[C::A_DMA];
+  // A half K tile (the last one when K % 128 == 64 bytes) loads its upper 64 bytes -- A
+  // chunks 4-7, the upper KB of each B block (int4: its lanes 32-63) -- from an offset past
+  // every buffer, so the range check writes zeros there and those MFMA halves add nothing
+  // (va0h / vbh; 0x80000000 plus any row offset stays past the 2^31-byte operands).
+  constexpr uint32_t kPast = 0x80000000u;
+  uint32_t va0[C::A_DMA], va0h[C::A_DMA];
 #pragma unroll
   for (int j = 0; j < C::A_DMA; ++j) {
     const int rloc = (wave + j * NW) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((rloc >> 1) & 7);
     va0[j] = (uint32_t)rloc * (uint32_t)K + (uint32_t)(c * 16);
+    va0h[j] = (kHalfOk && c >= 4) ? kPast : va0[j];
   }
   constexpr int PARTS = C::B_BLK / 1024;
   const uint32_t vb = (uint32_t)lane * 16u;
+  const uint32_t vbh = (kHalfOk && PARTS == 1 && lane >= 32) ? kPast : vb;
   const int b_bytes = (KIND == KIND_INT4) ? (N / 2) * K : N * K;
   const sgpr4 rsrc_b = buf_desc(p.b, (uint32_t)b_bytes);
 
@@ -207,15 +218,17 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   auto issue = [&](uint8_t* s, int m0, int n0, int kt) {
     const sgpr4 rsrc_a = buf_desc(p.a + (size_t)kt * KT, (uint32_t)(M * K - kt * KT));
     const uint32_t mo = (uint32_t)m0 * (uint32_t)K;
+    const bool half = half_k && kt == nk - 1;
 #pragma unroll
-    for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, va0[j] + mo, 0);
+    for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, (half ? va0h[j] : va0[j]) + mo, 0);
 #pragma unroll
     for (int j = 0; j < C::B_DMA; ++j) {
       const int q = wave + j * NW;
       const int nb = min(n0 / 16 + q / PARTS, nblk_max);
       const uint32_t so = (uint32_t)nb * (uint32_t)(C::B_BLK / KT) * (uint32_t)K + (uint32_t)((q % PARTS) * 1024) +
                           (uint32_t)kt * C::B_BLK;
-      dma16(rsrc_b, s + C::A_BYTES + q * 1024, vb, __builtin_amdgcn_readfirstlane(so));
+      const uint32_t vo = !half ? vb : (PARTS == 1 ? vbh : (q % PARTS == 1 ? kPast : vb));
+      dma16(rsrc_b, s + C::A_BYTES + q * 1024, vo, __builtin_amdgcn_readfirstlane(so));
     }
     // this K tile's scales: scale instruction q = wave, wave + NW, ... (q < SA_DMA: A region,
     // then B region); indices past the arrays are clamped

@@ -22,7 +22,8 @@ Differences from the reference, all on purpose:
   as hints only: the kernel variant comes from the library's MI355X table, keyed on the
   run-time M, N, K.  ``variant=`` forces one (tests, tuning).
 * Any ``N % 16 == 0`` is computed in full (the reference's grid silently skips a tail
-  when ``N % tile_n != 0``); K must be a multiple of 128 (64 for bf16/fp16).
+  when ``N % tile_n != 0``); K must be a multiple of 64 (32 for bf16/fp16): 64-byte K tiles, as the reference's
+  ``tile_k * elem_bytes % 64 == 0``.
 * GPU errors raise ``RuntimeError`` (the reference prints them).
 * ``in_dtype="fp4"`` (MXFP4, what ``compile_preshuffle_gemm_w4`` builds) takes packed e2m1
   bytes and shuffled E8M0 scale bytes (``flydsl_amd.fp4``); N % 32 == 0 and K % 256 == 0.
@@ -69,8 +70,8 @@ class PreshuffleGemm:
         if K % self.tile_k:
             raise ValueError(f"K={K} must be divisible by tile_k={self.tile_k}")
         is16 = self.in_dtype in ("bf16", "fp16")
-        if K % (64 if is16 else 128):
-            raise ValueError(f"K={K} must be a multiple of {64 if is16 else 128} on MI355X")
+        if K % (32 if is16 else 64):
+            raise ValueError(f"K={K} must be a multiple of {32 if is16 else 64} (64-byte K tile)")
         c = device_ptr(arg_c, "arg_c", M * N, dtypes=(_OUT_TORCH[self.out_dtype],))
         if is16:
             t = _IN_TORCH16[self.in_dtype]

@@ -18,7 +18,8 @@
  *    packed two values per byte as in tests/kernels/test_preshuffle_gemm.py:165-174.
  *    bf16/fp16 B uses the same rule on each row's bytes (8 elements per 16-byte chunk), which
  *    is what shuffle_weight produces for 2-byte elements.
- *  - Requirements: N % 16 == 0, K % 128 == 0 (K % 64 == 0 for bf16/fp16), M >= 0 (M == 0 is
+ *  - Requirements: N % 16 == 0, K % 64 == 0 (K % 32 == 0 for bf16/fp16: K tiles of 128 bytes, the
+ *    last one 64 bytes when K * elem_bytes % 128 == 64; blockscale K % 128), M >= 0 (M == 0 is
  *    a no-op), every operand below 2^31 bytes.  Violations return nonzero without launching.
  *  - Return value: 0 on success, otherwise a hipError_t code; flygemm_last_error() gives
  *    the message of the calling thread's last failure.

@@ -29,8 +29,9 @@ def bits16(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-def launch(ops, device, variant=-1, out_dtype="bf16", stream=None):
-    """Run the drop-in launcher for ``ops`` (from ``flydsl_amd.workloads.make_operands``)."""
+def launch(ops, device, variant=-1, out_dtype="bf16", stream=None, tile_k=None):
+    """Run the drop-in launcher for ``ops`` (from ``flydsl_amd.workloads.make_operands``);
+    ``tile_k`` defaults to 128 bytes of K."""
     w = ops["workload"]
     M, N, K = w.M, w.N, w.K
     a = dev_flat(ops["a"], device)
@@ -41,7 +42,7 @@ def launch(ops, device, variant=-1, out_dtype="bf16", stream=None):
                                                 out_dtype=out_dtype, variant=variant)
         fn(c.view(-1), a, b, ops["sa_t"].to(device).view(-1), ops["sb"].to(device).view(-1), M, N, stream)
     else:
-        tk = 64 if w.kind in ("bf16", "fp16") else 128  # 128 bytes of K either way
+        tk = tile_k or (64 if w.kind in ("bf16", "fp16") else 128)  # 128 bytes of K either way
         fn = compile_preshuffle_gemm_a8(K=K, tile_m=64, tile_n=128, tile_k=tk, in_dtype=w.kind,
                                         out_dtype=out_dtype, variant=variant)
         fn(c.view(-1), a, b, ops["sa"].to(device).view(-1), ops["sb"].to(device).view(-1), M, N, stream)

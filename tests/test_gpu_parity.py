@@ -142,6 +142,40 @@ def test_rows_variants(gpu, kind, variant):
             assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "bf16", "fp16"])
+def test_k_half_tile_every_variant(gpu, kind):
+    """K with a last K tile of 64 bytes (K = 64 mod 128 for 1-byte inputs, 32 mod 64 for 16-bit
+    ones: the reference's tile_k * elem_bytes % 64 == 0, e.g. int8 K = 192), through every
+    variant of all three families, on ragged M/N.  int8/int4/bf16/fp16 go through the launcher
+    with the 64-byte tile_k the reference harness would pass; fp8, whose reference launcher
+    wants tile_k % 128 == 0 on gfx950 (kernels/preshuffle_gemm.py:665-673), through the C ABI.
+    The half tile's upper 64 bytes (the next row's or block's bytes, or past the buffer) must
+    not enter the sums: int8/int4 raw accumulators and outputs bit-exact, the others within the
+    bar, and every output finite."""
+    eb = 2 if kind in ("bf16", "fp16") else 1
+    lib = _lib.load()
+    for (M, N, Kb) in [(5, 80, 64), (37, 272, 192), (130, 160, 320), (300, 96, 576)]:
+        K = Kb // eb
+        w = workloads.custom(kind, M, N, K, seed=M + N + K, b_std=0.02 if kind == "int4" else 1.0)
+        ops = workloads.make_operands(w)
+        for variant in range(len(VARIANTS)):
+            _say(f"half K tile {VARIANTS[variant]} {kind} {M}x{N}x{K}")
+            if kind == "fp8":
+                out = torch.empty(M, N, dtype=torch.bfloat16, device=gpu)
+                a, b = H.dev_flat(ops["a"], gpu), H.dev_flat(ops["b_dev"], gpu)
+                sa, sb = ops["sa"].to(gpu).contiguous(), ops["sb"].to(gpu).contiguous()
+                _lib.check(lib.flygemm_preshuffle(out.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(),
+                                                  sb.data_ptr(), M, N, K, _lib.FLYGEMM_IN["fp8"], 0, variant, None),
+                           "flygemm_preshuffle")
+            else:
+                out = H.launch(ops, gpu, variant=variant, tile_k=64 // eb)
+            torch.cuda.synchronize()
+            assert torch.isfinite(out.float()).all(), f"{VARIANTS[variant]} {kind} {M}x{N}x{K}: non-finite output"
+            ref = H.check(ops, out)
+            if kind in ("int8", "int4"):
+                assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("kind,M,N,K", [("fp8", 128, 4096, 4096), ("fp8_block", 33, 2112, 7168),
                                         ("fp8_block", 64, 2112, 7168), ("fp8_block", 256, 2112, 7168),
                                         ("int8", 128, 2048, 4096)])

@@ -98,7 +98,11 @@ def test_abi_rejects_bad_arguments_before_launch():
     rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 100, 256, 0, 0, -1, None)
     assert rc != 0 and b"multiple of 16" in lib.flygemm_last_error()
     rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 200, 0, 0, -1, None)
-    assert rc != 0 and b"multiple of 128" in lib.flygemm_last_error()
+    assert rc != 0 and b"multiple of 64" in lib.flygemm_last_error()
+    # K = 64 (mod 128) is accepted for 1-byte inputs (a last half K tile); blockscale keeps 128
+    assert lib.flygemm_preshuffle(p, p, p, p, p, 0, 128, 192, 1, 0, -1, None) == 0
+    rc = lib.flygemm_blockscale(p, p, p, p, p, 16, 128, 192, 128, 0, -1, None)
+    assert rc != 0 and b"multiple of scale_block_k" in lib.flygemm_last_error()
     rc = lib.flygemm_preshuffle(None, p, p, p, p, 16, 128, 256, 0, 0, -1, None)
     assert rc != 0 and b"null" in lib.flygemm_last_error()
     rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 128, 256, 7, 0, -1, None)
@@ -128,10 +132,10 @@ def test_abi_rejects_bad_arguments_before_launch():
     rc = lib.flygemm_quant_rows(ctypes.c_void_p(17), p, p, 4, 64, 0, 1, 0, None)
     assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
     assert lib.flygemm_quant_rows(p, p, p, 0, 64, 0, 1, 0, None) == 0
-    # 16-bit inputs: K counts elements and must be a multiple of 64; scales are not needed
-    rc = lib.flygemm_preshuffle(p, p, p, None, None, 16, 128, 96, 3, 0, -1, None)
-    assert rc != 0 and b"multiple of 64" in lib.flygemm_last_error()
-    assert lib.flygemm_preshuffle(p, p, p, None, None, 0, 128, 192, 4, 0, -1, None) == 0
+    # 16-bit inputs: K counts elements and must be a multiple of 32; scales are not needed
+    rc = lib.flygemm_preshuffle(p, p, p, None, None, 16, 128, 80, 3, 0, -1, None)
+    assert rc != 0 and b"multiple of 32" in lib.flygemm_last_error()
+    assert lib.flygemm_preshuffle(p, p, p, None, None, 0, 128, 96, 4, 0, -1, None) == 0
     # MXFP4
     rc = lib.flygemm_mxfp4(p, p, p, p, p, 16, 128, 384, 0, -1, None)
     assert rc != 0 and b"multiple of 256" in lib.flygemm_last_error()
