@@ -64,6 +64,61 @@ int pick_tile_n(int N, long runs) {
   return 64;
 }
 
+// Tile of a call: runs of R routing blocks per workgroup and tile_n output columns (the
+// caller's tile_n, already validated, is a hint).
+int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
+              const char* what, int* r_out, int* tn_out) {
+  const long routes = (long)tokens * topk;
+  // Runs of several routing blocks when experts hold two or more blocks on average, on 2 x 4
+  // waves: stage 1 128 rows x 128 output columns (128 gate + 128 up weight rows) with a 3-slot
+  // DMA ring; stage 2 256 rows x 256 columns with 2 slots.  The caller's tile_n is then
+  // overridden: tiling does not change results.  Not for blockscale nor W4A16 (their scales
+  // do not fit next to the run tiles).
+  int R = 1;
+  const int run_tn = stage == 1 ? 128 : 256;
+  if (!bs && kind != KIND_W4A16 && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
+    R = (stage == 1 ? 128 : 256) / tile_m;
+    tile_n = run_tn;
+  }
+  if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
+  // Few runs (decode): narrower column tiles until there are workgroups for every CU (each
+  // workgroup streams its own weight columns, so parallelism is bandwidth here).
+  if (R == 1 && (tile_n == 128 || tile_n == 256)) {
+    const long runs1 = est_runs(tokens, topk, experts, tile_m, 1);
+    while (tile_n > 64 && runs1 * (N / tile_n) < 256 && N % (tile_n / 2) == 0) tile_n /= 2;
+    // decode-sized routings (stage 2 up to 512 routes, stage 1 up to 256): 64-column tiles,
+    // whose short weight streams finish together (DS-V3 dims, top-8: stage 2 at 8 tokens 19.8
+    // µs against 27.2 with 256 columns, at 32 tokens 71.8 against 76.6; stage 1 at 32 tokens
+    // 101 against 115; from 128 tokens on the wider tiles are within +-7%)
+    if (routes <= (stage == 2 ? 512 : 256) && N % 64 == 0) tile_n = 64;
+    // stage 2 with more routes but still single-block tiles: 128 columns (1024-2048 routes:
+    // 0-11% faster than 256 for fp8 and blockscale, never slower), so stage 2 never runs
+    // single-block tiles of 256 columns
+    else if (stage == 2 && tile_n == 256 && N % 128 == 0) tile_n = 128;
+  }
+  if (tile_n != 64 && tile_n != 128 && tile_n != 256)
+    return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
+  if (N % tile_n != 0) return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
+  *r_out = R;
+  *tn_out = tile_n;
+  return 0;
+}
+
+// in_dtype -> kernel kind (and whether stage-1 activations come per route); -1 if unknown
+int moe_kind(int in_dtype, int stage, bool* token_slot) {
+  *token_slot = false;
+  switch (in_dtype) {
+    case FLYGEMM_IN_FP8: return KIND_FP8;
+    case FLYGEMM_IN_INT8: return KIND_INT8;
+    case FLYGEMM_IN_INT8_SMOOTH: *token_slot = stage == 1; return KIND_INT8;
+    case FLYGEMM_IN_INT4: return KIND_INT4;
+    case FLYGEMM_IN_INT4_BF16: return KIND_W4A16;
+    case FLYGEMM_IN_BF16: return KIND_BF16;
+    case FLYGEMM_IN_FP16: return KIND_F16;
+    default: return -1;
+  }
+}
+
 int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
                const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
                const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
@@ -83,51 +138,16 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
   if (tile_n > 0 && N % tile_n != 0)
     return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
-  // Runs of several routing blocks when experts hold two or more blocks on average, on 2 x 4
-  // waves: stage 1 128 rows x 128 output columns (128 gate + 128 up weight rows) with a 3-slot
-  // DMA ring; stage 2 256 rows x 256 columns with 2 slots.  The caller's tile_n is then overridden: tiling does not change results.
-  int kind;
   bool token_slot = false;
-  switch (in_dtype) {
-    case FLYGEMM_IN_FP8: kind = KIND_FP8; break;
-    case FLYGEMM_IN_INT8: kind = KIND_INT8; break;
-    case FLYGEMM_IN_INT8_SMOOTH: kind = KIND_INT8; token_slot = stage == 1; break;
-    case FLYGEMM_IN_INT4: kind = KIND_INT4; break;
-    case FLYGEMM_IN_INT4_BF16: kind = KIND_W4A16; break;
-    case FLYGEMM_IN_BF16: kind = KIND_BF16; break;
-    case FLYGEMM_IN_FP16: kind = KIND_F16; break;
-    default: return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
-  }
+  const int kind = moe_kind(in_dtype, stage, &token_slot);
+  if (kind < 0) return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
   if (bs && kind != KIND_FP8) return fail(hipErrorInvalidValue, "%s: blockscale takes fp8", what);
   // group scales: W4A16 only, 32-element groups along K (reference tests/utils.py:99-120)
   if (group_size > 0 && (kind != KIND_W4A16 || group_size != 32))
     return fail(hipErrorInvalidValue, "%s: group_size=%d: group scales are for int4_bf16 with group_size 32", what,
                 group_size);
-  const long routes = (long)tokens * topk;
   int R = 1;
-  const int run_tn = stage == 1 ? 128 : 256;
-  if (!bs && kind != KIND_W4A16 && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
-    R = (stage == 1 ? 128 : 256) / tile_m;   // stage 1: 128 rows, three LDS slots
-    tile_n = run_tn;
-  }
-  if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
-  // Few runs (decode): narrower column tiles until there are workgroups for every CU (each
-  // workgroup streams its own weight columns, so parallelism is bandwidth here).
-  if (R == 1 && (tile_n == 128 || tile_n == 256)) {
-    const long runs1 = est_runs(tokens, topk, experts, tile_m, 1);
-    while (tile_n > 64 && runs1 * (N / tile_n) < 256 && N % (tile_n / 2) == 0) tile_n /= 2;
-    // decode-sized routings (stage 2 up to 512 routes, stage 1 up to 256): 64-column tiles,
-    // whose short weight streams finish together (DS-V3 dims, top-8: stage 2 at 8 tokens 19.8
-    // µs against 27.2 with 256 columns, at 32 tokens 71.8 against 76.6; stage 1 at 32 tokens
-    // 101 against 115; from 128 tokens on the wider tiles are within +-7%)
-    if (routes <= (stage == 2 ? 512 : 256) && N % 64 == 0) tile_n = 64;
-    // stage 2 with more routes but still single-block tiles: 128 columns (1024-2048 routes:
-    // 0-11% faster than 256 for fp8 and blockscale, never slower)
-    else if (stage == 2 && tile_n == 256 && N % 128 == 0) tile_n = 128;
-  }
-  if (tile_n != 64 && tile_n != 128 && tile_n != 256)
-    return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);
-  if (N % tile_n != 0) return fail(hipErrorInvalidValue, "%s: N=%d must be a multiple of tile_n=%d", what, N, tile_n);
+  if (int rc = moe_tiles(stage, tokens, N, experts, topk, tile_m, tile_n, kind, bs, what, &R, &tile_n)) return rc;
   const bool is16 = moe_a_16bit(kind);      // 2-byte activations (bf16, fp16, W4A16)
   const long kb = is16 ? 2L * K : (long)K;  // activation bytes per row
   if (kb % 128 != 0)
@@ -297,6 +317,29 @@ int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t t
                      tokens, topk, model_dim);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of moe_reduce failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t experts, int32_t topk, int32_t tile_m,
+                            int32_t tile_n, int32_t in_dtype, int32_t blockscale, int32_t* runs, int32_t* tile_n_out) {
+  const char* what = "moe_select_tile";
+  if (stage != 1 && stage != 2) return fail(hipErrorInvalidValue, "%s: stage %d must be 1 or 2", what, stage);
+  if (tokens < 0 || n <= 0 || experts <= 0 || topk < 1 || topk > 255)
+    return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d n=%d experts=%d topk=%d", what, tokens, n, experts,
+                topk);
+  if (tile_m != 16 && tile_m != 32 && tile_m != 64)
+    return fail(hipErrorInvalidValue, "%s: tile_m=%d must be 16, 32 or 64", what, tile_m);
+  if (tile_n > 0 && ((tile_n != 64 && tile_n != 128 && tile_n != 256) || n % tile_n != 0))
+    return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256 and divide n=%d", what, tile_n, n);
+  if (!runs || !tile_n_out) return fail(hipErrorInvalidValue, "%s: null output pointer", what);
+  bool token_slot = false;
+  const int kind = moe_kind(in_dtype, stage, &token_slot);
+  if (kind < 0) return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
+  int r = 1, tn = 0;
+  if (int rc = moe_tiles(stage, tokens, n, experts, topk, tile_m, tile_n, kind, blockscale != 0, what, &r, &tn))
+    return rc;
+  *runs = r;
+  *tile_n_out = tn;
   return 0;
 }
 

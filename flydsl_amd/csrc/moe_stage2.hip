@@ -1,5 +1,5 @@
 // Kernel table of MoE stage 2 (the down projection), in a translation unit of its own so the
-// library's sources compile in parallel.  Tiles as listed with the stage-1 table in moe.hip.
+// library's sources compile in parallel.
 #include <hip/hip_runtime.h>
 
 #include "moe.h"
@@ -11,8 +11,10 @@ template <int KIND, bool F32, bool BS>
 MoeFn stage2_tile(int tm, int r, int tn) {
 #define T(M_, R_, N_, WM_, WN_) \
   if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, WM_, WN_, F32, BS>;
-  T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(16, 1, 256, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4)
-  T(32, 1, 256, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4) T(64, 1, 256, 1, 4)
+  // single-block tiles of 64 and 128 columns: the launcher never gives stage 2 single-block
+  // tiles of 256 columns (it narrows them to 128 or 64)
+  T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4) T(64, 1, 64, 1, 4)
+  T(64, 1, 128, 1, 4)
   // run tiles: not for blockscale (its partials and factors do not fit next to them) nor W4A16
   // (its group scales ride the two-slot pipeline)
   if constexpr (!BS && KIND != KIND_W4A16) {

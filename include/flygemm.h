@@ -183,6 +183,16 @@ int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const
                                  int32_t tile_n, int32_t scale_block_k, int32_t out_dtype, int32_t doweight_stage2,
                                  int32_t accumulate, void* stream);
 
+/* The MoE launchers' tile choice for a call with these sizes (they treat tile_n as a hint):
+ * *runs = routing blocks per workgroup (1: single-block tiles; more: runs of 128 rows in stage
+ * 1, 256 in stage 2) and *tile_n_out = output columns per tile.  n is inter_dim for stage 1 and
+ * model_dim for stage 2; in_dtype as for flygemm_moe_gemm1/2; blockscale != 0 for the
+ * blockscale MoE.  Validates like the launchers; touches no device.  Counterpart of the
+ * reference's compile-time tile arguments (kernels/moe_gemm_2stage.py:93-121), for tests and
+ * tuning, like flygemm_select_variant. */
+int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t experts, int32_t topk, int32_t tile_m,
+                            int32_t tile_n, int32_t in_dtype, int32_t blockscale, int32_t* runs, int32_t* tile_n_out);
+
 /* Reduce mode, second step: y [tokens][model_dim] = sum over k < topk of x [tokens][topk]
  * [model_dim] (only slots with valid_mask[t*topk+k] != 0 when valid_mask, int8 [tokens*topk], is
  * given), fp32 sums; dtype fp16, bf16 or fp32 for both x and y; model_dim a multiple of 8 (4 for

@@ -204,6 +204,9 @@ def test_stage1_bf16_output_and_stage2_unweighted(gpu):
 @pytest.mark.parametrize("tile_m", [16, 32, 64])
 @pytest.mark.parametrize("tile_n", [64, 128, 256])
 def test_every_tile(gpu, tile_m, tile_n):
+    """Every (tile_m, tile_n) a caller may pass.  tile_n is a hint: on this small routing the
+    launcher runs 64-column tiles (the wide single-block tiles are reached by
+    test_single_block_wide_tiles, the run tiles by test_runs_of_blocks)."""
     w = W.moe_custom(100, 512, 256, 6, 3, tile_m, tile_n, tile_n, "fp8", seed=tile_m + tile_n)
     p = W.moe_problem(w, gpu)
     _say(f"tile {tile_m}x{tile_n}")
@@ -585,3 +588,63 @@ def test_new_kinds_graph_capture(gpu, kind, group):
         torch.cuda.synchronize()
         assert torch.equal(o1, e1), f"replay {i} stage1"
         check_stage2(p, o2, True, what=f"graph replay {i} stage2 {kind}")
+
+
+# ---- single-block tiles of 256 (stage 1) and 128 (stage 2) columns -------------------------------
+def _chosen_tile(stage, w, kind, blockscale=0):
+    import ctypes
+    from flydsl_amd import _lib
+    r, tn = ctypes.c_int32(), ctypes.c_int32()
+    n = w.inter_dim if stage == 1 else w.model_dim
+    _lib.check(_lib.load().flygemm_moe_select_tile(stage, w.tokens, n, w.experts, w.topk, w.tile_m,
+                                                   w.tile_n1 if stage == 1 else w.tile_n2, _lib.FLYGEMM_IN[kind],
+                                                   blockscale, ctypes.byref(r), ctypes.byref(tn)),
+               "flygemm_moe_select_tile")
+    return r.value, tn.value
+
+
+WIDE_KINDS = [("fp8", -1), ("int8", -1), ("bf16", -1), ("fp16", -1), ("int4", -1), ("int8smooth", -1),
+              ("int4_bf16", -1), ("int4_bf16", 32)]
+
+
+@pytest.mark.parametrize("kind,group", WIDE_KINDS, ids=[k if g < 0 else f"{k}-g{g}" for k, g in WIDE_KINDS])
+def test_single_block_wide_tiles(gpu, kind, group):
+    """Routings with fewer than two blocks per expert but enough routes that the launcher keeps
+    wide single-block tiles: 160 tokens, top-4 of 64 experts, D = 512, I = 1024, tile_m 32,
+    tile_n 256 -> stage 1 runs the 256-column single-block kernel, stage 2 the 128-column one
+    (checked through flygemm_moe_select_tile first).  Stage 2 in atomic and reduce modes."""
+    w = W.moe_custom(160, 512, 1024, 64, 4, 32, 256, 256, kind, seed=11)
+    assert _chosen_tile(1, w, kind) == (1, 256) and _chosen_tile(2, w, kind) == (1, 128)
+    p = W.moe_problem(w, gpu, group_size=group)
+    p["group_size"] = group
+    _say(f"wide single-block tiles {kind} g={group}")
+    o1 = run_stage1(p, gpu, "bf16", doweight=True)
+    o2 = run_stage2(p, gpu, "f32", doweight=False)
+    torch.cuda.synchronize()
+    check_stage1(p, o1, True, what=f"stage1 {kind} 1x256")
+    check_stage2(p, o2, False, what=f"stage2 {kind} 1x128 atomic")
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+    fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                              tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=128, doweight_stage2=True, in_dtype=kind,
+                              group_size=group, out_dtype="f16", mode=MoeGemm2Mode.REDUCE)
+    o3 = torch.full((w.tokens, w.model_dim), float("nan"), dtype=torch.float16, device=gpu)
+    empty = torch.empty(0, dtype=torch.float32, device=gpu)
+    fn(o3, H.dev_flat(p["a2"], gpu), H.dev_flat(p["w2_shuf"], gpu), empty if p["sa2"] is None else p["sa2"],
+       empty if p["sw2"] is None else p["sw2"], p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"],
+       p["num_valid_ids"], w.tokens, w.model_dim, w.inter_dim, p["blocks"])
+    torch.cuda.synchronize()
+    check_stage2(p, o3, True, what=f"stage2 {kind} 1x128 reduce")
+
+
+def test_single_block_wide_tiles_blockscale(gpu):
+    """The same routing through the blockscale MoE: stage 1 single-block 256-column tiles,
+    stage 2 128-column ones."""
+    w = W.moe_custom(160, 512, 1024, 64, 4, 32, 256, 256, "fp8_block", seed=12)
+    assert _chosen_tile(1, w, "fp8", 1) == (1, 256) and _chosen_tile(2, w, "fp8", 1) == (1, 128)
+    p = W.moe_problem(w, gpu)
+    _say("wide single-block tiles blockscale")
+    o1 = run_bs_stage1(p, gpu, "f16", doweight=False)
+    o2 = run_bs_stage2(p, gpu, "f32", doweight=True)
+    torch.cuda.synchronize()
+    _check(o1, ref_bs1(p, False), what="blockscale stage1 1x256")
+    _check(o2, ref_bs2(p, True), what="blockscale stage2 1x128")

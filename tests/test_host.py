@@ -333,3 +333,38 @@ def test_moe_blockscale_validation():
     rc = lib.flygemm_moe_blockscale_gemm2(p, p, p, p, p, p, p, p, p, 16, 320, 128, 6, 4, 2, 16, 64, 128, 1, 1, 1,
                                           None)
     assert rc != 0 and b"multiple of 128" in lib.flygemm_last_error()
+
+
+def test_moe_tile_choice_pinned():
+    """flygemm_moe_select_tile gives the launchers' tile choice without a device: run tiles for
+    prefill routings, 64 columns for decode-sized ones, wide single-block tiles in between (the
+    reachable kernel set the GPU tests cover), and the launchers' validation."""
+    import ctypes
+    lib = _lib.load()
+
+    def sel(stage, tokens, n, experts, topk, tile_m, tile_n, kind="fp8", bs=0):
+        r, tn = ctypes.c_int32(), ctypes.c_int32()
+        rc = lib.flygemm_moe_select_tile(stage, tokens, n, experts, topk, tile_m, tile_n, _lib.FLYGEMM_IN[kind], bs,
+                                         ctypes.byref(r), ctypes.byref(tn))
+        return (r.value, tn.value) if rc == 0 else rc
+
+    # DS-TP8 prefill: runs of 128 rows (stage 1, 128 columns) / 256 rows (stage 2, 256 columns)
+    assert sel(1, 8192, 256, 128, 8, 64, 256) == (2, 128)
+    assert sel(2, 8192, 7168, 128, 8, 64, 256) == (4, 256)
+    # decode: 64-column single-block tiles whatever the caller asked
+    assert sel(1, 8, 256, 256, 8, 32, 256) == (1, 64)
+    assert sel(2, 8, 7168, 256, 8, 32, 256) == (1, 64)
+    # in between: the wide single-block tiles; stage 2 never keeps 256 single-block columns
+    for kind in ("fp8", "int8", "bf16", "fp16", "int4", "int8smooth", "int4_bf16"):
+        assert sel(1, 160, 1024, 64, 4, 32, 256, kind) == (1, 256), kind
+        assert sel(2, 160, 512, 64, 4, 32, 256, kind) == (1, 128), kind
+    assert sel(1, 160, 1024, 64, 4, 32, 256, "fp8", 1) == (1, 256)
+    assert sel(2, 128, 7168, 256, 8, 32, 0) == (1, 128)
+    # blockscale and W4A16 never take run tiles
+    assert sel(2, 8192, 7168, 128, 8, 64, 256, "fp8", 1)[0] == 1
+    assert sel(2, 8192, 7168, 128, 8, 64, 256, "int4_bf16")[0] == 1
+    # validation
+    assert sel(3, 16, 256, 4, 2, 16, 64) != 0 and b"stage" in lib.flygemm_last_error()
+    assert sel(1, 16, 256, 4, 2, 48, 64) != 0 and b"tile_m" in lib.flygemm_last_error()
+    assert sel(1, 16, 320, 4, 2, 16, 256) != 0 and b"tile_n" in lib.flygemm_last_error()
+    assert sel(1, 16, 256, 4, 2, 16, 64, "fp4") != 0 and b"in_dtype" in lib.flygemm_last_error()
