@@ -25,6 +25,7 @@ SIGNATURES = [
     ("flygemm_blockscale", ctypes.c_int, [_P, _P, _P, _F, _F, _I, _I, _I, _I, _I, _I, _P]),
     ("flygemm_accumulators", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     ("flygemm_quant_rows", ctypes.c_int, [_P, _F, _P, _I, _I, _I, _I, _I, _P]),
+    ("flygemm_preshuffle_quant_a", ctypes.c_int, [_P] * 5 + [_F] + [_I] * 8 + [_P]),
     ("flygemm_mxfp4", ctypes.c_int, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     ("flygemm_moe_gemm1", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 12 + [_P]),
     ("flygemm_moe_gemm2", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 13 + [_P]),

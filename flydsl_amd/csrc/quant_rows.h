@@ -42,33 +42,40 @@ constexpr int kQuantSlice = kQuantThreads * 8;  // elements per workgroup pass
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x2q __attribute__((ext_vector_type(2)));
 
+typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+
+// 8 consecutive 16-bit inputs (one 16-byte vector, element order) as fp32
+template <int IN>
+__device__ __forceinline__ f32x8 cvt8_16(u32x4q w) {
+  static_assert(IN == QIN_F16 || IN == QIN_BF16, "16-bit inputs");
+  f32x8 v;
+  const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t h0 = (uint16_t)(words[i] & 0xFFFFu), h1 = (uint16_t)(words[i] >> 16);
+    if constexpr (IN == QIN_F16) {
+      v[2 * i] = (float)__builtin_bit_cast(_Float16, h0);
+      v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, h1);
+    } else {
+      v[2 * i] = __builtin_bit_cast(float, (uint32_t)h0 << 16);
+      v[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)h1 << 16);
+    }
+  }
+  return v;
+}
+
 // 8 consecutive inputs starting at element `col` of `row_base`, as fp32
 template <int IN>
 __device__ __forceinline__ f32x8 load8(const void* row_base, int col) {
-  f32x8 v;
   if constexpr (IN == QIN_F32) {
     typedef float f32x4_t __attribute__((ext_vector_type(4)));
     const f32x4_t* p = (const f32x4_t*)((const float*)row_base + col);
     const f32x4_t lo = __builtin_nontemporal_load(p);
     const f32x4_t hi = __builtin_nontemporal_load(p + 1);
-    v = f32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    return f32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
   } else {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 w = __builtin_nontemporal_load((const u32x4*)((const uint16_t*)row_base + col));
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t h0 = (uint16_t)(words[i] & 0xFFFFu), h1 = (uint16_t)(words[i] >> 16);
-      if constexpr (IN == QIN_F16) {
-        v[2 * i] = (float)__builtin_bit_cast(_Float16, h0);
-        v[2 * i + 1] = (float)__builtin_bit_cast(_Float16, h1);
-      } else {
-        v[2 * i] = __builtin_bit_cast(float, (uint32_t)h0 << 16);
-        v[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)h1 << 16);
-      }
-    }
+    return cvt8_16<IN>(__builtin_nontemporal_load((const u32x4q*)((const uint16_t*)row_base + col)));
   }
-  return v;
 }
 
 // pertoken_quant's nan_to_num(nan=0, posinf=qmax, neginf=-qmax)
@@ -78,14 +85,19 @@ __device__ __forceinline__ float scrub(float x, float qmax) {
   return x;
 }
 
-template <int IN, int MODE>
-__device__ __forceinline__ f32x8 load8_prepared(const void* row_base, int col, float qmax) {
-  f32x8 v = load8<IN>(row_base, col);
+// the host quantizer's modes scrub NaN / inf before the scale is taken (see scrub)
+template <int MODE>
+__device__ __forceinline__ f32x8 prepare8(f32x8 v, float qmax) {
   if constexpr (MODE != QMODE_RECIP_TRUNC) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = scrub(v[i], qmax);
   }
   return v;
+}
+
+template <int IN, int MODE>
+__device__ __forceinline__ f32x8 load8_prepared(const void* row_base, int col, float qmax) {
+  return prepare8<MODE>(load8<IN>(row_base, col), qmax);
 }
 
 __device__ __forceinline__ float absmax8(const f32x8& v) {

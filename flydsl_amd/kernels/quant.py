@@ -13,7 +13,12 @@ Two interfaces over ``flygemm_quant_rows`` (``include/flygemm.h``):
   even by default (the benchmark workloads' rule) or truncates (``rounding="trunc"``, the
   reference's ``.to(torch.int8)``); fp8 (``torch.float8_e4m3fn``) rounds to nearest even.
 
-Both fail loudly if the HIP library is missing; there is no host fallback.
+* ``quant_gemm(x, b, scale_b, N, in_dtype=...)`` -- the GEMM of activations quantized on the
+  way in (``flygemm_preshuffle_quant_a``): the same result as ``per_token_quant`` followed by
+  the preshuffle GEMM launcher, bit for bit, with one kernel for decode-sized M that quantizes
+  A in registers while it streams B.
+
+All fail loudly if the HIP library is missing; there is no host fallback.
 """
 from __future__ import annotations
 
@@ -93,3 +98,52 @@ def per_token_quant(x: torch.Tensor, quant_dtype=torch.int8, rounding: str = "ne
     s = device_ptr(scale, "scale", M, dtypes=(torch.float32,))
     _launch(o, s, i, M, N, _QIN[x.dtype], out_code, mode, stream)
     return out, scale
+
+
+_GEMM_IN = {"fp8": 0, "int8": 1, "int4": 2}
+_GEMM_OUT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def quant_gemm(x: torch.Tensor, b, scale_b, N: int, *, in_dtype: str = "fp8", out_dtype: str = "bf16",
+               mode: str = "div_nearest", out=None, a_q=None, scale_a=None, fused: bool = False,
+               variant: int = -1, stream=None):
+    """``C[M, N] = GEMM(quant(x), B)`` with ``x`` [M, K] fp16 / bf16 / fp32 quantized per row to
+    fp8 (``in_dtype="fp8"``) or int8 codes (``"int8"``, or ``"int4"`` for packed int4 weights),
+    ``b`` the preshuffled weight bytes and ``scale_b`` [N] fp32, as ``per_token_quant`` (mode
+    ``"div_nearest"`` / ``"div_trunc"``) or the reference's quant kernel (``"recip_trunc"``)
+    followed by ``compile_preshuffle_gemm_a8``'s launcher.  Returns ``(out, a_q, scale_a)``.
+    With ``fused=True`` no code or scale buffers are passed (unless given) and the library runs
+    its one-launch kernel (decode-sized M, fp16/bf16 x, the kind's fused mode: fp8
+    ``"div_nearest"``, int8/int4 ``"recip_trunc"``); otherwise ``a_q`` [M, K] and ``scale_a``
+    [M, 1] are allocated when not given and the quant kernel and the GEMM run as two launches."""
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [M, K], got shape {tuple(x.shape)}")
+    if x.dtype not in _QIN:
+        raise TypeError(f"x dtype {x.dtype} not supported (fp16, bf16, fp32)")
+    if in_dtype not in _GEMM_IN:
+        raise ValueError(f"in_dtype must be one of {sorted(_GEMM_IN)}, got {in_dtype!r}")
+    if out_dtype not in _GEMM_OUT:
+        raise ValueError(f"out_dtype must be 'bf16' or 'fp16', got {out_dtype!r}")
+    if mode not in _lib.QUANT_MODE:
+        raise ValueError(f"mode must be one of {sorted(_lib.QUANT_MODE)}, got {mode!r}")
+    M, K = x.shape
+    N = int(N)
+    qdt = torch.float8_e4m3fn if in_dtype == "fp8" else torch.int8
+    if out is None:
+        out = torch.empty(M, N, dtype=_GEMM_OUT[out_dtype], device=x.device)
+    if a_q is None and not fused:
+        a_q = torch.empty(M, K, dtype=qdt, device=x.device)
+    if scale_a is None and not fused:
+        scale_a = torch.empty(M, 1, dtype=torch.float32, device=x.device)
+    b_elems = N * K // 2 if in_dtype == "int4" else N * K
+    c = device_ptr(out, "out", M * N, dtypes=(_GEMM_OUT[out_dtype],))
+    q = device_ptr(a_q, "a_q", M * K, elem_bytes=1) if a_q is not None else None
+    sa = device_ptr(scale_a, "scale_a", M, dtypes=(torch.float32,)) if scale_a is not None else None
+    xi = device_ptr(x, "x", M * K, dtypes=(x.dtype,))
+    bp = device_ptr(b, "b", b_elems, elem_bytes=1)
+    sb = device_ptr(scale_b, "scale_b", N, dtypes=(torch.float32,))
+    rc = _lib.load().flygemm_preshuffle_quant_a(c, q, sa, xi, bp, sb, int(M), N, int(K), _QIN[x.dtype],
+                                                _GEMM_IN[in_dtype], _lib.QUANT_MODE[mode],
+                                                _lib.FLYGEMM_OUT[out_dtype], int(variant), stream_handle(stream))
+    _lib.check(rc, "flygemm_preshuffle_quant_a")
+    return out, a_q, scale_a

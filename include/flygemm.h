@@ -103,6 +103,24 @@ enum { FLYGEMM_QMODE_RECIP_TRUNC = 0, FLYGEMM_QMODE_DIV_TRUNC = 1, FLYGEMM_QMODE
 int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int32_t N, int32_t in_dtype,
                        int32_t out_dtype, int32_t mode, void* stream);
 
+/* The GEMM of activations quantized per row on the way in: the result equals
+ *   flygemm_quant_rows(a_q, scale_a, x, M, K, x_dtype, fp8 or int8 codes, mode) followed by
+ *   flygemm_preshuffle(c, a_q, b, scale_a, scale_b, M, N, K, in_dtype, out_dtype, variant)
+ * bit for bit (the quant kernel of tests/kernels/test_quant.py:81-265 or pertoken_quant of
+ * tests/utils.py:29-73, then the launcher of kernels/preshuffle_gemm.py:1268-1301).  x: [M][K]
+ * FLYGEMM_QIN_* activations; in_dtype FLYGEMM_IN_FP8 (mode must be _DIV_NEAREST), _INT8 or
+ * _INT4 (int8 codes); mode and scale_b as for those entries.  Fused kernel: for a decode
+ * variant of 16-row blocks, fp16/bf16 x and the kind's fused mode (fp8: _DIV_NEAREST; int8 and
+ * int4: _RECIP_TRUNC, the reference's quant kernel), one launch in which each workgroup derives
+ * its rows' scales and quantizes A in registers as it streams B.  It runs when the caller
+ * forces such a variant or passes a_q / scale_a as NULL; otherwise (the faster path on MI355X
+ * wherever measured) the quant kernel and the GEMM run as two launches through a_q [M][K] and
+ * scale_a [M], which are then required.  a_q / scale_a, when given, receive the codes and
+ * scales either way.  No allocation; asynchronous on `stream`. */
+int flygemm_preshuffle_quant_a(void* c, void* a_q, float* scale_a, const void* x, const void* b, const float* scale_b,
+                               int32_t M, int32_t N, int32_t K, int32_t x_dtype, int32_t in_dtype, int32_t mode,
+                               int32_t out_dtype, int32_t variant, void* stream);
+
 /* MoE 2-stage GEMM over routing metadata sorted by expert (the reference's moe_sorting,
  * tests/kernels/test_moe_gemm.py:97-162):
  *   sorted_token_ids int32 [>= num_valid_ids[0]]: (slot << 24) | token, each expert's run
