@@ -256,16 +256,18 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   // in the preshuffled layout, copied verbatim.
   auto issue = [&](int jt, int kt, int slot) {
     uint8_t* st = ring + slot * C::SLOT;
+    // the guards below are compile-time true when the DMA count divides among the waves (no
+    // branches in the step then)
 #pragma unroll
     for (int j = 0; j < C::AQ; ++j) {
       const int q = wave + j * NW;
-      if (q < C::A_DMA) dma16(rsrc_a, st + q * 1024, va[j], (uint32_t)kt * KT);
+      if (C::A_DMA % NW == 0 || q < C::A_DMA) dma16(rsrc_a, st + q * 1024, va[j], (uint32_t)kt * KT);
     }
     const int n0 = jt * TN;
 #pragma unroll
     for (int j = 0; j < C::BQ; ++j) {
       const int q = wave + j * NW;
-      if (q >= C::B_DMA) continue;           // wave-uniform
+      if (C::B_DMA % NW != 0 && q >= C::B_DMA) continue;           // wave-uniform
       // local 16-column block lb (gate -- or W2 -- for lb < TN/16, up after) -> global block
       auto gblk = [&](int lb) { return lb < TN / 16 ? n0 / 16 + lb : (p.N + n0) / 16 + (lb - TN / 16); };
       uint32_t so, vo = vb;
