@@ -94,14 +94,16 @@ __device__ __forceinline__ f32x4 mfma_fp4(const i32x4& b, const i32x4& a, const 
 }
 
 // 4 packed int4 bytes (8 nibbles, little-endian) -> 8 sign-extended int8 in two dwords:
-// the low nibbles of bytes 0..3 first, then the high nibbles
-// (kernels/mfma_preshuffle_pipeline.py:277-291).
+// the low nibbles of bytes 0..3 first, then the high nibbles (the reference's unpack order,
+// kernels/mfma_preshuffle_pipeline.py:277-291).  Per byte, with the nibble u in the low half:
+// x = u ^ 0x88 is (u ^ 8) + 0x80, in 0x80..0x8F; x - 8 stays in 0x78..0x87, so the 32-bit
+// subtraction borrows across no byte; ^ 0x80 then leaves (u ^ 8) - 8, the signed nibble.
+// Full-rate bit operations only (a multiply by 0x1E for the sign fill compiles to the
+// quarter-rate v_mul_lo_u32, which cost as much as the MFMAs of a W4A8 step).  Checked equal
+// to the multiply form on all 2^32 inputs.
 __device__ __forceinline__ void unpack_int4x8(uint32_t p, int& lo, int& hi) {
-  uint32_t e = (p & 0x0F0F0F0Fu) | ((p & 0x08080808u) * 0x1Eu);
-  uint32_t t = p >> 4;
-  uint32_t o = (t & 0x0F0F0F0Fu) | ((t & 0x08080808u) * 0x1Eu);
-  lo = (int)e;
-  hi = (int)o;
+  lo = (int)((((p & 0x0F0F0F0Fu) ^ 0x88888888u) - 0x08080808u) ^ 0x80808080u);
+  hi = (int)(((((p >> 4) & 0x0F0F0F0Fu) ^ 0x88888888u) - 0x08080808u) ^ 0x80808080u);
 }
 
 __device__ __forceinline__ i32x4 unpack_int4x16(i32x2 p) {

@@ -98,7 +98,7 @@ __device__ __forceinline__ float silu_f(float x) {
 
 // F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
 // bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
-template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, int NS_ = 2>
+template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, int NS_ = 2, bool SCW = false>
 struct MoeCfg {
   static constexpr int NS = NS_;                      // LDS ring slots: the DMA runs NS-1 steps ahead
   static constexpr int NW = WM * WN;                  // waves: WM across the rows, WN across the columns
@@ -118,9 +118,14 @@ struct MoeCfg {
   // spreads the rows over the LDS banks)
   static constexpr int RS = TN * ESZ + 16;
   // one ring slot: a K step's A and B tiles, and at least 16 rows of the atomic epilogue's
-  // staging, which reuses the slot (int4 weights leave the data part small)
-  static constexpr int SLOT = A_BYTES + B_BYTES > 16 * RS ? A_BYTES + B_BYTES : 16 * RS;
-  static constexpr int CH = (SLOT / RS) / 16 * 16 < TME ? (SLOT / RS) / 16 * 16 : TME;  // rows per chunk
+  // staging, which reuses the slot (int4 weights leave the data part small); then, with
+  // per-column weight scales (SCW), the column tile's NB x TN fp32 scales, which the tile's
+  // last K step brings with its DMA (whole 1 KB instructions) so the epilogue reads them from
+  // LDS: a global load of them would be waited for behind the next step's DMA, issued after it
+  static constexpr int SLOT_DATA = A_BYTES + B_BYTES > 16 * RS ? A_BYTES + B_BYTES : 16 * RS;
+  static constexpr int SC_DMA = SCW ? (NB * TN * 4 + 1023) / 1024 : 0;
+  static constexpr int SLOT = SLOT_DATA + SC_DMA * 1024;
+  static constexpr int CH = (SLOT_DATA / RS) / 16 * 16 < TME ? (SLOT_DATA / RS) / 16 * 16 : TME;  // rows per chunk
   static constexpr int NCH = (TME + CH - 1) / CH;
   static constexpr int NST = MR * NR;                 // direct row stores per thread per column tile
   static_assert(TM % 16 == 0 && NR >= 1 && TN % (16 * WN) == 0 && TMW % 16 == 0 && A_BYTES % 1024 == 0,
@@ -149,7 +154,7 @@ struct MoeCfg {
 // kernels/moe_blockscale_2stage.py:677-777 for stage 1, :1836-1880 for stage 2).
 template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, bool BS = false, int NS = 2>
 __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
-  using C = MoeCfg<STAGE, KIND, TM, R, TN, WM, WN, F32, NS>;
+  using C = MoeCfg<STAGE, KIND, TM, R, TN, WM, WN, F32, NS, !kind_is_16bit(KIND) && !BS>;
   static_assert(NS == 2 || (!BS && STAGE == 1), "the 3-slot ring is for stage 1 row outputs");
   constexpr int NW = C::NW, TMW = C::TMW;
   static_assert(!BS || KIND == KIND_FP8, "blockscale is fp8");
@@ -223,7 +228,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     va[j] = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
   }
   // this lane's rows mi*16 + l16: scale, routing weight, destination row (-1: padding)
-  float sx_r[MR], rw_r[MR];
+  float sx_r[MR], rw_r[MR], fr_r[MR];
   int dst_r[MR], arow_r[MR];
 #pragma unroll
   for (int mi = 0; mi < MR; ++mi) {
@@ -238,6 +243,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
     sx_r[mi] = ok ? sxv : 0.f;  // 0 keeps padding rows finite; 1 for unscaled kinds
     rw_r[mi] = ok ? rwv : 0.f;
+    fr_r[mi] = sx_r[mi] * rw_r[mi];   // stage 2's row factor (rw_r is 1 without doweight)
   }
 
   const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
@@ -247,6 +253,8 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   // K/2 for int4 weights of int8 activations, K/4 for int4 weights of bf16 activations
   const uint32_t wrb = KIND == KIND_W4A16 ? (uint32_t)K / 4u : (KIND == KIND_INT4 ? (uint32_t)K / 2u : (uint32_t)K);
   const sgpr4 rsrc_w = buf_desc(p.w + (size_t)e * (size_t)wrows * wrb, (uint32_t)wrows * wrb);
+  // this expert's per-column weight scales (gate then up in stage 1)
+  const sgpr4 rsrc_s = buf_desc(p.sw + (size_t)e * wrows, (uint32_t)wrows * 4u);
   const uint32_t vb = (uint32_t)lane * 16u;
   // W4A16: one DMA instruction brings two adjacent 16-column blocks, 512 bytes each
   const uint32_t vb_w4 = (uint32_t)(lane & 31) * 16u + (uint32_t)(lane >> 5) * 16u * wrb;
@@ -280,6 +288,20 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
         so = (uint32_t)gblk(q >> 1) * 16u * wrb + (uint32_t)kt * 2048u + (uint32_t)(q & 1) * 1024u;
       }
       dma16(rsrc_w, st + C::A_BYTES + q * 1024, vo, __builtin_amdgcn_readfirstlane(so));
+    }
+    // the column tile's weight scales with its last K step, by the last waves (instruction i:
+    // scale elements 256i .. 256i+255 of [NB][TN]; lanes past the end bring zeros)
+    if constexpr (C::SC_DMA > 0) {
+      if (scaled_w && kt == nk - 1) {
+#pragma unroll
+        for (int i = 0; i < C::SC_DMA; ++i) {
+          if (wave != NW - 1 - i) continue;   // wave-uniform
+          const int idx = i * 256 + lane * 4;
+          const int h = idx / TN, col = idx - h * TN;
+          const uint32_t vs = idx < NB * TN ? (uint32_t)(h * p.N + jt * TN + col) * 4u : 0x80000000u;
+          dma16(rsrc_s, st + C::SLOT_DATA + i * 1024, vs, 0);
+        }
+      }
     }
   };
 
@@ -387,10 +409,6 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     }
   };
 
-  auto col_scale = [&](int jt, int h, int ni) -> f32x4 {
-    const int n = jt * TN + (wn * NR + ni) * 16 + lq * 4;
-    return scaled_w ? *(const f32x4*)(p.sw + (size_t)e * wrows + (h ? p.N : 0) + n) : f32x4{1.f, 1.f, 1.f, 1.f};
-  };
 
   // Epilogue of column tile jt.  Lane (l16, lq) holds row mi*16 + l16, columns 4*lq .. 4*lq+3
   // of each of its 16-column blocks.  Atomic outputs: through the LDS slot `ot` (free once every
@@ -399,72 +417,94 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   // (scattered 4-lane fragments would touch 16 cache lines per instruction, which costs the
   // atomics 8x their useful rate).
   const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
-  // column scales of the current tile, loaded at its first step ahead of that step's DMA (so
-  // the next step's wait covers them and the epilogue waits for nothing)
-  f32x4 sc[NB][NR];
-  auto epilogue = [&](int jt, uint8_t* ot) {
+  // `last`: the slot of the tile's last K step, which holds the column scales after its data;
+  // it is next written by a DMA issued after the following step's barrier, so every wave
+  // reads it here before any wave can overwrite it.
+  auto epilogue = [&](int jt, uint8_t* ot, const uint8_t* last) {
     const int n0 = jt * TN;
+    f32x4 sc[NB][NR];
+#pragma unroll
+    for (int h = 0; h < NB; ++h)
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni) {
+        sc[h][ni] = f32x4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (C::SC_DMA > 0)
+          if (scaled_w) sc[h][ni] = *(const f32x4*)(last + C::SLOT_DATA + (h * TN + (wn * NR + ni) * 16 + lq * 4) * 4);
+      }
+    // Output element (mi, ni, q) before rounding: stage 1 silu(gate) * up of the scaled
+    // accumulators, times the routing weight when W; stage 2 the accumulator times the column
+    // scale and the row factor fr (activation scale times routing weight, 1 without doweight:
+    // two multiplies per element).  Uniform facts (output type, doweight) are template tags of
+    // the loops below, so no per-element branch or select is left.
+    auto value = [&](int mi, int ni, int q, auto w_tag) -> float {
+      if constexpr (STAGE == 1) {
+        const float g = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
+        const float u = ((float)acc[1][mi][ni][q] * sx_r[mi]) * sc[1][ni][q];
+        const float v = silu_f(g) * u;
+        return decltype(w_tag)::value ? v * rw_r[mi] : v;
+      } else {
+        return ((float)acc[0][mi][ni][q] * sc[0][ni][q]) * fr_r[mi];
+      }
+    };
+    auto dispatch = [&](auto body) {
+      using T = std::true_type;
+      using F = std::false_type;
+      if (obf16) {
+        if (STAGE == 1 && p.doweight) body(T{}, T{}); else body(T{}, F{});
+      } else {
+        if (STAGE == 1 && p.doweight) body(F{}, T{}); else body(F{}, F{});
+      }
+    };
     if (!F32 && rows) {
       // Row outputs (stage 1, reduce mode): straight from the accumulators, 8 bytes per lane
       // (4 columns of one row), exactly NST buffer stores per thread (padding rows get an
       // offset past the buffer).  Partial lines merge in the write-back L2, so this costs no
       // more HBM traffic than staged full-line stores and saves the LDS round trip.
+      dispatch([&](auto bf_tag, auto w_tag) {
+        constexpr bool BF = decltype(bf_tag)::value;
 #pragma unroll
-      for (int mi = 0; mi < MR; ++mi) {
-#pragma unroll
-        for (int ni = 0; ni < NR; ++ni) {
-          const int c = (wn * NR + ni) * 16 + lq * 4;
-          float v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if constexpr (STAGE == 1) {
-              const float g = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
-              const float u = ((float)acc[1][mi][ni][q] * sx_r[mi]) * sc[1][ni][q];
-              v[q] = silu_f(g) * u;
-            } else {
-              v[q] = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
-            }
-            if (p.doweight) v[q] *= rw_r[mi];
-          }
+        for (int mi = 0; mi < MR; ++mi) {
           const int d = dst_r[mi];
-          const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)(n0 + c)) * 2u;
-          __builtin_amdgcn_raw_buffer_store_b64(obf16 ? pack_out4<true>(v) : pack_out4<false>(v), rsrc_o, off, 0, 0);
+          const uint32_t rowoff = d < 0 ? 0xFFFFFFF0u : (uint32_t)d * (uint32_t)p.N * 2u;
+#pragma unroll
+          for (int ni = 0; ni < NR; ++ni) {
+            const int c = (wn * NR + ni) * 16 + lq * 4;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = value(mi, ni, q, w_tag);
+            const uint32_t off = d < 0 ? rowoff : rowoff + (uint32_t)(n0 + c) * 2u;
+            __builtin_amdgcn_raw_buffer_store_b64(pack_out4<BF>(v), rsrc_o, off, 0, 0);
+          }
         }
-      }
+      });
       return;
     }
     workgroup_barrier();  // every wave is done computing from the slot
 #pragma unroll
     for (int ch = 0; ch < C::NCH; ++ch) {
       if (ch > 0) workgroup_barrier();  // the previous chunk's rows have been read out
+      dispatch([&](auto bf_tag, auto w_tag) {
+        constexpr bool BF = decltype(bf_tag)::value;
 #pragma unroll
-      for (int mi = 0; mi < MR; ++mi) {
-        if ((rw0 + mi * 16) / C::CH != ch) continue;   // wave-uniform: this row block is in another chunk
-        __builtin_amdgcn_sched_barrier(0);
-        const int r = rw0 + mi * 16 + l16 - ch * C::CH;
-        if (wn == 0 && lq == 0) *(int*)(ot + r * C::RS + TN * C::ESZ) = dst_r[mi];
+        for (int mi = 0; mi < MR; ++mi) {
+          if ((rw0 + mi * 16) / C::CH != ch) continue;   // wave-uniform: this row block is in another chunk
+          __builtin_amdgcn_sched_barrier(0);
+          const int r = rw0 + mi * 16 + l16 - ch * C::CH;
+          if (wn == 0 && lq == 0) *(int*)(ot + r * C::RS + TN * C::ESZ) = dst_r[mi];
 #pragma unroll
-        for (int ni = 0; ni < NR; ++ni) {
-          const int c = (wn * NR + ni) * 16 + lq * 4;
-          float v[4];
+          for (int ni = 0; ni < NR; ++ni) {
+            const int c = (wn * NR + ni) * 16 + lq * 4;
+            float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if constexpr (STAGE == 1) {
-              const float g = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
-              const float u = ((float)acc[1][mi][ni][q] * sx_r[mi]) * sc[1][ni][q];
-              v[q] = silu_f(g) * u;
-            } else {
-              v[q] = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
-            }
-            if (p.doweight) v[q] *= rw_r[mi];
+            for (int q = 0; q < 4; ++q) v[q] = value(mi, ni, q, w_tag);
+            uint8_t* dst = ot + r * C::RS + c * C::ESZ;
+            if constexpr (C::ESZ == 4)
+              *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+            else
+              *(i32x2*)dst = pack_out4<BF>(v);
           }
-          uint8_t* dst = ot + r * C::RS + c * C::ESZ;
-          if constexpr (C::ESZ == 4)
-            *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
-          else
-            *(i32x2*)dst = obf16 ? pack_out4<true>(v) : pack_out4<false>(v);
         }
-      }
+      });
       workgroup_barrier();
       const int nrows = min(C::CH, TME - ch * C::CH);
       {
@@ -498,7 +538,8 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     // Three slots, the DMA two steps ahead (for stage 1, whose gathered rows miss the L2 and
     // whose tiles are long).  A step's DMA is complete once no more than the next step's
     // DMA_PER_STEP operations are outstanding; the last step waits for everything.  Row stores
-    // and column scales issued between may make that wait longer, never too short.
+    // issued between, and the column-scale DMA that the last waves add to a tile's last step,
+    // may make that wait longer, never too short.
     const int S = (j1 - j0) * nk;
     int ij = j0, ik = 0;  // the next step to issue
     auto issue_next = [&](int sl) {
@@ -507,7 +548,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     };
     issue_next(0);
     if (S > 1) issue_next(1);
-    int s = 0, slot = 0;
+    int s = 0, slot = 0, last = 0;
     for (int jt = j0; jt < j1; ++jt) {
 #pragma unroll
       for (int h = 0; h < NB; ++h)
@@ -521,17 +562,12 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
         else
           wait_dma();
         workgroup_barrier();  // step s's slot is published; every wave is done with step s-1's
-        if (kt == 0) {
-#pragma unroll
-          for (int h = 0; h < NB; ++h)
-#pragma unroll
-            for (int ni = 0; ni < NR; ++ni) sc[h][ni] = col_scale(jt, h, ni);
-        }
         if (s + 2 < S) issue_next(slot == 0 ? 2 : slot - 1);   // the slot step s-1 used
         compute(ring + slot * C::SLOT);
+        last = slot;
         slot = slot == 2 ? 0 : slot + 1;
       }
-      epilogue(jt, nullptr);   // row outputs: stored from registers, no LDS staging
+      epilogue(jt, nullptr, ring + last * C::SLOT);   // row outputs: stored from registers
     }
     return;
   }
@@ -581,12 +617,6 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
         else if (jt + 1 < j1)
           load_bs(jt + 1, 0);
       }
-      if (kt == 0) {
-#pragma unroll
-        for (int h = 0; h < NB; ++h)
-#pragma unroll
-          for (int ni = 0; ni < NR; ++ni) sc[h][ni] = col_scale(jt, h, ni);
-      }
       if (kt + 1 < nk)
         issue(jt, kt + 1, slot ^ 1);
       else if (jt + 1 < j1)
@@ -594,7 +624,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
       compute(ring + slot * C::SLOT);
       slot ^= 1;
     }
-    epilogue(jt, ring + (slot ^ 1) * C::SLOT);
+    epilogue(jt, ring + (slot ^ 1) * C::SLOT, ring + (slot ^ 1) * C::SLOT);
     keep_stores = rows;
   }
 }
