@@ -83,14 +83,15 @@ class Runner:
         j = i % self.copies
         self.fn(self.c.view(-1), self.a[j], self.b[j], self.sa, self.sb, self.w.M, self.w.N, stream)
 
-    def time(self, steps, warmup, graph=False, replays=3):
+    def time(self, steps, warmup, graph=False, replays=3, warm_s=0.1):
         """Average milliseconds per launch over ``steps`` launches, timed with HIP events on
         the launch stream.  ``graph``: the launches are captured once into a HIP graph, the
-        graph is replayed twice untimed (so an MFMA-bound kernel runs at the clock it holds
-        under sustained load, which it reaches after some tens of milliseconds), and the
-        median of ``replays`` timed replays is reported; a kernel shorter than the host's
-        per-call cost (about 9 us through the Python launcher) is then timed at its own rate
-        rather than at the rate the host can issue calls."""
+        graph is replayed untimed for at least ``warm_s`` seconds of back-to-back work (at
+        least twice; the GPU reaches the clock it holds under sustained load only after some
+        tens of milliseconds, and two replays of 50 launches of a 25 us kernel last 2.5 ms),
+        and the median of ``replays`` timed replays is reported; a kernel shorter than the
+        host's per-call cost (about 9 us through the Python launcher) is then timed at its own
+        rate rather than at the rate the host can issue calls."""
         stream = torch.cuda.current_stream()
         for i in range(warmup):
             self.launch(i, stream)
@@ -102,9 +103,12 @@ class Runner:
                 cap = torch.cuda.current_stream()
                 for i in range(steps):
                     self.launch(i, cap)
-            for _ in range(2):
-                g.replay()
-            torch.cuda.synchronize()
+            t_warm, n_warm = time.perf_counter(), 0
+            while n_warm < 2 or (time.perf_counter() - t_warm < warm_s and n_warm < 2000):
+                for _ in range(4 if n_warm >= 2 else 2):
+                    g.replay()
+                n_warm += 4 if n_warm >= 2 else 2
+                torch.cuda.synchronize()
             times, walls = [], []
             for _ in range(replays):
                 t0 = time.perf_counter()
@@ -458,7 +462,7 @@ def main():
         ms2, _ = r2.time(n2, max(2, args.warmup // 2), graph=True)
         b2 = "hbm" if name in ("C1", "C2", "Q", "MD1", "MD2", "MD2R", "MB1", "MB2") else "mfma"
         sec[name] = {"ms": round(ms2, 5), "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
-                     "timing": f"HIP graph of {n2} launches, median of 3 timed replays after 2 untimed",
+                     "timing": f"HIP graph of {n2} launches, median of 3 timed replays after >= 0.1 s of untimed ones",
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
         if w2.flops:
             sec[name]["TFLOP/s"] = round(w2.flops / ms2 / 1e9, 1)
