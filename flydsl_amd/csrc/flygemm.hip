@@ -58,7 +58,8 @@ struct Shape {
   X(256, 128, 2, 4)    \
   X(128, 256, 2, 4)    \
   X(256, 64, 4, 1)     \
-  X(128, 64, 2, 2)
+  X(128, 64, 2, 2)     \
+  X(64, 64, 1, 4)
 
 #define DECODE_SHAPES(X) \
   X(1, 1, 8, 4)          \
@@ -96,10 +97,19 @@ constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 constexpr int kFirstDecode = 0 MAIN_SHAPES(COUNT);
 constexpr int kFirstRows = kFirstDecode DECODE_SHAPES(COUNT);
 #undef COUNT
-// at most this many 64x128 output tiles: the row-blocked streaming kernel instead (it is 1.7-2x
-// faster at 64 tiles and level at 128: 256x4096x4096 15.9 us against 15.6, 96x8192x8192 33.6
-// against 32.4)
-constexpr long kRowsMaxTiles = 96;
+// Fewer output tiles of 64x128 than the chip has CUs.  At most kRowsMaxTiles: the row-blocked
+// streaming kernel (128x4096x4096 fp8 8.8 us; 64x128 tiles 16.0, 64x64 tiles 13.0); up to
+// kSmallMaxTiles: 64x64 tiles, twice as many workgroups (graph-timed on MI355X, 64x64 against
+// 64x128 and the row-blocked kernel: 96-128 tiles of 64x128 -- 256x4096x4096 fp8 13.2 us against
+// 16.0 / 15.9, 128x8192x8192 27.7 against 34.2 / 33.9, 192x4096x4096 13.1 against 16.0 / 15.8,
+// 128x7168x2048 int8 8.2 against 10.1 / 10.4, 256x4096x4096 bf16 24.8 against 30.6 / 29.0,
+// int4 16.3 against 17.8 / 16.2, 128x7168x7168 blockscale 32.7 against 35.7 / 48.4; at 160 tiles
+// 320x4096x4096 16.5 against 16.1, at 224 fp8 256x7168x7168 32.0 against 28.6).  Not for MXFP4.
+// Blockscale and MXFP4 keep the row-blocked kernel up to 96 tiles (their 16-row blocks were
+// measured against 64x128 only: blockscale 256x2112x7168 25.1 us against 40.6).
+constexpr long kRowsMaxTiles = 64;
+constexpr long kRowsMaxTiles16 = 96;
+constexpr long kSmallMaxTiles = 144;
 
 // One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
@@ -219,9 +229,13 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     if (epi == EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && N % 256 != 0) continue;
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg || wg > list[i].max_wg) continue;
-    // the last resort (64x128) leaves CUs idle when there are at most 128 tiles: the
-    // row-blocked streaming kernel spreads the output over every CU instead
-    if (list[i].min_wg == 0 && wg <= kRowsMaxTiles) return select_rows(kind, epi);
+    // the last resort (64x128) leaves CUs idle with few tiles: the row-blocked streaming kernel
+    // or 64x64 tiles spread the output over more CUs instead
+    const long rows_max = (epi == EPI_BLOCK || kind == KIND_FP4) ? kRowsMaxTiles16 : kRowsMaxTiles;
+    if (list[i].min_wg == 0 && wg <= rows_max) return select_rows(kind, epi);
+    if (list[i].min_wg == 0 && wg <= kSmallMaxTiles && kind != KIND_FP4)
+      for (int v = 0; v < kFirstDecode; ++v)
+        if (kShapes[v].bm == 64 && kShapes[v].bn == 64) return v;
     for (int v = 0; v < kFirstDecode; ++v)
       if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }
@@ -520,6 +534,11 @@ int flygemm_mxfp4(void* c, const void* a, const void* b, const void* scale_a, co
   if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16 && out_dtype != FLYGEMM_OUT_F32)
     return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
   if (M > 0 && (!scale_a || !scale_b)) return fail(hipErrorInvalidValue, "null scale pointer");
+  // the MXFP4 compute reads one scale word per 32-column group of a wave's columns, so the
+  // 64x64 tile's 16-column wave tiles are not available here
+  if (variant >= 0 && kShapes[variant].family == FAM_MAIN && kShapes[variant].bm == 64 && kShapes[variant].bn == 64)
+    return fail(hipErrorInvalidValue, "variant %s is not available for MXFP4 (16-column wave tiles split a scale group)",
+                kShapes[variant].name);
   GemmArgs args{c, (const uint8_t*)a, (const uint8_t*)b, (const float*)scale_a, (const float*)scale_b, M, N, K / 2};
   if (out_dtype == FLYGEMM_OUT_F32) return launch(KIND_FP4, EPI_RAW, FLYGEMM_OUT_BF16, variant, args, (hipStream_t)stream);
   return launch(KIND_FP4, EPI_ROWCOL, out_dtype, variant, args, (hipStream_t)stream);

@@ -78,6 +78,12 @@ def test_reference_shapes(gpu, M, out_dtype):
 
 @pytest.mark.parametrize("variant", list(range(len(VARIANTS))))
 def test_variants_ragged_fp32(gpu, variant):
+    if VARIANTS[variant] == "main_64x64_w1x4":
+        # its 16-column wave tiles would split a 32-column scale group: rejected before launch
+        ops = workloads.make_operands(workloads.custom("mxfp4", 64, 64, 256, seed=1))
+        with pytest.raises(RuntimeError, match="not available for MXFP4"):
+            _run(ops, gpu, "fp32", variant)
+        return
     for (M, N, K) in [(1, 64, 256), (7, 2080, 512), (16, 1024, 768), (33, 1056, 256), (100, 288, 512),
                       (300, 544, 768)]:
         _say(f"variant {VARIANTS[variant]} mxfp4 {M}x{N}x{K}")

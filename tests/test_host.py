@@ -54,6 +54,15 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(32, 2112, 7168, 0, 1)].startswith("decode_m2")
     assert names[lib.flygemm_select_variant(16, 7168, 7168, 0, 1)].startswith("decode_m1")
+    # 65-144 tiles of 64x128: 64x64 tiles (twice the workgroups); at most 64: the row-blocked
+    # kernel; above 144: 64x128; never 64x64 for MXFP4
+    for args in [(256, 4096, 4096, 0, 0), (128, 8192, 8192, 0, 0), (192, 4096, 4096, 0, 0), (128, 7168, 2048, 1, 0),
+                 (256, 4096, 4096, 2, 0), (256, 4096, 4096, 3, 0), (128, 7168, 7168, 0, 1), (96, 8192, 8192, 0, 0)]:
+        assert names[lib.flygemm_select_variant(*args)] == "main_64x64_w1x4", args
+    assert names[lib.flygemm_select_variant(128, 4096, 4096, 1, 0)] == "rows_m2_nb4_w8_u3"    # 64 tiles
+    assert names[lib.flygemm_select_variant(320, 4096, 4096, 0, 0)] == "main_64x128_w1x4"     # 160 tiles
+    assert names[lib.flygemm_select_variant(256, 7168, 7168, 0, 0)] == "main_64x128_w1x4"     # 224 tiles
+    assert names[lib.flygemm_select_variant(256, 4096, 4096, 5, 0)] == "main_64x128_w1x4"     # MXFP4
     # blockscale: 256x256 from 200 tiles, 256x128 from 160
     assert names[lib.flygemm_select_variant(2048, 7168, 7168, 0, 1)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(2048, 3072, 1536, 0, 1)] == "main_128x256_w2x4"
@@ -68,12 +77,11 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 2, 0)] == "main_128x128_w2x2"  # int4: no 128x256
     assert names[lib.flygemm_select_variant(1280, 7168, 7168, 0, 0)] == "main_128x128_w2x2"  # 280 tiles of 128x256
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
-    # the row-blocked kernel where the 64x128 tiles leave CUs idle (at most 96 tiles), with
-    # 16-row blocks for blockscale and MXFP4
+    # the row-blocked kernel where the 64x128 tiles leave CUs idle (at most 64 tiles; 96 with
+    # the 16-row blocks of blockscale and MXFP4)
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 0)] == "rows_m2_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(128, 4096, 1024, 1, 0)] == "rows_m2_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(256, 8192, 4096, 0, 0)] == "main_64x128_w1x4"
-    assert names[lib.flygemm_select_variant(256, 4096, 4096, 0, 0)] == "main_64x128_w1x4"  # 128 tiles
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 1)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(256, 2112, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(33, 2112, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
