@@ -419,11 +419,72 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   // ---- epilogue ----
   // B is the MFMA's first operand, so each 16x16 accumulator tile is C transposed: lane
   // (lq, l16) holds row l16, columns 4*lq .. 4*lq+3 -- one 8-byte bf16/fp16 store (16 bytes
-  // for raw accumulators) per tile.  Every lane issues exactly MR*NR buffer stores; those
-  // outside C get an offset past the buffer end and are dropped by the bounds check, so the
-  // number of stores in flight is known when the next tile waits for its first loads.
+  // for raw accumulators) per tile.  Every lane issues exactly MR*NR buffer stores (NSTORE with
+  // the staged epilogue below); those outside C get an offset past the buffer end and are
+  // dropped by the bounds check, so the number of stores in flight is known when the next tile
+  // waits for its first loads.
   constexpr int ESZ = (EPI == EPI_RAW) ? 4 : 2;
   const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(p.c, M * N * ESZ);
+  // Staged epilogue (2-byte outputs): in two rounds, each wave's first and then second half of
+  // its rows go through the LDS stage `stg` (free once every wave is past the first barrier),
+  // then every thread stores 16-byte chunks so that each wave instruction writes whole
+  // 128-byte lines (the MFMA layout writes 16 rows x 32 bytes per instruction, which the memory
+  // system takes at about 2/3 of the rate of whole lines).  Staged row sr holds row
+  // (sr / HR) * TM + h * HR + sr % HR of the tile in round h (HR = TM / 2); its chunk c sits at
+  // chunk c ^ (sr % CPR).
+  constexpr int RB = BN * 2, CPR = RB / 16, HR = C::TM / 2, HMR = MR / 2;
+  // (not where its registers would spill: more than 4 column blocks per wave, or the blockscale
+  // epilogue's partials next to 32 accumulator tiles; nor for 64-column tiles, whose 128-byte
+  // rows gain less than the two barriers cost: 256x4096x4096 fp8 on 64x64 tiles 13.9 us staged
+  // against 13.6 direct -- those keep the direct stores).  Measured against the direct stores:
+  // C3 59.8 us against 62.1, C4 64.4 against 66.0, C5 20.9 against 21.8, T 412 against 418,
+  // 1024x7168x7168 fp8 56.3 against 58.0, MXFP4 4096^3 35.5 against 38.5.
+  constexpr bool kStage = EPI != EPI_RAW && MR % 2 == 0 && NR <= 4 && BN >= 128 && !(EPI == EPI_BLOCK && MR * NR >= 32) &&
+                          BM / 2 * RB <= C::STAGE && (BM / 2 * CPR) % C::NT == 0;
+  constexpr int SCH = kStage ? (BM / 2 * CPR) / C::NT : 0;
+  constexpr int NSTORE = SCH > 0 ? 2 * SCH : MR * NR;   // buffer stores per lane per tile
+  auto epilogue_staged = [&](int m0, int n0, uint8_t* stg) {
+    float sa_e[MR];
+    f32x4 sb_e[NR];
+    if constexpr (kScaled) {
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) sa_e[mi] = p.sa[min(m0 + wm * C::TM + mi * 16 + l16, M - 1)];
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni)
+        sb_e[ni] = *(const f32x4*)(p.sb + min(n0 + wn * C::TN + ni * 16 + lq * 4, N - 4));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      workgroup_barrier();   // the stage is free: computed from (h == 0) or read out (h == 1)
+#pragma unroll
+      for (int mh = 0; mh < HMR; ++mh) {
+        const int mi = h * HMR + mh;
+        const int sr = wm * HR + mh * 16 + l16;
+#pragma unroll
+        for (int ni = 0; ni < NR; ++ni) {
+          const int c = wn * C::TN + ni * 16 + lq * 4;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            v[q] = (float)acc[mi][ni][q];
+            if constexpr (kScaled) v[q] = (v[q] * sa_e[mi]) * sb_e[ni][q];
+          }
+          *(i32x2*)(stg + sr * RB + (((c >> 3) ^ (sr % CPR)) << 4) + (c & 7) * 2) = pack_out4<OUT_BF16>(v);
+        }
+      }
+      workgroup_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 2
+      for (int i = 0; i < SCH; ++i) {
+        const int cc = tid + i * C::NT;
+        const int sr = cc / CPR, ch = cc % CPR;
+        const i32x4 val = *(const i32x4*)(stg + sr * RB + ((ch ^ (sr % CPR)) << 4));
+        const int row = m0 + (sr / HR) * C::TM + h * HR + sr % HR, col = n0 + ch * 8;
+        const uint32_t off = (row < M && col < N) ? ((uint32_t)row * (uint32_t)N + (uint32_t)col) * 2u : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b128(val, rsrc_c, off, 0, 0);
+      }
+    }
+  };
   auto epilogue = [&](int m0, int n0) {
     float sa_e[MR];
     f32x4 sb_e[NR];
@@ -493,7 +554,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     };
     if (iw < nitems) issue_next(0);
     if (iw < nitems) issue_next(1);
-    int step = 0, slot = 0;
+    int step = 0, slot = 0, last = 0;
     for (int w = blockIdx.x; w < nitems; w += G) {
       int m0, n0, kb, ke;
       item(w, m0, n0, kb, ke);
@@ -509,10 +570,15 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         workgroup_barrier();  // step's stage is published; every wave is done with step-1's
         if (iw < nitems) issue_next(slot == 0 ? 2 : slot - 1);  // the stage step-1 used
         compute(ring(slot), kt != kb);
+        last = slot;
         slot = slot == 2 ? 0 : slot + 1;
       }
       if constexpr (EPI == EPI_BLOCK) flush_pending();
-      epilogue(m0, n0);
+      // the last step's stage is written next by the DMA issued after the next step's barrier
+      if constexpr (SCH > 0)
+        epilogue_staged(m0, n0, ring(last));
+      else
+        epilogue(m0, n0);
     }
     return;
   }
@@ -534,7 +600,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       // tile's MR*NR epilogue stores were issued after them and may still be in flight
       // (vector memory operations retire in issue order).
       if (kt == kb && step > 0)
-        wait_vmem_leaving<MR * NR>();
+        wait_vmem_leaving<NSTORE>();
       else
         wait_dma();
       // this step's tile has landed; every wave is done with the other stage.  A bare
@@ -551,7 +617,12 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       compute(cur, kt != kb);
     }
     if constexpr (EPI == EPI_BLOCK) flush_pending();
-    epilogue(m0, n0);
+    // the stage the last step computed from; the DMA issued after the next step's barrier is the
+    // next to write it
+    if constexpr (SCH > 0)
+      epilogue_staged(m0, n0, (step & 1) ? lds0 : lds1);
+    else
+      epilogue(m0, n0);
     m0 = nm0;
     n0 = nn0;
     kb = nkb;
