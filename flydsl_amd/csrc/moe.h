@@ -166,6 +166,21 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   const bool rows = STAGE == 1 || mode == MOE_OUT_F16_ROWS || mode == MOE_OUT_BF16_ROWS;
   const bool obf16 = moe_out_bf16(mode);
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * C::SLOT];
+  // Row outputs of tiles of 128+ columns go through the slot the tile's last K step computed
+  // from, in two rounds of half of every wave's rows, and leave as 16-byte chunks so each wave
+  // instruction writes whole 128-byte lines (the accumulator layout's direct stores cover 16
+  // rows x 32 bytes per instruction, which the memory system takes at about 2/3 of the rate of
+  // whole lines; these are random rows of the reduce mode's intermediate).  Staged row sr of
+  // round h is tile row (sr / HR) * TMW + h * HR + sr % HR; its 16-byte chunk c sits at chunk
+  // c ^ (sr % CPR).  NSTR: row stores per lane per tile.
+  constexpr int RB = TN * 2, CPR = RB / 16, HR = TMW / 2, HMR = MR / 2;
+  // (stage 2 only: stage 1 writes a 2*I-times smaller output and its run tiles were 1.7% slower
+  // staged; DS-TP8 prefill stage 2 in reduce mode 0.71 ms against 0.77)
+  constexpr bool kStageRows = STAGE == 2 && !F32 && MR % 2 == 0 && TN >= 128 && TME / 2 * RB <= C::SLOT_DATA &&
+                              (TME / 2 * CPR) % NT == 0;
+  constexpr int SCHR = kStageRows ? TME / 2 * CPR / NT : 0;
+  constexpr int NSTR = kStageRows ? 2 * SCHR : C::NST;
+  __shared__ int sdst[kStageRows ? TME / 2 : 1];   // destinations of the staged rows
 
   // ---- which run and which column tiles ----
   // Logical id L = block * nsplit + split over the blocks below num_valid_ids, dealt to the 8
@@ -447,11 +462,47 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
       }
     };
     auto pack_sel = [&](const float (&v)[4]) -> i32x2 { return obf16 ? pack_out4<true>(v) : pack_out4<false>(v); };
+    if constexpr (kStageRows) {
+      if (rows) {
+        uint8_t* stg = const_cast<uint8_t*>(last);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          workgroup_barrier();   // the slot is free: computed from (h == 0) or read out (h == 1)
+#pragma unroll
+          for (int mh = 0; mh < HMR; ++mh) {
+            const int mi = h * HMR + mh;
+            const int sr = wm * HR + mh * 16 + l16;
+#pragma unroll
+            for (int ni = 0; ni < NR; ++ni) {
+              const int c = (wn * NR + ni) * 16 + lq * 4;
+              float v[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] = value(mi, ni, q);
+              *(i32x2*)(stg + sr * RB + (((c >> 3) ^ (sr % CPR)) << 4) + (c & 7) * 2) = pack_sel(v);
+            }
+            if (wn == 0 && lq == 0) sdst[sr] = dst_r[mi];
+          }
+          workgroup_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 2
+          for (int i = 0; i < SCHR; ++i) {
+            const int cc = tid + i * NT;
+            const int sr = cc / CPR, ch = cc % CPR;
+            const i32x4 val = *(const i32x4*)(stg + sr * RB + ((ch ^ (sr % CPR)) << 4));
+            const int d = sdst[sr];
+            // padding rows: an offset past the buffer (out_bytes <= 0xFFFFFF00) that a 16-byte
+            // store cannot wrap
+            const uint32_t off = d < 0 ? 0xFFFFFFE0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)n0) * 2u + (uint32_t)ch * 16u;
+            __builtin_amdgcn_raw_buffer_store_b128(val, rsrc_o, off, 0, 0);
+          }
+        }
+        return;
+      }
+    }
     if (!F32 && rows) {
       // Row outputs (stage 1, reduce mode): straight from the accumulators, 8 bytes per lane
       // (4 columns of one row), exactly NST buffer stores per thread (padding rows get an
-      // offset past the buffer).  Partial lines merge in the write-back L2, so this costs no
-      // more HBM traffic than staged full-line stores and saves the LDS round trip.
+      // offset past the buffer).
       {
 #pragma unroll
         for (int mi = 0; mi < MR; ++mi) {
@@ -579,7 +630,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
         for (int j = 0; j < NR; ++j) acc[h][i][j] = AccT{0, 0, 0, 0};
     for (int kt = 0; kt < nk; ++kt) {
       if (keep_stores)
-        wait_vmem_leaving<C::NST>();
+        wait_vmem_leaving<NSTR>();
       else
         wait_dma();
       keep_stores = false;
