@@ -79,6 +79,16 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
   if (!bs && kind != KIND_W4A16 && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
     R = (stage == 1 ? 128 : 256) / tile_m;
     tile_n = run_tn;
+    // Stage 1 of 64-row blocks with four or more blocks per expert on average and a narrow
+    // inter_dim: single-block tiles of 64 columns instead (4 waves, 48 KB of LDS, so up to three
+    // workgroups share a CU and one's epilogue -- silu, the scales, the stores -- runs beside
+    // another's MFMAs).  DS-TP8 dims (128 experts, inter_dim 256), fp8: 4096 tokens 213 us
+    // against 259 for the run tile, 8192 422 against 466, 16384 714 against 908; at 2048 tokens
+    // (two blocks per expert) 167 against 162.  Not measured as better for 16- or 32-row blocks.
+    if (stage == 1 && tile_m == 64 && N <= 256 && N % 64 == 0 && routes >= 4L * tile_m * experts) {
+      R = 1;
+      tile_n = 64;
+    }
   }
   if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
   // Few runs (decode): narrower column tiles until there are workgroups for every CU (each

@@ -356,8 +356,14 @@ def test_moe_tile_choice_pinned():
                                          ctypes.byref(r), ctypes.byref(tn))
         return (r.value, tn.value) if rc == 0 else rc
 
-    # DS-TP8 prefill: runs of 128 rows (stage 1, 128 columns) / 256 rows (stage 2, 256 columns)
-    assert sel(1, 8192, 256, 128, 8, 64, 256) == (2, 128)
+    # DS-TP8 prefill: stage 1 with four or more 64-row blocks per expert: 64-column single-block
+    # tiles; with two or three: runs of 128 rows and 128 columns; stage 2 runs of 256 rows and
+    # 256 columns
+    assert sel(1, 8192, 256, 128, 8, 64, 256) == (1, 64)
+    assert sel(1, 4096, 256, 128, 8, 64, 256) == (1, 64)
+    assert sel(1, 2048, 256, 128, 8, 64, 256) == (2, 128)
+    assert sel(1, 8192, 256, 128, 8, 32, 256) == (4, 128)
+    assert sel(1, 8192, 1024, 128, 8, 64, 256) == (2, 128)
     assert sel(2, 8192, 7168, 128, 8, 64, 256) == (4, 256)
     # decode: 64-column single-block tiles whatever the caller asked
     assert sel(1, 8, 256, 256, 8, 32, 256) == (1, 64)
