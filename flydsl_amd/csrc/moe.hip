@@ -76,7 +76,16 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
   // do not fit next to the run tiles).
   int R = 1;
   const int run_tn = stage == 1 ? 128 : 256;
-  if (!bs && kind != KIND_W4A16 && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
+  // Stage 2 of 32- and 64-row blocks keeps single-block tiles (128 columns, below): with three
+  // workgroups per CU their epilogues and row stores overlap each other's MFMAs.  DS-TP8 dims
+  // (128 experts, model_dim 7168, inter_dim 256), fp8, graph-timed: 64-row blocks, reduce mode
+  // 2048 / 4096 / 8192 / 16384 tokens 167 / 296 / 610 / 1153 us against 247 / 363 / 711 / 1508
+  // for 256-row runs, atomics 270 / 435 / 846 / 1539 against 341 / 457 / 937 / 2167; 32-row
+  // blocks reduce 189 / 381 / 702 / 1369 against 277 / 374 / 723 / 1512, atomics 254 / 502 /
+  // 835 / 1701 against 385 / 454 / 991 / 2185.  16-row blocks keep the runs (reduce mode 1.0-1.3x
+  // slower single-block from 4096 tokens).
+  const bool runs_ok = !(stage == 2 && tile_m >= 32);
+  if (!bs && kind != KIND_W4A16 && runs_ok && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
     R = (stage == 1 ? 128 : 256) / tile_m;
     tile_n = run_tn;
     // Stage 1 of 64-row blocks with four or more blocks per expert on average and a narrow

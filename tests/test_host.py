@@ -357,14 +357,16 @@ def test_moe_tile_choice_pinned():
         return (r.value, tn.value) if rc == 0 else rc
 
     # DS-TP8 prefill: stage 1 with four or more 64-row blocks per expert: 64-column single-block
-    # tiles; with two or three: runs of 128 rows and 128 columns; stage 2 runs of 256 rows and
-    # 256 columns
+    # tiles; with two or three: runs of 128 rows and 128 columns; stage 2: 128-column single-block
+    # tiles for 32- and 64-row blocks, runs of 256 rows and 256 columns for 16-row blocks
     assert sel(1, 8192, 256, 128, 8, 64, 256) == (1, 64)
     assert sel(1, 4096, 256, 128, 8, 64, 256) == (1, 64)
     assert sel(1, 2048, 256, 128, 8, 64, 256) == (2, 128)
     assert sel(1, 8192, 256, 128, 8, 32, 256) == (4, 128)
     assert sel(1, 8192, 1024, 128, 8, 64, 256) == (2, 128)
-    assert sel(2, 8192, 7168, 128, 8, 64, 256) == (4, 256)
+    assert sel(2, 8192, 7168, 128, 8, 64, 256) == (1, 128)
+    assert sel(2, 8192, 7168, 128, 8, 32, 256) == (1, 128)
+    assert sel(2, 8192, 7168, 128, 8, 16, 256) == (16, 256)
     # decode: 64-column single-block tiles whatever the caller asked
     assert sel(1, 8, 256, 256, 8, 32, 256) == (1, 64)
     assert sel(2, 8, 7168, 256, 8, 32, 256) == (1, 64)
@@ -375,8 +377,9 @@ def test_moe_tile_choice_pinned():
     assert sel(1, 160, 1024, 64, 4, 32, 256, "fp8", 1) == (1, 256)
     assert sel(2, 128, 7168, 256, 8, 32, 0) == (1, 128)
     # blockscale and W4A16 never take run tiles
-    assert sel(2, 8192, 7168, 128, 8, 64, 256, "fp8", 1)[0] == 1
-    assert sel(2, 8192, 7168, 128, 8, 64, 256, "int4_bf16")[0] == 1
+    assert sel(2, 8192, 7168, 128, 8, 16, 256, "fp8", 1)[0] == 1
+    assert sel(2, 8192, 7168, 128, 8, 16, 256, "int4_bf16")[0] == 1
+    assert sel(1, 8192, 256, 128, 8, 16, 256, "fp8", 1)[0] == 1
     # validation
     assert sel(3, 16, 256, 4, 2, 16, 64) != 0 and b"stage" in lib.flygemm_last_error()
     assert sel(1, 16, 256, 4, 2, 48, 64) != 0 and b"tile_m" in lib.flygemm_last_error()
