@@ -13,7 +13,8 @@ using namespace flygemm;
 
 // Kernel tables, one per stage (stage 2 lives in moe_stage2.hip, compiled in parallel).
 // Instantiated tiles: runs of one routing block (R = 1, 4 waves) for every (tile_m, tile_n);
-// runs of 128 rows (stage 1) or 256 rows (stage 2) with 256-column tiles and 8 waves.
+// runs of 128 rows (stage 1, 128 columns) and, for 16-row blocks, of 256 rows (stage 2, 256
+// columns) with 8 waves.
 namespace flygemm {
 MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
 }

@@ -15,10 +15,11 @@ MoeFn stage2_tile(int tm, int r, int tn) {
   // tiles of 256 columns (it narrows them to 128 or 64)
   T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4) T(64, 1, 64, 1, 4)
   T(64, 1, 128, 1, 4)
-  // run tiles: not for blockscale (its partials and factors do not fit next to them) nor W4A16
-  // (its group scales ride the two-slot pipeline)
+  // run tiles of 256 rows: for 16-row blocks only (32- and 64-row blocks keep single-block
+  // tiles in stage 2); not for blockscale (its partials and factors do not fit next to them)
+  // nor W4A16 (its group scales ride the two-slot pipeline)
   if constexpr (!BS && KIND != KIND_W4A16) {
-    T(16, 16, 256, 2, 4) T(32, 8, 256, 2, 4) T(64, 4, 256, 2, 4)
+    T(16, 16, 256, 2, 4)
   }
 #undef T
   return nullptr;
