@@ -181,6 +181,11 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   constexpr int SCHR = kStageRows ? TME / 2 * CPR / NT : 0;
   constexpr int NSTR = kStageRows ? 2 * SCHR : C::NST;
   __shared__ int sdst[kStageRows ? TME / 2 : 1];   // destinations of the staged rows
+  // Stage-2 row outputs with at most two K tiles (`ares`): steps alternate the two slots and
+  // every column tile has the same K tiles, so K tile kt's A rows stay in the A part of slot kt
+  // (of both slots for a single K tile) after the first column tile (two for a single K tile),
+  // and later steps DMA only B.  The row staging then uses the last slot's B part.
+  constexpr bool kAres = STAGE == 2 && NS == 2 && !F32 && !BS && (!kStageRows || TME / 2 * RB <= C::B_BYTES);
 
   // ---- which run and which column tiles ----
   // Logical id L = block * nsplit + split over the blocks below num_valid_ids, dealt to the 8
@@ -208,6 +213,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   if (j0 >= j1) return;
   const int K = p.K;
   const int nk = K / KT;
+  const bool ares = kAres && rows && nk <= 2;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -281,10 +287,12 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     uint8_t* st = ring + slot * C::SLOT;
     // the guards below are compile-time true when the DMA count divides among the waves (no
     // branches in the step then)
+    if (!(ares && jt - j0 >= (nk == 1 ? 2 : 1))) {   // A already resident in this slot
 #pragma unroll
-    for (int j = 0; j < C::AQ; ++j) {
-      const int q = wave + j * NW;
-      if (C::A_DMA % NW == 0 || q < C::A_DMA) dma16(rsrc_a, st + q * 1024, va[j], (uint32_t)kt * KT);
+      for (int j = 0; j < C::AQ; ++j) {
+        const int q = wave + j * NW;
+        if (C::A_DMA % NW == 0 || q < C::A_DMA) dma16(rsrc_a, st + q * 1024, va[j], (uint32_t)kt * KT);
+      }
     }
     const int n0 = jt * TN;
 #pragma unroll
@@ -464,7 +472,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     auto pack_sel = [&](const float (&v)[4]) -> i32x2 { return obf16 ? pack_out4<true>(v) : pack_out4<false>(v); };
     if constexpr (kStageRows) {
       if (rows) {
-        uint8_t* stg = const_cast<uint8_t*>(last);
+        uint8_t* stg = const_cast<uint8_t*>(last) + (ares ? C::A_BYTES : 0);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           workgroup_barrier();   // the slot is free: computed from (h == 0) or read out (h == 1)
