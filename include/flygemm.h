@@ -79,7 +79,9 @@ int flygemm_accumulators(void* acc, const void* a, const void* b, int32_t M, int
  * shuffle_weight_w4(b, 16, False, False) (tests/kernels/utils/fp4_utils.py:578-621), which
  * is the 1-byte preshuffle rule on rows of K/2 bytes.  scale_a / scale_b: E8M0 bytes
  * [round_up(M, 32)][K/32] / [N][K/32] after shuffle_scale_w4(s, 1, False) (:624-653).
- * K % 256 == 0, N % 32 == 0.  out_dtype bf16, fp16 or fp32.  Replaces the launcher of
+ * K % 256 == 0, N % 32 == 0.  out_dtype bf16, fp16 or fp32.  A forced variant of 64x64
+ * tiles is rejected (its 16-column wave tiles would split a 32-column scale group; the
+ * library's own choice never takes it for MXFP4).  Replaces the launcher of
  * compile_preshuffle_gemm_w4 (reference kernels/preshuffle_gemm.py:1306-1337, MFMA use
  * :692-732; harness tests/kernels/test_preshuffle_gemm.py:261-379). */
 int flygemm_mxfp4(void* c, const void* a, const void* b, const void* scale_a, const void* scale_b, int32_t M,
