@@ -699,9 +699,7 @@ __global__ void __launch_bounds__(256) moe_reduce_kernel(void* y, const void* x,
 #pragma unroll
   for (int q = 0; q < VE; ++q) acc[q] = 0.f;
   const i32x4* src = (const i32x4*)x + ((long)t * topk * vpr + v);
-  for (int k = 0; k < topk; ++k) {
-    if (mask && mask[(long)t * topk + k] == 0) continue;
-    const i32x4 w = __builtin_nontemporal_load(src + (long)k * vpr);
+  auto add = [&](const i32x4& w) {
     if constexpr (DT == 2) {
       const f32x4 f = __builtin_bit_cast(f32x4, w);
 #pragma unroll
@@ -712,6 +710,20 @@ __global__ void __launch_bounds__(256) moe_reduce_kernel(void* y, const void* x,
       const ET8 h = __builtin_bit_cast(ET8, w);
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] += (float)h[q];
+    }
+  };
+  if (topk == 8 && !mask) {
+    // the common case: all eight slots' loads in flight at once, then the sums in slot order
+    // (one load at a time left each thread waiting out the memory latency per slot)
+    i32x4 w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = __builtin_nontemporal_load(src + (long)k * vpr);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) add(w[k]);
+  } else {
+    for (int k = 0; k < topk; ++k) {
+      if (mask && mask[(long)t * topk + k] == 0) continue;
+      add(__builtin_nontemporal_load(src + (long)k * vpr));
     }
   }
   i32x4* dst = (i32x4*)y + idx;
