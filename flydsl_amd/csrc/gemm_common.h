@@ -93,24 +93,31 @@ __device__ __forceinline__ f32x4 mfma_fp4(const i32x4& b, const i32x4& a, const 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(b8, a8, c, 4, 4, 2 * H, (int)sb, 2 * H, (int)sa);
 }
 
-// 4 packed int4 bytes (8 nibbles, little-endian) -> 8 sign-extended int8 in two dwords:
-// the low nibbles of bytes 0..3 first, then the high nibbles (the reference's unpack order,
-// kernels/mfma_preshuffle_pipeline.py:277-291).  Per byte, with the nibble u in the low half:
-// x = u ^ 0x88 is (u ^ 8) + 0x80, in 0x80..0x8F; x - 8 stays in 0x78..0x87, so the 32-bit
-// subtraction borrows across no byte; ^ 0x80 then leaves (u ^ 8) - 8, the signed nibble.
-// Full-rate bit operations only (a multiply by 0x1E for the sign fill compiles to the
-// quarter-rate v_mul_lo_u32, which cost as much as the MFMAs of a W4A8 step).  Checked equal
-// to the multiply form on all 2^32 inputs.
-__device__ __forceinline__ void unpack_int4x8(uint32_t p, int& lo, int& hi) {
-  lo = (int)((((p & 0x0F0F0F0Fu) ^ 0x88888888u) - 0x08080808u) ^ 0x80808080u);
-  hi = (int)(((((p >> 4) & 0x0F0F0F0Fu) ^ 0x88888888u) - 0x08080808u) ^ 0x80808080u);
-}
-
+// 8 packed int4 bytes (16 nibbles, little-endian) -> 16 int8 MFMA operands in four dwords: per
+// source dword, the low nibbles of its bytes 0..3 first, then the high nibbles (the reference's
+// unpack order, kernels/mfma_preshuffle_pipeline.py:277-291).  Each nibble lands in the high
+// half of its byte with zeros below, i.e. as the int8 value 16 * n of the signed nibble n (its
+// top bit becomes the byte's sign bit): (p << 4) & 0xF0F0F0F0 for the low nibbles,
+// p & 0xF0F0F0F0 for the high ones -- three full-rate bit operations per dword, against seven
+// for a sign extension in place (which held W4A8 steps back as VALU work next to the MFMAs).
+// The int32 accumulators of int4 weights therefore hold 16x the dot product; int4_acc()
+// divides it out exactly before anything reads them.  16 * |dot| <= 16 * 128 * 8 * K stays
+// below 2^31 for K <= kInt4MaxK, which the entry points check.
 __device__ __forceinline__ i32x4 unpack_int4x16(i32x2 p) {
-  int a, b, c, d;
-  unpack_int4x8((uint32_t)p.x, a, b);
-  unpack_int4x8((uint32_t)p.y, c, d);
-  return i32x4{a, b, c, d};
+  const uint32_t x = (uint32_t)p.x, y = (uint32_t)p.y;
+  return i32x4{(int)((x << 4) & 0xF0F0F0F0u), (int)(x & 0xF0F0F0F0u), (int)((y << 4) & 0xF0F0F0F0u),
+               (int)(y & 0xF0F0F0F0u)};
+}
+constexpr int kInt4MaxK = 131072;
+
+// An accumulator as the dot product: int4 weights' accumulators hold 16x it (exact arithmetic
+// shift), every other kind's are unchanged.
+template <int KIND, typename T>
+__device__ __forceinline__ T int4_acc(T v) {
+  if constexpr (KIND == KIND_INT4)
+    return v >> 4;
+  else
+    return v;
 }
 
 template <bool BF16>

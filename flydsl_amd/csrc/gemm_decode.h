@@ -375,6 +375,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       AccT s = red[0][mi * NBW + j][lane];
 #pragma unroll
       for (int w = 1; w < NW; ++w) s += red[w][mi * NBW + j][lane];
+      s = int4_acc<KIND>(s);
       const int row = m0 + mi * 16 + l16;
       if (row >= M) continue;
       const size_t idx = (size_t)row * N + col;

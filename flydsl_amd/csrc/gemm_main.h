@@ -444,6 +444,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   constexpr int SCH = kStage ? (BM / 2 * CPR) / C::NT : 0;
   constexpr int NSTORE = SCH > 0 ? 2 * SCH : MR * NR;   // buffer stores per lane per tile
   auto epilogue_staged = [&](int m0, int n0, uint8_t* stg) {
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni) acc[mi][ni] = int4_acc<KIND>(acc[mi][ni]);
     float sa_e[MR];
     f32x4 sb_e[NR];
     if constexpr (kScaled) {
@@ -486,6 +490,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     }
   };
   auto epilogue = [&](int m0, int n0) {
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NR; ++ni) acc[mi][ni] = int4_acc<KIND>(acc[mi][ni]);
     float sa_e[MR];
     f32x4 sb_e[NR];
     if constexpr (kScaled) {

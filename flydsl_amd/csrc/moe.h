@@ -462,11 +462,11 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
     // above the branch and spill.
     auto value = [&](int mi, int ni, int q) -> float {
       if constexpr (STAGE == 1) {
-        const float g = ((float)acc[0][mi][ni][q] * sx_r[mi]) * sc[0][ni][q];
-        const float u = ((float)acc[1][mi][ni][q] * sx_r[mi]) * sc[1][ni][q];
+        const float g = ((float)int4_acc<KIND>(acc[0][mi][ni][q]) * sx_r[mi]) * sc[0][ni][q];
+        const float u = ((float)int4_acc<KIND>(acc[1][mi][ni][q]) * sx_r[mi]) * sc[1][ni][q];
         return (silu_f(g) * u) * rw_r[mi];
       } else {
-        return ((float)acc[0][mi][ni][q] * sc[0][ni][q]) * fr_r[mi];
+        return ((float)int4_acc<KIND>(acc[0][mi][ni][q]) * sc[0][ni][q]) * fr_r[mi];
       }
     };
     auto pack_sel = [&](const float (&v)[4]) -> i32x2 { return obf16 ? pack_out4<true>(v) : pack_out4<false>(v); };
