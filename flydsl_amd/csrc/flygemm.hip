@@ -285,9 +285,9 @@ int check_common(const void* c, const void* a, const void* b, int M, int N, int 
 
 // variant: -1 = the library's choice, else the index of a variant in the table.
 int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, hipStream_t stream) {
-  if (kind == KIND_INT4 && args.K > kInt4MaxK)
-    return fail(hipErrorInvalidValue, "K=%d: int4 weights take K <= %d (int32 accumulators of 16x the dot product)",
-                args.K, kInt4MaxK);
+  if (kind == KIND_INT4 && args.K >= kInt4KLimit)
+    return fail(hipErrorInvalidValue, "K=%d: int4 weights take K < %d (int32 accumulators of 16x the dot product)",
+                args.K, kInt4KLimit);
   if (args.M == 0) return 0;
   const int v = variant >= 0 ? variant : select_variant(args.M, args.N, args.K, kind, epi);
   if (v < 0 || v >= kNumShapes)
@@ -489,9 +489,9 @@ int flygemm_preshuffle_quant_a(void* c, void* a_q, float* scale_a, const void* x
   if (kb < 0) return hipErrorInvalidValue;
   int rc = check_common(c, x, b, M, N, kb, variant);
   if (rc) return rc;
-  if (in_dtype == FLYGEMM_IN_INT4 && K > kInt4MaxK)
-    return fail(hipErrorInvalidValue, "K=%d: int4 weights take K <= %d (int32 accumulators of 16x the dot product)", K,
-                kInt4MaxK);
+  if (in_dtype == FLYGEMM_IN_INT4 && K >= kInt4KLimit)
+    return fail(hipErrorInvalidValue, "K=%d: int4 weights take K < %d (int32 accumulators of 16x the dot product)", K,
+                kInt4KLimit);
   const int xsz = x_dtype == FLYGEMM_QIN_F32 ? 4 : 2;
   if ((long)(M + 16) * K * xsz >= (1L << 31))
     return fail(hipErrorInvalidValue, "activations too large for 32-bit offsets (M=%d K=%d)", M, K);

@@ -101,14 +101,14 @@ __device__ __forceinline__ f32x4 mfma_fp4(const i32x4& b, const i32x4& a, const 
 // p & 0xF0F0F0F0 for the high ones -- three full-rate bit operations per dword, against seven
 // for a sign extension in place (which held W4A8 steps back as VALU work next to the MFMAs).
 // The int32 accumulators of int4 weights therefore hold 16x the dot product; int4_acc()
-// divides it out exactly before anything reads them.  16 * |dot| <= 16 * 128 * 8 * K stays
-// below 2^31 for K <= kInt4MaxK, which the entry points check.
+// divides it out exactly before anything reads them.  16 * |dot| <= 16 * 128 * 8 * K = 2^14 * K
+// stays below 2^31 for K < kInt4KLimit = 2^17, which the entry points check.
 __device__ __forceinline__ i32x4 unpack_int4x16(i32x2 p) {
   const uint32_t x = (uint32_t)p.x, y = (uint32_t)p.y;
   return i32x4{(int)((x << 4) & 0xF0F0F0F0u), (int)(x & 0xF0F0F0F0u), (int)((y << 4) & 0xF0F0F0F0u),
                (int)(y & 0xF0F0F0F0u)};
 }
-constexpr int kInt4MaxK = 131072;
+constexpr int kInt4KLimit = 131072;
 
 // An accumulator as the dot product: int4 weights' accumulators hold 16x it (exact arithmetic
 // shift), every other kind's are unchanged.

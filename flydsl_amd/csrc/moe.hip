@@ -162,9 +162,9 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   const int kind = moe_kind(in_dtype, stage, &token_slot);
   if (kind < 0) return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
   if (bs && kind != KIND_FP8) return fail(hipErrorInvalidValue, "%s: blockscale takes fp8", what);
-  if (kind == KIND_INT4 && K > kInt4MaxK)
-    return fail(hipErrorInvalidValue, "%s: K=%d: int4 weights take K <= %d (int32 accumulators of 16x the dot product)",
-                what, K, kInt4MaxK);
+  if (kind == KIND_INT4 && K >= kInt4KLimit)
+    return fail(hipErrorInvalidValue, "%s: K=%d: int4 weights take K < %d (int32 accumulators of 16x the dot product)",
+                what, K, kInt4KLimit);
   // group scales: W4A16 only, 32-element groups along K (reference tests/utils.py:99-120)
   if (group_size > 0 && (kind != KIND_W4A16 || group_size != 32))
     return fail(hipErrorInvalidValue, "%s: group_size=%d: group scales are for int4_bf16 with group_size 32", what,

@@ -51,7 +51,7 @@ enum { FLYGEMM_OUT_BF16 = 0, FLYGEMM_OUT_FP16 = 1, FLYGEMM_OUT_F32 = 2 /* flygem
  * acc = sum_k A[m][k] * B[n][k] in fp32 (fp8, bf16, fp16) or int32 (int8/int4);
  * bf16/fp16 inputs are not scaled: C = out_dtype(acc) (reference preshuffle_gemm.py:804-806).
  * scale_a: fp32 [M] per token; scale_b: fp32 [N] per output channel.
- * int4 weights take K <= 131072 (here, in flygemm_accumulators and flygemm_preshuffle_quant_a).
+ * int4 weights take K < 131072 (here, in flygemm_accumulators and flygemm_preshuffle_quant_a).
  * Replaces the launcher returned by compile_preshuffle_gemm_a8
  * (reference kernels/preshuffle_gemm.py:39-57, launch_gemm :1268-1301; epilogue :863-883). */
 int flygemm_preshuffle(void* c, const void* a, const void* b, const float* scale_a, const float* scale_b,
@@ -137,7 +137,7 @@ int flygemm_preshuffle_quant_a(void* c, void* a_q, float* scale_a, const void* x
  *     x [topk*tokens][model_dim] with row s*tokens + t (slot-major) and scale_x [topk*tokens] in
  *     the same order; stage 2 is plain int8;
  *   FLYGEMM_IN_INT4 ("int4", W4A8): int8 activations, weights packed two int4 per byte exactly as
- *     the dense int4 B (the preshuffled int8 bytes, then packed), per-row scale_w; K <= 131072;
+ *     the dense int4 B (the preshuffled int8 bytes, then packed), per-row scale_w; K < 131072;
  *   FLYGEMM_IN_INT4_BF16 ("int4_bf16", W4A16): bf16 activations (no scale_x), the same packed int4
  *     weights, converted to bf16 in registers; scale_w per weight row when group_size <= 0, or
  *     group scales [experts][K/32][rows of the expert's weight] (w[n][k] * scale[e][k/32][n],

@@ -130,14 +130,15 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc != 0 and b"invalid sizes" in lib.flygemm_last_error()
     # M == 0 is a no-op that succeeds without launching
     assert lib.flygemm_preshuffle(p, p, p, p, p, 0, 128, 256, 0, 0, -1, None) == 0
-    # int4 weights take K <= 131072: their int32 accumulators hold 16x the dot product
-    rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 16, 131072 + 64, 2, 0, -1, None)
-    assert rc != 0 and b"int4 weights take K <= 131072" in lib.flygemm_last_error()
-    rc = lib.flygemm_accumulators(p, p, p, 16, 16, 131072 + 64, 2, -1, None)
-    assert rc != 0 and b"int4 weights take K <= 131072" in lib.flygemm_last_error()
-    rc = lib.flygemm_preshuffle_quant_a(p, p, p, p, p, p, 16, 16, 131072 + 64, 0, 2, 0, 0, -1, None)
-    assert rc != 0 and b"int4 weights take K <= 131072" in lib.flygemm_last_error()
-    assert lib.flygemm_preshuffle(p, p, p, p, p, 0, 16, 131072, 2, 0, -1, None) == 0
+    # int4 weights take K < 131072: their int32 accumulators hold 16x the dot product, and
+    # 16 * 1024 * 131072 (every product (-128) * (-8)) would reach 2^31
+    rc = lib.flygemm_preshuffle(p, p, p, p, p, 16, 16, 131072, 2, 0, -1, None)
+    assert rc != 0 and b"int4 weights take K < 131072" in lib.flygemm_last_error()
+    rc = lib.flygemm_accumulators(p, p, p, 16, 16, 131072, 2, -1, None)
+    assert rc != 0 and b"int4 weights take K < 131072" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle_quant_a(p, p, p, p, p, p, 16, 16, 131072, 0, 2, 0, 0, -1, None)
+    assert rc != 0 and b"int4 weights take K < 131072" in lib.flygemm_last_error()
+    assert lib.flygemm_preshuffle(p, p, p, p, p, 0, 16, 131072 - 64, 2, 0, -1, None) == 0
     # per-row quantization
     rc = lib.flygemm_quant_rows(p, p, p, 4, 12, 0, 1, 0, None)
     assert rc != 0 and b"multiple of 8" in lib.flygemm_last_error()
@@ -275,7 +276,7 @@ def test_moe_abi_rejects_bad_arguments_before_launch():
     assert s1(topk=0) != 0 and b"topk" in err()
     assert s1(tokens=1 << 24) != 0 and b"2^24" in err()
     assert s1(tokens=0) == 0 and s1(blocks=0) == 0                # nothing to do
-    assert s1(in_dtype=2, model=131072 + 128) != 0 and b"int4 weights take K <= 131072" in err()
+    assert s1(in_dtype=2, model=131072) != 0 and b"int4 weights take K < 131072" in err()
     rc = lib.flygemm_moe_gemm2(p, p, p, None, p, p, p, p, p, 64, 256, 128, 12, 4, 2, 16, 64, 0, 2, 1, 1, -1, None)
     assert rc != 0 and b"null scale" in err()
     rc = lib.flygemm_moe_gemm2(p, p, p, None, None, p, p, None, p, 64, 256, 128, 12, 4, 2, 16, 64, 3, 2, 1, 1, -1,
