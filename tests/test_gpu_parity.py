@@ -117,6 +117,28 @@ def test_variants_ragged(gpu, kind, variant):
             assert np.array_equal(H.raw_acc(ops, gpu, variant).cpu().numpy(), ref)
 
 
+# ---------------------------------------------------------------- int4 accumulators at the K bound
+@pytest.mark.parametrize("bval, byte", [(-8, 0x88), (7, 0x77)])
+def test_int4_accumulators_exact_at_the_k_bound(gpu, bval, byte):
+    """The int4 unpack leaves each nibble in the high half of its byte, so the int32 accumulators
+    hold 16x the dot product until an exact shift.  At the largest accepted K (131008, a half
+    last K tile) with every activation -128 and every weight -8 (16 * 1024 * K, the largest
+    positive sum, just below 2^31) or 7 (the most negative one with this activation), every raw
+    accumulator of every variant equals the closed form K * (-128) * bval."""
+    lib = _lib.load()
+    M, N, K = 16, 32, 131008
+    a = torch.full((M * K,), -128, dtype=torch.int8, device=gpu)
+    b = torch.full((N * K // 2,), byte, dtype=torch.uint8, device=gpu)   # two equal nibbles a byte
+    acc = torch.empty(M, N, dtype=torch.int32, device=gpu)
+    for v in [-1] + list(range(len(VARIANTS))):
+        _say(f"int4 K bound {VARIANTS[v] if v >= 0 else 'auto'} b={bval} {M}x{N}x{K}")
+        acc.fill_(0)
+        _lib.check(lib.flygemm_accumulators(acc.data_ptr(), a.data_ptr(), b.data_ptr(), M, N, K,
+                                            _lib.FLYGEMM_IN["int4"], v, None), "flygemm_accumulators")
+        torch.cuda.synchronize()
+        assert bool((acc == K * (-128) * bval).all()), (v, acc.min().item(), acc.max().item())
+
+
 # ---------------------------------------------------------------- row-blocked streaming kernel
 ROWS = [i for i, n in enumerate(VARIANTS) if n.startswith("rows_")]
 
