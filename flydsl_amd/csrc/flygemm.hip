@@ -357,22 +357,30 @@ KernelFn aq_kernel(int kind, bool bf16_out, int x_dtype, int mode, int v) {
 typedef void (*QuantFn)(QuantArgs);
 
 // registers-resident variant for rows of up to 1, 2, 4 or 8 slices, streaming beyond
-template <int IN, int OUT, int MODE>
+template <int IN, int OUT, int MODE, int NT>
 QuantFn quant_fn(int nslices) {
-  if (nslices <= 1) return quant_rows_kernel<IN, OUT, MODE, 1>;
-  if (nslices <= 2) return quant_rows_kernel<IN, OUT, MODE, 2>;
-  if (nslices <= 4) return quant_rows_kernel<IN, OUT, MODE, 4>;
-  if (nslices <= 8) return quant_rows_kernel<IN, OUT, MODE, 8>;
-  return quant_rows_kernel<IN, OUT, MODE, 0>;
+  if (nslices <= 1) return quant_rows_kernel<IN, OUT, MODE, 1, NT>;
+  if (nslices <= 2) return quant_rows_kernel<IN, OUT, MODE, 2, NT>;
+  if (nslices <= 4) return quant_rows_kernel<IN, OUT, MODE, 4, NT>;
+  if (nslices <= 8) return quant_rows_kernel<IN, OUT, MODE, 8, NT>;
+  return quant_rows_kernel<IN, OUT, MODE, 0, NT>;
 }
 
-template <int IN>
+template <int IN, int NT>
 QuantFn quant_fn_in(int out_dtype, int mode, int nslices) {
-  if (out_dtype == QOUT_FP8) return mode == QMODE_DIV_NEAREST ? quant_fn<IN, QOUT_FP8, QMODE_DIV_NEAREST>(nslices) : nullptr;
-  if (mode == QMODE_RECIP_TRUNC) return quant_fn<IN, QOUT_INT8, QMODE_RECIP_TRUNC>(nslices);
-  if (mode == QMODE_DIV_TRUNC) return quant_fn<IN, QOUT_INT8, QMODE_DIV_TRUNC>(nslices);
-  if (mode == QMODE_DIV_NEAREST) return quant_fn<IN, QOUT_INT8, QMODE_DIV_NEAREST>(nslices);
+  if (out_dtype == QOUT_FP8)
+    return mode == QMODE_DIV_NEAREST ? quant_fn<IN, QOUT_FP8, QMODE_DIV_NEAREST, NT>(nslices) : nullptr;
+  if (mode == QMODE_RECIP_TRUNC) return quant_fn<IN, QOUT_INT8, QMODE_RECIP_TRUNC, NT>(nslices);
+  if (mode == QMODE_DIV_TRUNC) return quant_fn<IN, QOUT_INT8, QMODE_DIV_TRUNC, NT>(nslices);
+  if (mode == QMODE_DIV_NEAREST) return quant_fn<IN, QOUT_INT8, QMODE_DIV_NEAREST, NT>(nslices);
   return nullptr;
+}
+
+template <int NT>
+QuantFn quant_fn_nt(int in_dtype, int out_dtype, int mode, int nslices) {
+  return in_dtype == FLYGEMM_QIN_F16    ? quant_fn_in<QIN_F16, NT>(out_dtype, mode, nslices)
+         : in_dtype == FLYGEMM_QIN_BF16 ? quant_fn_in<QIN_BF16, NT>(out_dtype, mode, nslices)
+                                        : quant_fn_in<QIN_F32, NT>(out_dtype, mode, nslices);
 }
 
 // K in bytes for the kernels, which take K tiles of 128 bytes and a last tile of 64 bytes
@@ -461,13 +469,13 @@ int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int3
   if (!out || !scales || !in) return fail(hipErrorInvalidValue, "null pointer");
   if (((uintptr_t)in & 15) || ((uintptr_t)out & 7) || ((uintptr_t)scales & 3))
     return fail(hipErrorInvalidValue, "misaligned pointer (input needs 16-byte, output 8-byte alignment)");
-  const int nslices = (N + kQuantSlice - 1) / kQuantSlice;
-  QuantFn fn = in_dtype == FLYGEMM_QIN_F16    ? quant_fn_in<QIN_F16>(out_dtype, mode, nslices)
-               : in_dtype == FLYGEMM_QIN_BF16 ? quant_fn_in<QIN_BF16>(out_dtype, mode, nslices)
-                                              : quant_fn_in<QIN_F32>(out_dtype, mode, nslices);
+  const int nt = N >= kQuantWideN ? 2 * kQuantThreads : kQuantThreads;
+  const int nslices = (N + nt * 8 - 1) / (nt * 8);
+  QuantFn fn = nt == kQuantThreads ? quant_fn_nt<kQuantThreads>(in_dtype, out_dtype, mode, nslices)
+                                   : quant_fn_nt<2 * kQuantThreads>(in_dtype, out_dtype, mode, nslices);
   if (!fn) return fail(hipErrorInvalidValue, "unsupported quant combination");
   QuantArgs args{out, scales, in, M, N};
-  hipLaunchKernelGGL(fn, dim3(M), dim3(kQuantThreads), 0, (hipStream_t)stream, args);
+  hipLaunchKernelGGL(fn, dim3(M), dim3(nt), 0, (hipStream_t)stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of quant_rows failed: %s", hipGetErrorString(e));
   return 0;

@@ -14,10 +14,10 @@
 //    rounds half to even instead (and clamps to +-127), the int8 rule of the benchmark
 //    workloads.  fp8 (e4m3fn) always rounds to nearest even, as torch's cast does.
 //
-// One workgroup (256 threads) per row.  Each thread owns 8 consecutive elements per
-// 2048-element slice of the row; rows of up to VPT slices stay in registers between the
-// max pass and the quantize pass, so HBM is read once (VPT == 0: streaming variant for
-// long rows, which re-reads the row from L2).  Loads (16-byte vectors) and stores (8 bytes)
+// One workgroup (NT = 256 threads, 512 for rows of 8192 elements or more) per row.  Each
+// thread owns 8 consecutive elements per (8 * NT)-element slice of the row; rows of up to VPT
+// slices stay in registers between the max pass and the quantize pass, so HBM is read once
+// (VPT == 0: streaming variant for long rows, which re-reads the row from L2).  Loads (16-byte vectors) and stores (8 bytes)
 // are non-temporal; consecutive lanes touch consecutive addresses in every instruction.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -37,7 +37,9 @@ struct QuantArgs {
 };
 
 constexpr int kQuantThreads = 256;
-constexpr int kQuantSlice = kQuantThreads * 8;  // elements per workgroup pass
+// rows of at least this many elements take 512 threads (Q, 4096x8192 fp16 -> int8, on MI355X:
+// 18.3 us against 18.7 with 256; 1024 threads 20.5)
+constexpr int kQuantWideN = 8192;
 
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef int i32x2q __attribute__((ext_vector_type(2)));
@@ -153,8 +155,9 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-template <int IN, int OUT, int MODE, int VPT>
-__global__ void __launch_bounds__(kQuantThreads) quant_rows_kernel(QuantArgs p) {
+template <int IN, int OUT, int MODE, int VPT, int NT>
+__global__ void __launch_bounds__(NT) quant_rows_kernel(QuantArgs p) {
+  constexpr int kQuantSlice = NT * 8;  // elements per workgroup pass
   constexpr int ESZ = (IN == QIN_F32) ? 4 : 2;
   constexpr float QMAX = (OUT == QOUT_FP8) ? 448.f : 127.f;
   const int row = blockIdx.x;
@@ -182,13 +185,13 @@ __global__ void __launch_bounds__(kQuantThreads) quant_rows_kernel(QuantArgs p) 
       if (col < N) m = __builtin_fmaxf(m, absmax8(load8_prepared<IN, MODE>(rin, col, QMAX)));
     }
   }
-  __shared__ float red[kQuantThreads / 64];
+  __shared__ float red[NT / 64];
   m = wave_max(m);
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   m = red[0];
 #pragma unroll
-  for (int w = 1; w < kQuantThreads / 64; ++w) m = __builtin_fmaxf(m, red[w]);
+  for (int w = 1; w < NT / 64; ++w) m = __builtin_fmaxf(m, red[w]);
 
   float scale = m / QMAX;
   if (scale == 0.f) scale = 1.f;
