@@ -110,6 +110,10 @@ constexpr int kFirstRows = kFirstDecode DECODE_SHAPES(COUNT);
 constexpr long kRowsMaxTiles = 64;
 constexpr long kRowsMaxTiles16 = 96;
 constexpr long kSmallMaxTiles = 144;
+// Blockscale keeps 64x64 tiles up to 272 tiles of 64x128 (graph-timed on MI355X, 64x64 against
+// 64x128: 1024x2112x7168 38.9 us against 42.7, 512x4096x7168 32.5 against 35.0, 256x7168x7168
+// 35.6 against 36.4; at 448 tiles, 512x7168x2304, 19.9 against 17.2).
+constexpr long kSmallMaxTilesBlock = 272;
 
 // One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
@@ -229,11 +233,15 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     if (epi == EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && N % 256 != 0) continue;
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg || wg > list[i].max_wg) continue;
+    // blockscale 256x256 tiles between one and two per CU: the second round runs half empty
+    // behind the slow blockscale tile (1024x24576x1536, 384 tiles: 62.6 us against 50.4 for
+    // 256x128; at 768 tiles, 2048x24576x1536, 94.6 against 99.1)
+    if (epi == EPI_BLOCK && list[i].bm == 256 && list[i].bn == 256 && wg > 256 && wg < 512) continue;
     // the last resort (64x128) leaves CUs idle with few tiles: the row-blocked streaming kernel
     // or 64x64 tiles spread the output over more CUs instead
     const long rows_max = (epi == EPI_BLOCK || kind == KIND_FP4) ? kRowsMaxTiles16 : kRowsMaxTiles;
     if (list[i].min_wg == 0 && wg <= rows_max) return select_rows(kind, epi);
-    if (list[i].min_wg == 0 && wg <= kSmallMaxTiles && kind != KIND_FP4)
+    if (list[i].min_wg == 0 && wg <= (epi == EPI_BLOCK ? kSmallMaxTilesBlock : kSmallMaxTiles) && kind != KIND_FP4)
       for (int v = 0; v < kFirstDecode; ++v)
         if (kShapes[v].bm == 64 && kShapes[v].bn == 64) return v;
     for (int v = 0; v < kFirstDecode; ++v)
