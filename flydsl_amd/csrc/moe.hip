@@ -23,7 +23,8 @@ namespace {
 
 template <int KIND, bool BS>
 MoeFn moe_stage1_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, WM_, WN_, NS_) \
+#define T(M_, R_, N_, WM_, WN_, NS_)                                                                        \
+  static_assert(WM_ * WN_ * 64 == (R_ > 1 ? 512 : 256), "moe_launch gives run tiles 8 waves, others 4"); \
   if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS, NS_>;
   T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
   T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)

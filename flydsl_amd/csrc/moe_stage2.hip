@@ -9,7 +9,8 @@ namespace flygemm {
 namespace {
 template <int KIND, bool F32, bool BS>
 MoeFn stage2_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, WM_, WN_) \
+#define T(M_, R_, N_, WM_, WN_)                                                                            \
+  static_assert(WM_ * WN_ * 64 == (R_ > 1 ? 512 : 256), "moe_launch gives run tiles 8 waves, others 4"); \
   if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, WM_, WN_, F32, BS>;
   // single-block tiles of 64 and 128 columns: the launcher never gives stage 2 single-block
   // tiles of 256 columns (it narrows them to 128 or 64)
