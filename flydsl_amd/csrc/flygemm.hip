@@ -231,6 +231,13 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   for (int i = 0; i < n; ++i) {
     if (kind == KIND_INT4 && !list[i].int4) continue;
     if (epi == EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && N % 256 != 0) continue;
+    // one 128x256 tile per CU needs long K to amortise its fill and epilogue: below 32 K tiles
+    // (4096 bytes) 128x128 is faster (fp8 1024x7168 with K = 1536 / 2048 / 3072: 15.1 / 18.2 /
+    // 24.7 us against 16.1 / 19.2 / 25.7; int8 K = 2048 19.2 against 20.0; bf16 K = 1024 18.2
+    // against 19.3; from K = 4096 bytes 128x256 wins: fp8 32.8 against 35.7, bf16 K = 2048
+    // 34.3 against 36.6).  Not for MXFP4, whose K bytes hold two elements (7168 elements,
+    // 3584 bytes: 34.7 us against 36.1 for 128x128).
+    if (epi != EPI_BLOCK && kind != KIND_FP4 && list[i].bm == 128 && list[i].bn == 256 && K < 4096) continue;
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg || wg > list[i].max_wg) continue;
     // blockscale 256x256 tiles between one and two per CU: the second round runs half empty

@@ -77,8 +77,14 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(1536, 8192, 8192, 0, 0)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(512, 28672, 8192, 0, 0)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(1024, 8192, 8192, 0, 0)] == "main_128x256_w2x4"
-    # 128x128 once it gives more than one tile per CU
+    # 128x128 once it gives more than one tile per CU, or for K below 4096 bytes (not MXFP4)
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 0, 0)] == "main_128x256_w2x4"
+    assert names[lib.flygemm_select_variant(1024, 7168, 4096, 0, 0)] == "main_128x256_w2x4"
+    assert names[lib.flygemm_select_variant(1024, 7168, 2048, 0, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 7168, 3072, 1, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 7168, 2048, 3, 0)] == "main_128x256_w2x4"   # 4096 bytes
+    assert names[lib.flygemm_select_variant(1024, 7168, 1024, 3, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 7168, 7168, 5, 0)] == "main_128x256_w2x4"   # MXFP4
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 2, 0)] == "main_128x128_w2x2"  # int4: no 128x256
     assert names[lib.flygemm_select_variant(1280, 7168, 7168, 0, 0)] == "main_128x128_w2x2"  # 280 tiles of 128x256
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
