@@ -114,6 +114,7 @@ constexpr long kSmallMaxTiles = 144;
 // 64x128: 1024x2112x7168 38.9 us against 42.7, 512x4096x7168 32.5 against 35.0, 256x7168x7168
 // 35.6 against 36.4; at 448 tiles, 512x7168x2304, 19.9 against 17.2).
 constexpr long kSmallMaxTilesBlock = 272;
+constexpr long kMidMaxTiles = 256;
 
 // One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
@@ -251,6 +252,15 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     if (list[i].min_wg == 0 && wg <= (epi == EPI_BLOCK ? kSmallMaxTilesBlock : kSmallMaxTiles) && kind != KIND_FP4)
       for (int v = 0; v < kFirstDecode; ++v)
         if (kShapes[v].bm == 64 && kShapes[v].bn == 64) return v;
+    // up to 256 such tiles and at least 384 rows: the same number of 128x64 tiles (graph-timed,
+    // against 64x128: fp8 512x4096x7168 26.5 us against 27.7, 512x3072x7168 25.6 against 26.9,
+    // 512x2560x8192 28.8 against 30.1, 384x5120x7168 27.3 against 28.0, 768x2112x4096 16.5
+    // against 17.1, int8 512x4096x4096 16.7 against 17.3, bf16 30.6 against 31.5; at 256 rows
+    // level or up to 2% slower; int4 10% slower), not for blockscale nor MXFP4
+    if (list[i].min_wg == 0 && wg <= kMidMaxTiles && M >= 384 && epi != EPI_BLOCK && kind != KIND_INT4 &&
+        kind != KIND_FP4 && (long)((M + 127) / 128) * ((N + 63) / 64) <= wg)
+      for (int v = 0; v < kFirstDecode; ++v)
+        if (kShapes[v].bm == 128 && kShapes[v].bn == 64) return v;
     for (int v = 0; v < kFirstDecode; ++v)
       if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }

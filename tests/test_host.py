@@ -88,6 +88,13 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 2, 0)] == "main_128x128_w2x2"  # int4: no 128x256
     assert names[lib.flygemm_select_variant(1280, 7168, 7168, 0, 0)] == "main_128x128_w2x2"  # 280 tiles of 128x256
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
+    # 145-256 tiles of 64x128 and at least 384 rows: 128x64 tiles (not int4, MXFP4, blockscale)
+    assert names[lib.flygemm_select_variant(512, 4096, 7168, 0, 0)] == "main_128x64_w2x2"
+    assert names[lib.flygemm_select_variant(384, 5120, 7168, 1, 0)] == "main_128x64_w2x2"
+    assert names[lib.flygemm_select_variant(512, 4096, 4096, 3, 0)] == "main_128x64_w2x2"
+    assert names[lib.flygemm_select_variant(512, 4096, 4096, 2, 0)] == "main_64x128_w1x4"   # int4
+    assert names[lib.flygemm_select_variant(320, 4096, 4096, 0, 0)] == "main_64x128_w1x4"   # ragged 128-row tiles
+    assert names[lib.flygemm_select_variant(768, 4096, 4096, 0, 0)] == "main_64x128_w1x4"   # 384 tiles
     # the row-blocked kernel where the 64x128 tiles leave CUs idle (at most 64 tiles; 96 with
     # the 16-row blocks of blockscale and MXFP4)
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 0, 0)] == "rows_m2_nb4_w8_u3"
