@@ -259,20 +259,31 @@ def roofline(w: workloads.Workload, ms_per_launch: float, bound: str, traffic=No
 
 def cpu_baseline(w: workloads.Workload):
     """The reference's CPU path for this GEMM, timed on the host: dequantize A and B to fp32
-    with their per-row scales, ``torch.mm`` in fp32 on all host cores, cast to bf16
-    (``run_torch``, reference tests/kernels/test_preshuffle_gemm.py:55-65), on the full call of
-    the workload's seeded operands; 1 warm-up, median of 3.  The
-    oracle's numpy float32 restatement of the same path is timed once as a second figure."""
+    with their scales, ``torch.mm`` in fp32 on all host cores, cast to bf16 (``run_torch``,
+    reference tests/kernels/test_preshuffle_gemm.py:55-65; blockscale: the 1x128 / 128x128
+    scale expansion of ``run_torch_blockscale``, test_blockscale_preshuffle_gemm.py:86-109;
+    bf16/fp16: no scales), on the full call of the workload's seeded operands; 1 warm-up,
+    median of 3.  The oracle's numpy float32 restatement of the same
+    path is timed once as a second figure.  MXFP4 has no CPU baseline here (its e2m1 bytes
+    are not a torch dtype)."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import gemm as og
 
+    if w.kind not in ("fp8", "int8", "int4", "fp8_block", "bf16", "fp16"):
+        raise ValueError(f"no CPU baseline for kind {w.kind!r}")
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     ops = workloads.make_operands(w)
     a_q, b_q = ops["a"], ops["b"]
-    sa, sb = ops["sa"].reshape(-1, 1).float(), ops["sb"].reshape(-1, 1).float()
+    if w.kind == "fp8_block":
+        sa = ops["sa"].float().repeat_interleave(128, dim=1)[:, : w.K]
+        sb = ops["sb"].float().repeat_interleave(128, dim=0).repeat_interleave(128, dim=1)[: w.N, : w.K]
+    elif w.kind in ("bf16", "fp16"):
+        sa = sb = torch.ones(1, 1)
+    else:
+        sa, sb = ops["sa"].reshape(-1, 1).float(), ops["sb"].reshape(-1, 1).float()
 
     def run_torch():
         a = a_q.to(torch.float32) * sa
@@ -286,12 +297,21 @@ def cpu_baseline(w: workloads.Workload):
         run_torch()
         times.append(time.perf_counter() - t0)
     t = sorted(times)[1]
-    a = a_q.view(torch.uint8).numpy() if a_q.dtype != torch.int8 else a_q.numpy()
-    b = b_q.view(torch.uint8).numpy() if b_q.dtype != torch.int8 else b_q.numpy()
-    kind = "fp8" if w.kind in ("fp8", "fp8_block") else "int8"
+
+    def raw(x):
+        if x.dtype in (torch.bfloat16, torch.float16):
+            return x.view(torch.int16).numpy().view(np.uint16)
+        return x.view(torch.uint8).numpy() if x.dtype != torch.int8 else x.numpy()
+
     with threadpool_limits(limits=cores):
         t0 = time.perf_counter()
-        og.run_torch(a, b, sa.numpy().reshape(-1), sb.numpy().reshape(-1), kind)
+        if w.kind == "fp8_block":
+            og.run_torch_blockscale(raw(a_q), raw(b_q), ops["sa"].numpy(), ops["sb"].numpy())
+        elif w.kind in ("bf16", "fp16"):
+            og.run_torch(raw(a_q), raw(b_q), None, None, w.kind)
+        else:
+            og.run_torch(raw(a_q), raw(b_q), ops["sa"].numpy().reshape(-1), ops["sb"].numpy().reshape(-1),
+                         "fp8" if w.kind == "fp8" else "int8")
         t_np = time.perf_counter() - t0
     return {"value": round(w.bytes / t / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"full {w.name} call ({w.M}x{w.N}x{w.K}): dequantize to fp32, torch.mm fp32 on {cores} threads, "
@@ -320,6 +340,95 @@ def traffic_from_profile(name: str):
         if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
             return int(parts[2])
     return None
+
+
+def gfx_clock_under(work, seconds=0.4):
+    """Median graphics clock (MHz) that amdsmi reports while ``work`` runs back to back for
+    ``seconds`` (None if amdsmi is unavailable)."""
+    import threading
+    try:
+        import amdsmi
+        amdsmi.amdsmi_init()
+        h = amdsmi.amdsmi_get_processor_handles()[0]
+    except Exception as e:  # no amdsmi or no permission: the line goes without a clock
+        log(f"[bench] no clock reading: {type(e).__name__}: {str(e)[:100]}")
+        return None
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            try:
+                samples.append(float(amdsmi.amdsmi_get_clock_info(h, amdsmi.AmdSmiClkType.GFX)["clk"]))
+            except Exception:
+                pass
+            time.sleep(0.005)
+
+    t = threading.Thread(target=sample)
+    t0 = time.perf_counter()
+    work()
+    t.start()
+    while time.perf_counter() - t0 < seconds:
+        work()
+    stop.set()
+    t.join()
+    try:
+        amdsmi.amdsmi_shut_down()
+    except Exception:
+        pass
+    if not samples:
+        return None
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def dispatch_cost(dev, calls=1000):
+    """Host cost of one eager call (microseconds), on a 1x64x128 fp8 GEMM: the validating
+    launcher, the pre-bound callable of ``flydsl_amd.compile`` and the bare ctypes call; and C1
+    timed eagerly through the pre-bound callable (HIP events around 200 back-to-back launches)
+    against its graph-replay time."""
+    import flydsl_amd
+
+    def host_us(fn):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        t = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        return round(t / calls * 1e6, 2)
+
+    w = workloads.custom("fp8", 1, 64, 128, seed=0)
+    ops = workloads.make_operands(w)
+    a, b = _dev_flat(ops["a"], dev), _dev_flat(ops["b_dev"], dev)
+    sa, sb = ops["sa"].to(dev).view(-1), ops["sb"].to(dev).view(-1)
+    c = torch.empty(w.M * w.N, dtype=torch.bfloat16, device=dev)
+    fn = compile_preshuffle_gemm_a8(K=w.K, tile_m=16, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
+    s = torch.cuda.current_stream()
+    h = s.cuda_stream
+    cf = flydsl_amd.compile(fn, c, a, b, sa, sb, w.M, w.N, h)
+    lib = _lib.load()
+    pc, pa, pb, psa, psb = c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr()
+    out = {"shape": f"fp8 {w.M}x{w.N}x{w.K}", "calls": calls,
+           "launcher_us": host_us(lambda: fn(c, a, b, sa, sb, w.M, w.N, s)),
+           "compiled_us": host_us(lambda: cf(c, a, b, sa, sb, w.M, w.N, h)),
+           "ctypes_us": host_us(lambda: lib.flygemm_preshuffle(pc, pa, pb, psa, psb, w.M, w.N, w.K, 0, 0, -1, h))}
+    r = Runner(workloads.WORKLOADS["C1"], dev)
+    cc = flydsl_amd.compile(r.fn, r.c.view(-1), r.a[0], r.b[0], r.sa, r.sb, r.w.M, r.w.N, h)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 200
+    for i in range(20):
+        cc(r.c.view(-1), r.a[i % r.copies], r.b[i % r.copies], r.sa, r.sb, r.w.M, r.w.N, h)
+    torch.cuda.synchronize()
+    ev0.record(s)
+    for i in range(n):
+        cc(r.c.view(-1), r.a[i % r.copies], r.b[i % r.copies], r.sa, r.sb, r.w.M, r.w.N, h)
+    ev1.record(s)
+    torch.cuda.synchronize()
+    out["C1_eager_ms"] = round(ev0.elapsed_time(ev1) / n, 5)
+    out["C1_graph_ms"] = round(r.time(50, 2, graph=True)[0], 5)
+    return out
 
 
 def launches_only(name: str, n: int):
@@ -397,12 +506,13 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="C2")
-    ap.add_argument("--secondary", default="C1,C3,C4,C5,T,Q",
+    ap.add_argument("--secondary", default="C1,C3,C4,C5,T,Q,G1,G2,G3,G4,G5,G6,G7",
                     help="extra workloads, comma separated ('' to skip)")
     ap.add_argument("--secondary-launches", type=int, default=50,
                     help="launches per timed graph replay of each secondary workload")
     ap.add_argument("--all", action="store_true", help="also time every configuration")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-dispatch", action="store_true", help="skip the host dispatch-cost line")
     ap.add_argument("--launches-only", default="", help="profiling: only launch this workload --n times")
     ap.add_argument("--n", type=int, default=20)
     ap.add_argument("--copy-bytes", type=int, default=0, help="profiling: copy this many bytes on the GPU")
@@ -460,16 +570,30 @@ def main():
         log(f"[bench] timing {name} variant={r2.variant}")
         n2 = max(50, args.secondary_launches)
         ms2, _ = r2.time(n2, max(2, args.warmup // 2), graph=True)
-        b2 = "hbm" if name in ("C1", "C2", "Q", "MD1", "MD2", "MD2R", "MB1", "MB2") else "mfma"
+        b2 = "hbm" if name in ("C1", "C2", "G1", "G2", "Q", "MD1", "MD2", "MD2R", "MB1", "MB2") else "mfma"
         sec[name] = {"ms": round(ms2, 5), "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
                      "timing": f"HIP graph of {n2} launches, median of 3 timed replays after >= 0.1 s of untimed ones",
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
         if w2.flops:
             sec[name]["TFLOP/s"] = round(w2.flops / ms2 / 1e9, 1)
+        if name == "T":
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cap = torch.cuda.current_stream()
+                for i in range(n2):
+                    r2.launch(i, cap)
+            clk = gfx_clock_under(lambda: (g.replay(), torch.cuda.synchronize()))
+            del g
+            if clk:
+                # the dense peak assumes 2.4 GHz; under sustained MFMA load the chip holds less
+                sec[name]["clock_mhz"] = clk
+                sec[name]["frac_at_clock"] = round(sec[name]["roofline"]["frac"] * 2400.0 / clk, 4)
         del r2
         torch.cuda.empty_cache()
     if sec:
         result["secondary"] = sec
+    if not args.no_dispatch:
+        result["dispatch"] = dispatch_cost(dev)
     if not args.no_cpu:
         log("[bench] CPU baseline")
         result["cpu_baseline"] = cpu_baseline(w)

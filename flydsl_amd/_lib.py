@@ -38,6 +38,7 @@ SIGNATURES = [
     ("flygemm_num_variants", ctypes.c_int32, []),
     ("flygemm_variant_name", ctypes.c_char_p, [_I]),
     ("flygemm_select_variant", ctypes.c_int32, [_I, _I, _I, _I, _I]),
+    ("flygemm_launch_shape", ctypes.c_int, [_I] * 6 + [_P] * 4),
     ("flygemm_last_error", ctypes.c_char_p, []),
 ]
 

@@ -308,32 +308,46 @@ int check_common(const void* c, const void* a, const void* b, int M, int N, int 
   return 0;
 }
 
-// variant: -1 = the library's choice, else the index of a variant in the table.
+// The kernel, grid and work items of one call (M > 0): variant -1 = the library's choice, else
+// the index of a variant in the table.
+struct Plan {
+  int v;
+  KernelFn fn;
+  int grid, threads;
+  long items;
+};
+
+int plan_launch(int kind, int epi, int out_dtype, int variant, int M, int N, int K, Plan* pl) {
+  const int v = variant >= 0 ? variant : select_variant(M, N, K, kind, epi);
+  if (v < 0 || v >= kNumShapes) return fail(hipErrorInvalidValue, "no kernel variant for M=%d N=%d K=%d", M, N, K);
+  const Shape& s = kShapes[v];
+  const KernelFn* row = kernel_row(kind, epi, out_dtype);
+  if (!row) return fail(hipErrorInvalidValue, "unsupported combination kind=%d epilogue=%d", kind, epi);
+  pl->v = v;
+  pl->fn = row[v];
+  pl->threads = s.threads;
+  if (s.family == FAM_MAIN) {
+    pl->items = (long)((M + s.bm - 1) / s.bm) * ((N + s.bn - 1) / s.bn);
+    return persistent_grid(row[v], s.threads, pl->items, &pl->grid);
+  }
+  // one workgroup per (row block, column group); a decode shape normally has one row block
+  const long nrb = (M + s.bm - 1) / s.bm;
+  const long ncg = (N / 16 + s.bn / 16 - 1) / (s.bn / 16);
+  pl->items = nrb * ncg;
+  pl->grid = (int)pl->items;
+  return 0;
+}
+
 int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, hipStream_t stream) {
   if (kind == KIND_INT4 && args.K >= kInt4KLimit)
     return fail(hipErrorInvalidValue, "K=%d: int4 weights take K < %d (int32 accumulators of 16x the dot product)",
                 args.K, kInt4KLimit);
   if (args.M == 0) return 0;
-  const int v = variant >= 0 ? variant : select_variant(args.M, args.N, args.K, kind, epi);
-  if (v < 0 || v >= kNumShapes)
-    return fail(hipErrorInvalidValue, "no kernel variant for M=%d N=%d K=%d", args.M, args.N, args.K);
-  const Shape& s = kShapes[v];
-  const KernelFn* row = kernel_row(kind, epi, out_dtype);
-  if (!row) return fail(hipErrorInvalidValue, "unsupported combination kind=%d epilogue=%d", kind, epi);
-  dim3 grid;
-  if (s.family == FAM_MAIN) {
-    const long ntiles = (long)((args.M + s.bm - 1) / s.bm) * ((args.N + s.bn - 1) / s.bn);
-    int g = 0;
-    int rc = persistent_grid(row[v], s.threads, ntiles, &g);
-    if (rc) return rc;
-    grid = dim3(g);
-  } else {
-    // one workgroup per (row block, column group); a decode shape normally has one row block
-    const long nrb = (args.M + s.bm - 1) / s.bm;
-    const long ncg = (args.N / 16 + s.bn / 16 - 1) / (s.bn / 16);
-    grid = dim3((unsigned)(nrb * ncg));
-  }
-  hipLaunchKernelGGL(row[v], grid, dim3(s.threads), 0, stream, args);
+  Plan pl;
+  int rc = plan_launch(kind, epi, out_dtype, variant, args.M, args.N, args.K, &pl);
+  if (rc) return rc;
+  const Shape& s = kShapes[pl.v];
+  hipLaunchKernelGGL(pl.fn, dim3(pl.grid), dim3(pl.threads), 0, stream, args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of %s failed: %s", s.name, hipGetErrorString(e));
   return 0;
@@ -532,6 +546,9 @@ int flygemm_preshuffle_quant_a(void* c, void* a_q, float* scale_a, const void* x
     return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
   if (M > 0 && !scale_b) return fail(hipErrorInvalidValue, "null scale pointer");
   if (M == 0) return 0;
+  // the same alignment on both paths below: 16-byte activation loads, 8-byte code stores
+  if (((uintptr_t)x & 15) || ((uintptr_t)a_q & 7) || ((uintptr_t)scale_a & 3))
+    return fail(hipErrorInvalidValue, "misaligned pointer (x needs 16-byte, a_q 8-byte, scale_a 4-byte alignment)");
   const int qout = in_dtype == FLYGEMM_IN_FP8 ? FLYGEMM_QOUT_FP8 : FLYGEMM_QOUT_INT8;
   const int v = variant >= 0 ? variant : select_variant(M, N, kb, in_dtype, EPI_ROWCOL);
   if (v < 0 || v >= kNumShapes) return fail(hipErrorInvalidValue, "no kernel variant for M=%d N=%d K=%d", M, N, K);
@@ -594,6 +611,25 @@ int32_t flygemm_select_variant(int32_t M, int32_t N, int32_t K, int32_t in_dtype
   // the kernels count K in bytes: two per element for 16-bit inputs, half for MXFP4
   const int kb = (in_dtype == FLYGEMM_IN_BF16 || in_dtype == FLYGEMM_IN_FP16) ? 2 * K : (in_dtype == FLYGEMM_IN_FP4 ? K / 2 : K);
   return select_variant(M, N, kb, in_dtype, blockscale ? EPI_BLOCK : EPI_ROWCOL);
+}
+
+int flygemm_launch_shape(int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t blockscale, int32_t variant,
+                         int32_t* variant_out, int32_t* grid, int32_t* threads, int32_t* items) {
+  if (in_dtype < FLYGEMM_IN_FP8 || in_dtype > FLYGEMM_IN_FP4)
+    return fail(hipErrorInvalidValue, "in_dtype %d not supported", in_dtype);
+  if (blockscale && in_dtype != FLYGEMM_IN_FP8) return fail(hipErrorInvalidValue, "blockscale takes fp8 inputs");
+  if (M <= 0 || N <= 0 || K <= 0) return fail(hipErrorInvalidValue, "invalid sizes M=%d N=%d K=%d", M, N, K);
+  if (variant < -1 || variant >= kNumShapes) return fail(hipErrorInvalidValue, "unknown variant %d", variant);
+  if (!variant_out || !grid || !threads || !items) return fail(hipErrorInvalidValue, "null output pointer");
+  const int kb = (in_dtype == FLYGEMM_IN_BF16 || in_dtype == FLYGEMM_IN_FP16) ? 2 * K : (in_dtype == FLYGEMM_IN_FP4 ? K / 2 : K);
+  Plan pl;
+  const int rc = plan_launch(in_dtype, blockscale ? EPI_BLOCK : EPI_ROWCOL, FLYGEMM_OUT_BF16, variant, M, N, kb, &pl);
+  if (rc) return rc;
+  *variant_out = pl.v;
+  *grid = pl.grid;
+  *threads = pl.threads;
+  *items = (int32_t)pl.items;
+  return 0;
 }
 
 const char* flygemm_last_error(void) { return g_err; }

@@ -85,6 +85,11 @@ __device__ __forceinline__ i32x4 int4x8_to_bf16(uint32_t p, float s, bool scaled
 // route's row out[token*topk + slot] with plain stores (the reduce mode, summed by
 // moe_reduce_kernel afterwards).  Stage 1 takes F16 or BF16.
 typedef void (*MoeFn)(MoeArgs);
+// A kernel of the tables and the workgroup size it was instantiated for (its waves x 64).
+struct MoeKernel {
+  MoeFn fn;
+  int threads;
+};
 
 enum MoeOut : int { MOE_OUT_F16 = 0, MOE_OUT_BF16 = 1, MOE_OUT_F32 = 2, MOE_OUT_F16_ROWS = 3, MOE_OUT_BF16_ROWS = 4 };
 constexpr bool moe_out_bf16(int o) { return o == MOE_OUT_BF16 || o == MOE_OUT_BF16_ROWS; }

@@ -16,16 +16,16 @@ using namespace flygemm;
 // runs of 128 rows (stage 1, 128 columns) and, for 16-row blocks, of 256 rows (stage 2, 256
 // columns) with 8 waves.
 namespace flygemm {
-MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
+MoeKernel moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
 }
 
 namespace {
 
 template <int KIND, bool BS>
-MoeFn moe_stage1_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, WM_, WN_, NS_)                                                                        \
-  static_assert(WM_ * WN_ * 64 == (R_ > 1 ? 512 : 256), "moe_launch gives run tiles 8 waves, others 4"); \
-  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS, NS_>;
+MoeKernel moe_stage1_tile(int tm, int r, int tn) {
+#define T(M_, R_, N_, WM_, WN_, NS_) \
+  if (tm == M_ && r == R_ && tn == N_)  \
+    return MoeKernel{moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS, NS_>, WM_ * WN_ * 64};
   T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
   T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)
   T(64, 1, 256, 1, 4, 2)
@@ -35,11 +35,11 @@ MoeFn moe_stage1_tile(int tm, int r, int tn) {
     T(16, 8, 128, 2, 4, 3) T(32, 4, 128, 2, 4, 3) T(64, 2, 128, 2, 4, 3)
   }
 #undef T
-  return nullptr;
+  return MoeKernel{nullptr, 0};
 }
 
-MoeFn moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
-  if (bs) return kind == KIND_FP8 ? moe_stage1_tile<KIND_FP8, true>(tm, r, tn) : nullptr;
+MoeKernel moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
+  if (bs) return kind == KIND_FP8 ? moe_stage1_tile<KIND_FP8, true>(tm, r, tn) : MoeKernel{nullptr, 0};
   switch (kind) {
     case KIND_FP8: return moe_stage1_tile<KIND_FP8, false>(tm, r, tn);
     case KIND_INT8: return moe_stage1_tile<KIND_INT8, false>(tm, r, tn);
@@ -47,7 +47,7 @@ MoeFn moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
     case KIND_W4A16: return moe_stage1_tile<KIND_W4A16, false>(tm, r, tn);
     case KIND_BF16: return moe_stage1_tile<KIND_BF16, false>(tm, r, tn);
     case KIND_F16: return moe_stage1_tile<KIND_F16, false>(tm, r, tn);
-    default: return nullptr;
+    default: return MoeKernel{nullptr, 0};
   }
 }
 
@@ -140,11 +140,19 @@ int moe_kind(int in_dtype, int stage, bool* token_slot) {
   }
 }
 
-int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
-               const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
-               const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
-               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, bool bs, int group_size,
-               hipStream_t stream) {
+// A validated MoE GEMM launch; kernel null when there is nothing to launch (no tokens or blocks).
+struct MoePlan {
+  MoeKernel kernel;
+  long grid;
+  MoeArgs args;
+};
+
+// Every check of a MoE GEMM call and its launch parameters, without launching anything.
+int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
+             const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w, const int32_t* num_valid,
+             int tokens, int N, int K, int blocks, int experts, int topk, int tile_m, int tile_n, int in_dtype,
+             int out_dtype, int doweight, int accumulate, bool bs, int group_size, MoePlan* pl) {
+  pl->kernel = MoeKernel{nullptr, 0};
   const char* what = bs ? (stage == 1 ? "moe_blockscale_gemm1" : "moe_blockscale_gemm2")
                         : (stage == 1 ? "moe_gemm1" : "moe_gemm2");
   if (tokens < 0 || N <= 0 || K <= 0 || blocks < 0 || experts <= 0)
@@ -202,9 +210,9 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   if (bs && (2L * N) % (stage == 1 ? 128 : 256) != 0)
     return fail(hipErrorInvalidValue, "%s: %s=%d must be a multiple of 128 (weight scale blocks)", what,
                 stage == 1 ? "2*inter_dim" : "model_dim", stage == 1 ? 2 * N : N);
-  MoeFn fn = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n, bs)
-                        : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
-  if (!fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
+  const MoeKernel k = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n, bs)
+                                 : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
+  if (!k.fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
 
   // column ranges per run: about 1024 workgroups in all
   const long ntn = N / tile_n;
@@ -220,11 +228,32 @@ int moe_launch(int stage, void* out, const void* a, const void* w, const float* 
   // those that do not start a run exit at once)
   const long g = (nsplit * blocks + 7) / 8 * 8;
   if (g >= (1L << 31)) return fail(hipErrorInvalidValue, "%s: grid too large", what);
-  // the run kernels (R > 1) have 8 waves, the others 4
-  hipLaunchKernelGGL(fn, dim3((unsigned)g), dim3(R > 1 ? 512 : 256), 0, stream, args);
+  pl->kernel = k;
+  pl->grid = g;
+  pl->args = args;
+  return 0;
+}
+
+int moe_run(const MoePlan& pl, const char* what, hipStream_t stream) {
+  if (!pl.kernel.fn) return 0;
+  hipLaunchKernelGGL(pl.kernel.fn, dim3((unsigned)pl.grid), dim3(pl.kernel.threads), 0, stream, pl.args);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(e, "launch of %s failed: %s", what, hipGetErrorString(e));
   return 0;
+}
+
+int moe_launch(int stage, void* out, const void* a, const void* w, const float* sa, const float* sw,
+               const int32_t* sorted_ids, const int32_t* expert_ids, const float* sorted_w,
+               const int32_t* num_valid, int tokens, int N, int K, int blocks, int experts, int topk, int tile_m,
+               int tile_n, int in_dtype, int out_dtype, int doweight, int accumulate, bool bs, int group_size,
+               hipStream_t stream) {
+  MoePlan pl;
+  if (int rc = moe_plan(stage, out, a, w, sa, sw, sorted_ids, expert_ids, sorted_w, num_valid, tokens, N, K, blocks,
+                        experts, topk, tile_m, tile_n, in_dtype, out_dtype, doweight, accumulate, bs, group_size, &pl))
+    return rc;
+  return moe_run(pl, bs ? (stage == 1 ? "moe_blockscale_gemm1" : "moe_blockscale_gemm2")
+                        : (stage == 1 ? "moe_gemm1" : "moe_gemm2"),
+                 stream);
 }
 
 // Per-route rows of flygemm_moe_gemm2_reduce_noalloc: a device array of the library's own, so
@@ -239,14 +268,24 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device, resolved once per device.
-int noalloc_scratch(void** out, const char* what) {
+// Device address of `scratch` on the current device, resolved once per device.  The first
+// resolution on a device must not happen while `stream` is being captured into a graph (the
+// symbol lookup is not a stream operation and may invalidate the capture): that call fails
+// with a message instead.
+int noalloc_scratch(void** out, const char* what, hipStream_t stream) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(e, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
   if (dev < 0 || dev >= kMaxDevices) return fail(hipErrorInvalidDevice, "%s: device %d out of range", what, dev);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return fail(e, "%s: hipStreamIsCapturing failed: %s", what, hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(hipErrorStreamCaptureUnsupported,
+                  "%s: the first call on device %d is under graph capture; make one eager call on this device "
+                  "first (it resolves the scratch address)", what, dev);
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !ptr)
@@ -388,9 +427,20 @@ int flygemm_moe_gemm2_reduce_noalloc(void* out, const void* a2, const void* w, c
     return fail(hipErrorInvalidValue, "%s: tokens*topk*model_dim*2 = %ld bytes exceeds the static scratch of %ld bytes",
                 what, need, kNoAllocScratchBytes);
   if (tokens == 0) return 0;
-  void* inter = nullptr;
-  if (int rc = noalloc_scratch(&inter, what)) return rc;
+  // every check comes before the first launch: a rejected call queues nothing on the stream
+  if (!out) return fail(hipErrorInvalidValue, "%s: null output pointer", what);
+  if ((uintptr_t)out & 15) return fail(hipErrorInvalidValue, "%s: misaligned output (16 bytes needed)", what);
   hipStream_t s = (hipStream_t)stream;
+  // the GEMM's checks run with `out` standing in for the scratch (both are non-null); the
+  // scratch address goes into the arguments once resolved
+  MoePlan pl;
+  if (int rc = moe_plan(2, out, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
+                        num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
+                        in_dtype, out_dtype, doweight_stage2, 0, false, group_size, &pl))
+    return rc;
+  void* inter = nullptr;
+  if (int rc = noalloc_scratch(&inter, what, s)) return rc;
+  pl.args.out = inter;
   if (zero_intermediate && !valid_mask) {
     const long n = need / 16;
     const long g = (n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048;
@@ -398,10 +448,7 @@ int flygemm_moe_gemm2_reduce_noalloc(void* out, const void* a2, const void* w, c
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(e, "%s: launch of the zero fill failed: %s", what, hipGetErrorString(e));
   }
-  if (int rc = moe_launch(2, inter, a2, w, scale_a2, scale_w, sorted_token_ids, sorted_expert_ids, sorted_weights,
-                          num_valid_ids, tokens, model_dim, inter_dim, size_expert_ids, experts, topk, tile_m, tile_n,
-                          in_dtype, out_dtype, doweight_stage2, 0, false, group_size, s))
-    return rc;
+  if (int rc = moe_run(pl, what, s)) return rc;
   return flygemm_moe_reduce(out, inter, valid_mask, tokens, topk, model_dim, out_dtype, stream);
 }
 

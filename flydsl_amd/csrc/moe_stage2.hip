@@ -8,10 +8,10 @@ namespace flygemm {
 
 namespace {
 template <int KIND, bool F32, bool BS>
-MoeFn stage2_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, WM_, WN_)                                                                            \
-  static_assert(WM_ * WN_ * 64 == (R_ > 1 ? 512 : 256), "moe_launch gives run tiles 8 waves, others 4"); \
-  if (tm == M_ && r == R_ && tn == N_) return moe_gemm_kernel<2, KIND, M_, R_, N_, WM_, WN_, F32, BS>;
+MoeKernel stage2_tile(int tm, int r, int tn) {
+#define T(M_, R_, N_, WM_, WN_)        \
+  if (tm == M_ && r == R_ && tn == N_) \
+    return MoeKernel{moe_gemm_kernel<2, KIND, M_, R_, N_, WM_, WN_, F32, BS>, WM_ * WN_ * 64};
   // single-block tiles of 64 and 128 columns: the launcher never gives stage 2 single-block
   // tiles of 256 columns (it narrows them to 128 or 64)
   T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4) T(64, 1, 64, 1, 4)
@@ -23,18 +23,18 @@ MoeFn stage2_tile(int tm, int r, int tn) {
     T(16, 16, 256, 2, 4)
   }
 #undef T
-  return nullptr;
+  return MoeKernel{nullptr, 0};
 }
 
 template <int KIND>
-MoeFn stage2_kind(int tm, int r, int tn, bool f32) {
+MoeKernel stage2_kind(int tm, int r, int tn, bool f32) {
   return f32 ? stage2_tile<KIND, true, false>(tm, r, tn) : stage2_tile<KIND, false, false>(tm, r, tn);
 }
 }  // namespace
 
-MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs) {
+MoeKernel moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs) {
   if (bs)
-    return kind != KIND_FP8 ? nullptr
+    return kind != KIND_FP8 ? MoeKernel{nullptr, 0}
                             : (f32 ? stage2_tile<KIND_FP8, true, true>(tm, r, tn)
                                    : stage2_tile<KIND_FP8, false, true>(tm, r, tn));
   switch (kind) {
@@ -44,7 +44,7 @@ MoeFn moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs) {
     case KIND_W4A16: return stage2_kind<KIND_W4A16>(tm, r, tn, f32);
     case KIND_BF16: return stage2_kind<KIND_BF16>(tm, r, tn, f32);
     case KIND_F16: return stage2_kind<KIND_F16>(tm, r, tn, f32);
-    default: return nullptr;
+    default: return MoeKernel{nullptr, 0};
   }
 }
 

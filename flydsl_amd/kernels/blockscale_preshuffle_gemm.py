@@ -51,6 +51,20 @@ class BlockscaleGemm:
                                     _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
         _lib.check(rc, "flygemm_blockscale")
 
+    def _bind(self):
+        """The launch without the per-call checks, for ``flydsl_amd.compile`` (as
+        ``PreshuffleGemm._bind``)."""
+        fn = _lib.load().flygemm_blockscale
+        K, sbk, out, var = self.K, self.scale_block_k, _lib.FLYGEMM_OUT[self.out_dtype], self.variant
+        check = _lib.check
+
+        def call(c, a, b, sa, sb, M, N, stream=None):
+            s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
+            rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, sbk, out, var, s)
+            if rc:
+                check(rc, "flygemm_blockscale")
+        return call
+
 
 def compile_blockscale_preshuffle_gemm(*, M: int = 0, N: int = 0, K: int, tile_m: int = 64, tile_n: int = 128,
                                        tile_k: int = 128, scale_block_k: int = 128, out_dtype: str = "bf16",

@@ -89,6 +89,40 @@ class PreshuffleGemm:
                                     _lib.FLYGEMM_OUT[self.out_dtype], self.variant, h_stream)
         _lib.check(rc, "flygemm_preshuffle")
 
+    def _bind(self):
+        """The launch without the per-call checks, for ``flydsl_amd.compile``: tensor data
+        pointers, M, N and the stream are read per call and go straight to the C entry point
+        (which still checks the sizes); dtypes, contiguity and capacities are the caller's, as
+        in the reference's ``CompiledFunction`` (python/flydsl/compiler/jit_function.py:895-915)."""
+        lib = _lib.load()
+        K, var, out = self.K, self.variant, _lib.FLYGEMM_OUT[self.out_dtype]
+        check = _lib.check
+        if self.in_dtype == "fp4":
+            fn = lib.flygemm_mxfp4
+
+            def call(c, a, b, sa, sb, M, N, stream=None):
+                s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
+                rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, out, var, s)
+                if rc:
+                    check(rc, "flygemm_mxfp4")
+            return call
+        fn = lib.flygemm_preshuffle
+        ind = _lib.FLYGEMM_IN[self.in_dtype]
+        if self.in_dtype in _IN_TORCH16:
+            def call(c, a, b, sa, sb, M, N, stream=None):
+                s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
+                rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), None, None, M, N, K, ind, out, var, s)
+                if rc:
+                    check(rc, "flygemm_preshuffle")
+            return call
+
+        def call(c, a, b, sa, sb, M, N, stream=None):
+            s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
+            rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, ind, out, var, s)
+            if rc:
+                check(rc, "flygemm_preshuffle")
+        return call
+
     def _call_fp4(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):
         """MXFP4: packed e2m1 A [M, K/2] and preshuffled B [N, K/2] bytes, shuffled E8M0 scales
         [round_up(M, 32), K/32] and [N, K/32] bytes (``flydsl_amd.fp4``; reference harness

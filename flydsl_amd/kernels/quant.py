@@ -30,6 +30,7 @@ from ._launch import device_ptr, stream_handle
 BLOCK_THREADS = 256
 WARP_SIZE = 64
 VEC_WIDTH = 8
+WIDE_N = 8192
 
 _QIN = {torch.float16: _lib.QUANT_IN["fp16"], torch.bfloat16: _lib.QUANT_IN["bf16"],
         torch.float32: _lib.QUANT_IN["fp32"]}
@@ -46,7 +47,10 @@ def build_quant_module(N: int):
     N = int(N)
     if N <= 0 or N % VEC_WIDTH:
         raise ValueError(f"N={N} must be a positive multiple of {VEC_WIDTH}")
-    tile_cols = BLOCK_THREADS * VEC_WIDTH
+    # the library runs rows of WIDE_N or more elements with twice the threads (kQuantWideN in
+    # csrc/quant_rows.h): each thread still owns VEC_WIDTH consecutive elements per slice
+    threads = 2 * BLOCK_THREADS if N >= WIDE_N else BLOCK_THREADS
+    tile_cols = threads * VEC_WIDTH
 
     def launch_quant(Input, Output, Scales, m_in, stream=None):
         M = int(m_in)
@@ -59,7 +63,7 @@ def build_quant_module(N: int):
 
     config = {
         "N": N,
-        "BLOCK_THREADS": BLOCK_THREADS,
+        "BLOCK_THREADS": threads,
         "VEC_WIDTH": VEC_WIDTH,
         "ELEMS_PER_BLOCK_ITER": tile_cols,
         "ITERS": (N + tile_cols - 1) // tile_cols,

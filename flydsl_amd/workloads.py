@@ -54,6 +54,14 @@ WORKLOADS = {
     "T": Workload("T", "fp8", 8192, 8192, 8192, 5, note="FP8 8192^3, MFMA-bound target"),
     "T16": Workload("T16", "bf16", 8192, 8192, 8192, 6, note="BF16 8192^3 (in_dtype='bf16', unscaled)"),
     "F4": Workload("F4", "mxfp4", 8192, 8192, 8192, 7, note="MXFP4 8192^3 (1x32 E8M0 block scales)"),
+    # the reference's GEMM benchmark list (scripts/run_benchmark.sh:71-79) beyond T
+    "G1": Workload("G1", "fp8", 16, 40960, 5120, 8, note="FP8 decode (reference benchmark list)"),
+    "G2": Workload("G2", "fp8", 16, 77824, 5120, 9, note="FP8 decode (reference benchmark list)"),
+    "G3": Workload("G3", "fp8", 5120, 5120, 8320, 10, note="FP8 (reference benchmark list)"),
+    "G4": Workload("G4", "fp8", 9728, 8192, 8320, 11, note="FP8 (reference benchmark list)"),
+    "G5": Workload("G5", "int8", 9728, 8192, 8320, 12, note="INT8 W8A8 (reference benchmark list)"),
+    "G6": Workload("G6", "int4", 9728, 8192, 8320, 13, b_std=0.02, note="W4A8 (reference benchmark list)"),
+    "G7": Workload("G7", "bf16", 5120, 5120, 8320, 14, note="BF16 (reference benchmark list)"),
 }
 
 

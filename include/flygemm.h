@@ -249,6 +249,17 @@ int32_t flygemm_num_variants(void);
 const char* flygemm_variant_name(int32_t variant);
 int32_t flygemm_select_variant(int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t blockscale);
 
+/* The launch that flygemm_preshuffle (blockscale == 0), flygemm_blockscale (blockscale != 0) or
+ * flygemm_mxfp4 (in_dtype FLYGEMM_IN_FP4) would make for these sizes and variant (-1: the
+ * table's choice), on the current device: the variant index, the workgroup count, threads per
+ * workgroup and the work items the grid walks (output tiles for the large-M kernel, which is
+ * persistent: one workgroup takes tiles w, w + grid, ...; workgroups for the others, one item
+ * each).  K counts elements as in those entry points.  Launches nothing; it queries the
+ * device's CU count and occupancy.  Counterpart of the grid the reference's launcher computes
+ * (kernels/preshuffle_gemm.py:1268-1301), for tests and tuning. */
+int flygemm_launch_shape(int32_t M, int32_t N, int32_t K, int32_t in_dtype, int32_t blockscale, int32_t variant,
+                         int32_t* variant_out, int32_t* grid, int32_t* threads, int32_t* items);
+
 /* Message of the calling thread's last failure ("" if none).  The reference prints HIP
  * errors instead of returning them (lib/Runtime/FlyRocmRuntimeWrappers.cpp:22-30). */
 const char* flygemm_last_error(void);

@@ -13,6 +13,18 @@ from oracle import numerics as on
 OUT_TORCH = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
+def variant_names() -> list[str]:
+    """The library's kernel variant names, for parametrizing GPU tests at collection time; an
+    empty list when the library is not built (then those tests collect as skipped, and CPU-only
+    runs, which deselect them, still collect)."""
+    from flydsl_amd import _lib
+
+    try:
+        return _lib.variants()
+    except RuntimeError:
+        return []
+
+
 def u8(t: torch.Tensor) -> np.ndarray:
     t = t.contiguous().cpu()
     return t.view(torch.uint8).numpy() if t.dtype != torch.uint8 else t.numpy()

@@ -15,7 +15,7 @@ from oracle import gemm as og
 from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
-VARIANTS = _lib.variants()
+VARIANTS = H.variant_names()
 DT = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 

@@ -18,9 +18,10 @@ import torch
 
 from flydsl_amd import _lib, quant
 from flydsl_amd.kernels.quant import quant_gemm
+from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
-VARIANTS = _lib.variants()
+VARIANTS = H.variant_names()
 FUSED = [i for i, n in enumerate(VARIANTS) if n.startswith("decode_m1_")]
 OUT_T = {"bf16": torch.bfloat16, "fp16": torch.float16}
 QIN = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}

@@ -11,9 +11,10 @@ from flydsl_amd import _lib, workloads
 from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8, compile_preshuffle_gemm_w4
 from oracle import gemm as og
 from oracle import mxfp4 as om
+from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
-VARIANTS = _lib.variants()
+VARIANTS = H.variant_names()
 OUT = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}
 
 

@@ -16,7 +16,7 @@ from tests import helpers as H
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-VARIANTS = _lib.variants()
+VARIANTS = H.variant_names()
 MAIN = [i for i, n in enumerate(VARIANTS) if n.startswith("main_")]
 
 
@@ -307,3 +307,49 @@ def test_graph_replay(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(c, eager), f"replay {i}"
+
+
+def test_compiled_fast_path_matches_launcher(gpu):
+    """``flydsl_amd.compile(launcher, *args)`` (the reference's ``flyc.compile``) runs the launch
+    once with its checks, then repeats it for new tensors, M and stream without them: the same
+    bits as the launcher, for fp8, int8, blockscale and bf16, on the default and a side stream."""
+    import flydsl_amd
+    from flydsl_amd.kernels.blockscale_preshuffle_gemm import compile_blockscale_preshuffle_gemm
+    from flydsl_amd.kernels.preshuffle_gemm import compile_preshuffle_gemm_a8
+
+    side = torch.cuda.Stream()
+    for kind in ("fp8", "int8", "fp8_block", "bf16"):
+        N, K = 512, 1024
+        first, second = [workloads.make_operands(workloads.custom(kind, M, N, K, seed=M + 5)) for M in (64, 200)]
+        if kind == "fp8_block":
+            fn = compile_blockscale_preshuffle_gemm(M=64, N=N, K=K, tile_m=64, tile_n=128, tile_k=128, out_dtype="bf16")
+        else:
+            fn = compile_preshuffle_gemm_a8(K=K, tile_m=64, tile_n=128, tile_k=64 if kind == "bf16" else 128,
+                                            in_dtype=kind, out_dtype="bf16")
+
+        def args(ops, c):
+            sa = ops["sa_t"] if kind == "fp8_block" else ops["sa"]
+            return (c.view(-1), H.dev_flat(ops["a"], gpu), H.dev_flat(ops["b_dev"], gpu),
+                    sa.to(gpu).contiguous().view(-1), ops["sb"].to(gpu).contiguous().view(-1))
+
+        _say(f"compiled fast path {kind}")
+        c1 = torch.empty(64, N, dtype=torch.bfloat16, device=gpu)
+        cf = flydsl_amd.compile(fn, *args(first, c1), 64, N, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        want1 = H.launch(first, gpu)
+        torch.cuda.synchronize()
+        assert torch.equal(c1, want1)
+        c2 = torch.zeros(200, N, dtype=torch.bfloat16, device=gpu)
+        with torch.cuda.stream(side):
+            cf(*args(second, c2), 200, N, side)
+        side.synchronize()
+        want2 = H.launch(second, gpu)
+        torch.cuda.synchronize()
+        assert torch.equal(c2, want2)
+        H.check(second, c2)
+        c1.zero_()
+        cf(*args(first, c1), 64, N, torch.cuda.current_stream().cuda_stream)   # a raw stream handle
+        torch.cuda.synchronize()
+        assert torch.equal(c1, want1)
+    with pytest.raises(RuntimeError, match="multiple of 16"):   # the C entry still checks sizes
+        cf(*args(first, c1), 64, 100, None)

@@ -28,7 +28,8 @@ def test_reference_kernel_semantics(gpu, M, N):
     _say(f"quant recip_trunc fp16->int8 M={M} N={N}")
     x = _ref_data(M, N)
     launch, cfg = build_quant_module(N)
-    assert cfg["ITERS"] == (N + 2047) // 2048 and cfg["BLOCK_THREADS"] == 256
+    threads = 512 if N >= 8192 else 256   # rows of 8192+ elements run 512 threads
+    assert cfg["BLOCK_THREADS"] == threads and cfg["ITERS"] == (N + threads * 8 - 1) // (threads * 8)
     xi = torch.from_numpy(x).to(gpu)
     out = torch.empty(M, N, dtype=torch.int8, device=gpu)
     sc = torch.empty(M, dtype=torch.float32, device=gpu)

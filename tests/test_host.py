@@ -166,6 +166,11 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc != 0 and b"in_dtype" in lib.flygemm_last_error()
     rc = lib.flygemm_quant_rows(ctypes.c_void_p(17), p, p, 4, 64, 0, 1, 0, None)
     assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
+    # the GEMM that quantizes its activations checks alignment before it picks its path (fused
+    # kernel or quant + GEMM): x 16 bytes, a_q 8, scale_a 4
+    for x, aq, sa in [(ctypes.c_void_p(24), p, p), (p, ctypes.c_void_p(20), p), (p, p, ctypes.c_void_p(18))]:
+        rc = lib.flygemm_preshuffle_quant_a(p, aq, sa, x, p, p, 16, 128, 256, 0, 1, 0, 0, -1, None)
+        assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
     assert lib.flygemm_quant_rows(p, p, p, 0, 64, 0, 1, 0, None) == 0
     # 16-bit inputs: K counts elements and must be a multiple of 32; scales are not needed
     rc = lib.flygemm_preshuffle(p, p, p, None, None, 16, 128, 80, 3, 0, -1, None)
@@ -312,6 +317,16 @@ def test_moe_abi_rejects_bad_arguments_before_launch():
     assert lib.flygemm_moe_reduce(p, p, None, 4, 2, 128, 7, None) != 0 and b"dtype" in err()
     assert lib.flygemm_moe_reduce(ctypes.c_void_p(8), p, None, 4, 2, 128, 1, None) != 0 and b"misaligned" in err()
     assert lib.flygemm_moe_reduce(p, p, None, 0, 2, 128, 1, None) == 0
+    # the no-alloc stage 2 + reduction checks everything before its first launch and before it
+    # looks up its scratch (which needs a device): here, without one, the argument errors come back
+
+    def noalloc(out=p, tile_n=64, tokens=64):
+        return lib.flygemm_moe_gemm2_reduce_noalloc(out, p, p, p, p, p, p, p, p, tokens, 256, 128, 12, 4, 2, 16,
+                                                    tile_n, 0, 1, 0, -1, None, 1, None)
+    assert noalloc(tile_n=96) != 0 and b"tile_n" in err()
+    assert noalloc(out=ctypes.c_void_p(264)) != 0 and b"misaligned output" in err()
+    assert noalloc(out=None) != 0 and b"null output" in err()
+    assert noalloc(tokens=0) == 0
 
 
 def test_moe_launchers_validate_like_reference():
@@ -413,3 +428,19 @@ def test_moe_tile_choice_pinned():
     assert sel(1, 16, 256, 4, 2, 48, 64) != 0 and b"tile_m" in lib.flygemm_last_error()
     assert sel(1, 16, 320, 4, 2, 16, 256) != 0 and b"tile_n" in lib.flygemm_last_error()
     assert sel(1, 16, 256, 4, 2, 16, 64, "fp4") != 0 and b"in_dtype" in lib.flygemm_last_error()
+
+
+def test_compile_validates_on_first_call():
+    """``flydsl_amd.compile`` runs the launch once with every check (host tensors are refused
+    before anything reaches the library); a callable that is not one of this package's
+    launchers comes back as it is, after its first call."""
+    import flydsl_amd
+    fn = compile_preshuffle_gemm_a8(K=256, tile_m=64, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
+    x = torch.zeros(64 * 256, dtype=torch.int8)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        flydsl_amd.compile(fn, torch.zeros(64 * 128, dtype=torch.bfloat16), x, x, torch.ones(64), torch.ones(128),
+                           64, 128, None)
+    seen = []
+    plain = lambda *a: seen.append(a)   # noqa: E731
+    assert flydsl_amd.compile(plain, 1, 2) is plain and seen == [(1, 2)]
+
