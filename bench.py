@@ -342,43 +342,32 @@ def traffic_from_profile(name: str):
     return None
 
 
-def gfx_clock_under(work, seconds=0.4):
-    """Median graphics clock (MHz) that amdsmi reports while ``work`` runs back to back for
-    ``seconds`` (None if amdsmi is unavailable)."""
-    import threading
-    try:
-        import amdsmi
-        amdsmi.amdsmi_init()
-        h = amdsmi.amdsmi_get_processor_handles()[0]
-    except Exception as e:  # no amdsmi or no permission: the line goes without a clock
-        log(f"[bench] no clock reading: {type(e).__name__}: {str(e)[:100]}")
+def gfx_clock_under(work, dev, seconds=0.5):
+    """Median shader clock (MHz) while ``work`` (a graph replay) runs: a one-wave probe on a
+    side stream counts core cycles (s_memtime) against the 100 MHz constant counter for 100 us
+    in the middle of each replay (``flydsl_amd/_clockprobe.so``).  None if the probe is not built."""
+    import ctypes
+
+    from flydsl_amd.build import PROBE_OUT
+    if not os.path.exists(PROBE_OUT):
+        log("[bench] no clock probe library: the line goes without a clock")
         return None
-    samples, stop = [], threading.Event()
-
-    def sample():
-        while not stop.is_set():
-            try:
-                samples.append(float(amdsmi.amdsmi_get_clock_info(h, amdsmi.AmdSmiClkType.GFX)["clk"]))
-            except Exception:
-                pass
-            time.sleep(0.005)
-
-    t = threading.Thread(target=sample)
+    probe = ctypes.CDLL(PROBE_OUT).flygemm_clock_probe
+    probe.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    out = torch.zeros(2, dtype=torch.int64, device=dev)
+    side = torch.cuda.Stream()
+    vals = []
     t0 = time.perf_counter()
-    work()
-    t.start()
-    while time.perf_counter() - t0 < seconds:
+    while time.perf_counter() - t0 < seconds or len(vals) < 5:
         work()
-    stop.set()
-    t.join()
-    try:
-        amdsmi.amdsmi_shut_down()
-    except Exception:
-        pass
-    if not samples:
-        return None
-    samples.sort()
-    return samples[len(samples) // 2]
+        if probe(out.data_ptr(), 10000, side.cuda_stream) != 0:
+            return None
+        side.synchronize()
+        torch.cuda.synchronize()
+        cyc, ticks = out.tolist()
+        vals.append(cyc / (ticks / 100.0))
+    vals.sort()
+    return round(vals[len(vals) // 2])
 
 
 def dispatch_cost(dev, calls=1000):
@@ -404,7 +393,7 @@ def dispatch_cost(dev, calls=1000):
     a, b = _dev_flat(ops["a"], dev), _dev_flat(ops["b_dev"], dev)
     sa, sb = ops["sa"].to(dev).view(-1), ops["sb"].to(dev).view(-1)
     c = torch.empty(w.M * w.N, dtype=torch.bfloat16, device=dev)
-    fn = compile_preshuffle_gemm_a8(K=w.K, tile_m=16, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
+    fn = compile_preshuffle_gemm_a8(K=w.K, tile_m=32, tile_n=128, tile_k=128, in_dtype="fp8", out_dtype="bf16")
     s = torch.cuda.current_stream()
     h = s.cuda_stream
     cf = flydsl_amd.compile(fn, c, a, b, sa, sb, w.M, w.N, h)
@@ -576,13 +565,13 @@ def main():
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}
         if w2.flops:
             sec[name]["TFLOP/s"] = round(w2.flops / ms2 / 1e9, 1)
-        if name == "T":
+        if b2 == "mfma" and name not in MOE_BENCH:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 cap = torch.cuda.current_stream()
                 for i in range(n2):
                     r2.launch(i, cap)
-            clk = gfx_clock_under(lambda: (g.replay(), torch.cuda.synchronize()))
+            clk = gfx_clock_under(g.replay, dev)
             del g
             if clk:
                 # the dense peak assumes 2.4 GHz; under sustained MFMA load the chip holds less

@@ -36,9 +36,20 @@ def hipcc() -> str:
     return path
 
 
+# measurement aid for bench.py (shader clock under load), a library of its own so the GEMM
+# ABI stays as declared in include/flygemm.h
+PROBE_SRC = os.path.join(PKG_DIR, "csrc", "clock_probe.hip")
+PROBE_OUT = os.path.join(PKG_DIR, "_clockprobe.so")
+
+
 def build(verbose: bool = False) -> str:
-    """Compile each source to an object in parallel, then link the shared library."""
+    """Compile each source to an object in parallel, then link the shared library (and the
+    clock probe next to it)."""
     objs, procs = [], []
+    probe = [hipcc(), *HIPCC_FLAGS, "-o", PROBE_OUT + ".tmp", PROBE_SRC]
+    if verbose:
+        print(" ".join(probe), flush=True)
+    procs.append((PROBE_SRC, subprocess.Popen(probe, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
     for src in SOURCES:
         obj = os.path.splitext(OUT)[0] + "_" + os.path.splitext(os.path.basename(src))[0] + ".o"
         cmd = [hipcc(), *[f for f in HIPCC_FLAGS if f != "-shared"], "-c", "-o", obj, src]
@@ -61,6 +72,7 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-8000:]}")
     os.replace(tmp, OUT)
+    os.replace(PROBE_OUT + ".tmp", PROBE_OUT)
     for obj in objs:
         os.remove(obj)
     return OUT

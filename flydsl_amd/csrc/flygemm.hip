@@ -66,6 +66,8 @@ struct Shape {
   X(1, 2, 8, 4)          \
   X(1, 4, 8, 3)          \
   X(1, 7, 8, 2)          \
+  X(1, 5, 8, 3)          \
+  X(1, 10, 8, 2)         \
   X(2, 1, 8, 4)          \
   X(2, 2, 8, 3)          \
   X(4, 1, 8, 3)          \
@@ -115,6 +117,8 @@ constexpr long kSmallMaxTiles = 144;
 // 35.6 against 36.4; at 448 tiles, 512x7168x2304, 19.9 against 17.2).
 constexpr long kSmallMaxTilesBlock = 272;
 constexpr long kMidMaxTiles = 256;
+// CUs of an MI355X: the decode selection balances its workgroups over them
+constexpr long kCUs = 256;
 
 // One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
@@ -184,15 +188,37 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   const int ncol = (N + 127) / 128;
   const bool tile_small_m = M > 32 || (M > 16 && (ncol >= 200 || (epi == EPI_BLOCK && ncol >= 32)));
   if (M <= 64 && !tile_small_m) {
-    // decode family: fewest rows that cover M, then the most column blocks per workgroup
-    // that still leaves about one workgroup per CU
+    // decode family: fewest rows that cover M, then the column blocks per workgroup
     const int rows = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
     const int nblk = N / 16;
+    // One 16-row block of fp8 / int8 / int4 codes: the most column blocks per workgroup whose
+    // workgroups fill their last round over the CUs to at least 85% -- a partly filled last
+    // round runs the tail on a fraction of the chip (graph-timed on MI355X, fp8 16 x N x K:
+    // 40960x5120 35.3 us with 5 blocks (512 workgroups, two full rounds) against 39.5 with 7
+    // (366, the last round 43% full); 24576x8192 32.8 with 7 (220, 86%) against 39.0 with 4
+    // (384, 50%); 14336x4096 11.7 with 4 (224) against 13.8 with 7 (128); int4 40960x5120 19.2
+    // with 10 blocks (256) against 23.9 with 7; the rule picks the fastest measured variant or
+    // one within 6% on 10 shapes per kind).  Ten blocks only for int4, whose blocks carry half
+    // the bytes (fp8 with ten spills registers: 77.6 us on 40960x5120).
+    if (rows == 16 && (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_INT4) && epi != EPI_BLOCK) {
+      int best = -1;
+      for (int v = kFirstDecode; v < kFirstRows; ++v) {
+        if (kShapes[v].bm != 16) continue;
+        const int nbw = kShapes[v].bn / 16;
+        if (nbw == 10 && kind != KIND_INT4) continue;
+        const long wg = (nblk + nbw - 1) / nbw;
+        const long rounds = (wg + kCUs - 1) / kCUs;
+        if (wg * 100 >= rounds * kCUs * 85 && (best < 0 || nbw > kShapes[best].bn / 16)) best = v;
+      }
+      if (best >= 0) return best;
+    }
+    // otherwise the most column blocks per workgroup that still leaves about one workgroup per CU
     int best = -1;
     for (int v = kFirstDecode; v < kFirstRows; ++v) {
       if (kShapes[v].bm != rows) continue;
       const int nbw = kShapes[v].bn / 16;
       if (kind == KIND_FP4 && nbw > 4) continue;  // MXFP4's scale words push 7 blocks past the register file
+      if (nbw == 5 || nbw == 10) continue;        // measured only for the codes above
       // int4 blocks carry half the bytes: 4 blocks per workgroup beat 2 even at 224 workgroups
       // (16x14336x4096: 7.6 us against 8.5)
       const int min_wg = kind == KIND_INT4 ? 200 : 240;

@@ -105,9 +105,18 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(33, 2112, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 5, 0)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(128, 4096, 2048, 3, 0)] == "rows_m2_nb4_w8_u3"  # 2 bytes/elt
-    # int4 decode takes more column blocks per workgroup (half-size blocks)
-    assert names[lib.flygemm_select_variant(16, 14336, 4096, 2, 0)] == "decode_m1_nb4_w8_u3"
-    assert names[lib.flygemm_select_variant(16, 14336, 4096, 1, 0)] == "decode_m1_nb2_w8_u4"
+    # decode of one 16-row block (fp8 / int8 / int4 codes): the most column blocks per workgroup
+    # whose workgroups fill their last round over 256 CUs to at least 85%; ten blocks only for
+    # int4 (half-size blocks)
+    dec = {(16, 14336, 4096, 2): "nb4", (16, 14336, 4096, 1): "nb4", (16, 40960, 5120, 0): "nb5",
+           (16, 40960, 5120, 1): "nb5", (16, 40960, 5120, 2): "nb10", (16, 77824, 5120, 0): "nb7",
+           (16, 77824, 5120, 2): "nb10", (16, 24576, 8192, 0): "nb7", (16, 7168, 2048, 0): "nb2",
+           (16, 4096, 4096, 1): "nb1", (1, 57344, 8192, 0): "nb7", (16, 28672, 8192, 2): "nb7"}
+    for (m, n, k, ind), want in dec.items():
+        assert names[lib.flygemm_select_variant(m, n, k, ind, 0)] == f"decode_m1_{want}_w8_" + \
+            {"nb1": "u4", "nb2": "u4", "nb4": "u3", "nb5": "u3", "nb7": "u2", "nb10": "u2"}[want], (m, n, k, ind)
+    # other kinds keep the rule of about one workgroup per CU (bf16 16x40960x5120: 2560 blocks)
+    assert names[lib.flygemm_select_variant(16, 40960, 5120, 3, 0)] == "decode_m1_nb7_w8_u2"
     # MXFP4 decode keeps to at most 4 column blocks per workgroup
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 5, 0)] == "decode_m1_nb4_w8_u3"
     for m in (1, 17, 64, 65, 100, 1000, 5000):
