@@ -343,9 +343,12 @@ def traffic_from_profile(name: str):
 
 
 def gfx_clock_under(work, dev, seconds=0.5):
-    """Median shader clock (MHz) while ``work`` (a graph replay) runs: a one-wave probe on a
-    side stream counts core cycles (s_memtime) against the 100 MHz constant counter for 100 us
-    in the middle of each replay (``flydsl_amd/_clockprobe.so``).  None if the probe is not built."""
+    """Median shader clock (MHz) while ``work`` (a graph replay on the current stream) runs: a
+    one-wave probe on a side stream counts core cycles (s_memtime) against the 100 MHz constant
+    counter for 100 us (``flydsl_amd/_clockprobe.so``).  A sample counts only if the probe ended
+    before the replay did (a second, one-tick probe queued behind the replay on its stream
+    gives the replay's end), so the clock is the one under load.  None if the probe is not built
+    or no sample overlapped."""
     import ctypes
 
     from flydsl_amd.build import PROBE_OUT
@@ -354,18 +357,23 @@ def gfx_clock_under(work, dev, seconds=0.5):
         return None
     probe = ctypes.CDLL(PROBE_OUT).flygemm_clock_probe
     probe.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
-    out = torch.zeros(2, dtype=torch.int64, device=dev)
-    side = torch.cuda.Stream()
-    vals = []
+    out = torch.zeros(4, dtype=torch.int64, device=dev)
+    end = torch.zeros(4, dtype=torch.int64, device=dev)
+    main, side = torch.cuda.current_stream(), torch.cuda.Stream()
+    vals, tries = [], 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds or len(vals) < 5:
+    while (time.perf_counter() - t0 < seconds or len(vals) < 5) and tries < 200:
+        tries += 1
         work()
-        if probe(out.data_ptr(), 10000, side.cuda_stream) != 0:
+        if probe(out.data_ptr(), 10000, side.cuda_stream) or probe(end.data_ptr(), 1, main.cuda_stream):
             return None
-        side.synchronize()
         torch.cuda.synchronize()
-        cyc, ticks = out.tolist()
-        vals.append(cyc / (ticks / 100.0))
+        cyc, ticks, _, r_end = out.tolist()
+        if r_end + 100 < end.tolist()[2]:
+            vals.append(cyc / (ticks / 100.0))
+    log(f"[bench] clock probe: {len(vals)} of {tries} samples overlapped the work")
+    if not vals:
+        return None
     vals.sort()
     return round(vals[len(vals) // 2])
 

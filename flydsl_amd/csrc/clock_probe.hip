@@ -15,10 +15,13 @@ __global__ void __launch_bounds__(64) clock_probe_kernel(unsigned long long* out
   if (threadIdx.x == 0) {
     out[0] = c1 - c0;
     out[1] = r1 - r0;
+    out[2] = r0;
+    out[3] = r1;
   }
 }
 
-// out: two device uint64 (core cycles, 100 MHz ticks); ticks: the spin, in 10 ns units.
+// out: four device uint64 (core cycles, 100 MHz ticks elapsed, then the 100 MHz counter at the
+// start and at the end); ticks: the spin, in 10 ns units.
 extern "C" int flygemm_clock_probe(unsigned long long* out, long long ticks, void* stream) {
   if (!out || ticks <= 0 || ticks > 100000000) return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(clock_probe_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, out, (unsigned long long)ticks);
