@@ -47,19 +47,24 @@ struct Shape {
   int family;
   int bm, bn, threads;  // main: workgroup tile; decode/rows: bm = 16*MR rows, bn = 16*NBW cols
   bool rows;            // row-blocked streaming variant (chosen for M > 64 with few output tiles)
+  int ksub;             // main: K tiles per pipeline step
 };
 
 // Ordered by preference: the selector takes the first tile that yields enough workgroups.
-#define MAIN_SHAPES(X) \
-  X(256, 256, 2, 4)    \
-  X(256, 256, 4, 2)    \
-  X(128, 128, 2, 2)    \
-  X(64, 128, 1, 4)     \
-  X(256, 128, 2, 4)    \
-  X(128, 256, 2, 4)    \
-  X(256, 64, 4, 1)     \
-  X(128, 64, 2, 2)     \
-  X(64, 64, 1, 4)
+// (BM, BN, WM, WN, K tiles per step, name suffix).  The two-K-tile steps exist for the
+// two-stage tiles without per-K-tile scales (int4 weights on the 4-wave tiles).
+#define MAIN_SHAPES(X)       \
+  X(256, 256, 2, 4, 1, "")   \
+  X(256, 256, 4, 2, 1, "")   \
+  X(128, 128, 2, 2, 1, "")   \
+  X(64, 128, 1, 4, 1, "")    \
+  X(256, 128, 2, 4, 1, "")   \
+  X(128, 256, 2, 4, 1, "")   \
+  X(256, 64, 4, 1, 1, "")    \
+  X(128, 64, 2, 2, 1, "")    \
+  X(64, 64, 1, 4, 1, "")     \
+  X(64, 128, 1, 4, 2, "_k2") \
+  X(64, 64, 1, 4, 2, "_k2")
 
 #define DECODE_SHAPES(X) \
   X(1, 1, 8, 4)          \
@@ -84,13 +89,13 @@ struct Shape {
   X(2, 4, 8, 3)
 
 const Shape kShapes[] = {
-#define MS(BM, BN, WM, WN) {"main_" #BM "x" #BN "_w" #WM "x" #WN, FAM_MAIN, BM, BN, WM * WN * 64, false},
+#define MS(BM, BN, WM, WN, KS, SUF) {"main_" #BM "x" #BN "_w" #WM "x" #WN SUF, FAM_MAIN, BM, BN, WM * WN * 64, false, KS},
     MAIN_SHAPES(MS)
 #undef MS
-#define DS(MR, NBW, NW, U) {"decode_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, false},
+#define DS(MR, NBW, NW, U) {"decode_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, false, 1},
         DECODE_SHAPES(DS)
 #undef DS
-#define RS(MR, NBW, NW, U) {"rows_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, true},
+#define RS(MR, NBW, NW, U) {"rows_m" #MR "_nb" #NBW "_w" #NW "_u" #U, FAM_DECODE, 16 * MR, 16 * NBW, NW * 64, true, 1},
             ROW_SHAPES(RS)
 #undef RS
 };
@@ -120,12 +125,23 @@ constexpr long kMidMaxTiles = 256;
 // CUs of an MI355X: the decode selection balances its workgroups over them
 constexpr long kCUs = 256;
 
+// The large-M kernel of one table entry.  Two K tiles per step need the two-stage ring and no
+// per-K-tile scales; where a kind lacks them (the three-stage 4-wave tiles of fp8, int8 and
+// 16-bit inputs, blockscale, MXFP4) the entry runs the one-K-tile kernel of the same tile.
+template <int BM, int BN, int WM, int WN, int KS, int KIND, int EPI, bool BF16>
+constexpr KernelFn main_fn() {
+  if constexpr (KS > 1 && MainCfg<BM, BN, WM, WN, KIND>::NS == 2 && EPI != EPI_BLOCK && KIND != KIND_FP4)
+    return gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16, KS>;
+  else
+    return gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16>;
+}
+
 // One row of kernels per (kind, epilogue, output dtype) combination, one column per shape.
 template <int KIND, int EPI, bool BF16>
 struct KernelRow {
   static const KernelFn* get() {
     static const KernelFn fns[] = {
-#define MS(BM, BN, WM, WN) gemm_main_kernel<BM, BN, WM, WN, KIND, EPI, BF16>,
+#define MS(BM, BN, WM, WN, KS, SUF) main_fn<BM, BN, WM, WN, KS, KIND, EPI, BF16>(),
         MAIN_SHAPES(MS)
 #undef MS
 #define DS(MR, NBW, NW, U) gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI, BF16, true>,
@@ -253,6 +269,27 @@ int select_variant(int M, int N, int K, int kind, int epi) {
                                 {256, 128, 512, 160, 1 << 30, true},
                                 {128, 128, 256, 240, 1 << 30, true},
                                 {64, 128, 256, 0, 1 << 30, true}};
+  // int4 weights with few output tiles (at most 512 of 64x128): two K tiles per pipeline step.
+  // A 4-wave tile's step moves little, so a step waits on DMA latency rather than bandwidth;
+  // two K tiles per stage halve the waits (graph-timed on MI355X, int4 M x N x K with t 64x128
+  // tiles: 64x64 tiles with two K tiles per step against the table's choice -- 64x14336x4096
+  // (t = 112) 12.7 us against 17.5, 128x7168x8192 (112) 20.5 against 30.7, 256x4096x4096 (128)
+  // 11.9 against 16.8, 128x14336x4096 (224) 14.1 against 18.3, 256x8192x4096 (256) 13.9 against
+  // 18.4, 320x8192x8192 (320) 33.3 against 38.0; 64x128 tiles with two K tiles per step from 353
+  // to 512 tiles with K of at least 8192: 256x14336x8192 (448) 39.4 against 47.7, while at K =
+  // 4096 the one-K-tile 64x128 is level or faster (256x14336x4096: 19.6 against 19.7,
+  // 384x8192x4096: 19.1 against 19.7); at most 64 tiles the row-blocked kernel stays faster:
+  // 128x4096x4096 8.5 against 11.5)
+  if (kind == KIND_INT4 && epi != EPI_BLOCK) {
+    const long t128 = (long)((M + 63) / 64) * ((N + 127) / 128);
+    auto find = [](int bm, int bn, int ks) {
+      for (int v = 0; v < kFirstDecode; ++v)
+        if (kShapes[v].bm == bm && kShapes[v].bn == bn && kShapes[v].ksub == ks) return v;
+      return -1;
+    };
+    if (t128 > kRowsMaxTiles && t128 <= 352) return find(64, 64, 2);
+    if (t128 > 352 && t128 <= 512 && K >= 8192) return find(64, 128, 2);
+  }
   const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
   const int n = epi == EPI_BLOCK ? 5 : 4;
   for (int i = 0; i < n; ++i) {

@@ -148,9 +148,14 @@ __device__ __forceinline__ void workgroup_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16>
+// KSUB: K tiles per pipeline step (two-stage ring only).  With 2, each LDS stage holds two
+// 128-byte K tiles and a step waits for, and multiplies, both: half the barriers and twice the
+// bytes in flight per wait, for tiles whose steps are short next to the DMA latency.
+template <int BM, int BN, int WM, int WN, int KIND, int EPI, bool OUT_BF16, int KSUB = 1>
 __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) {
   using C = MainCfg<BM, BN, WM, WN, KIND>;
+  static_assert(KSUB == 1 || (KSUB == 2 && C::NS == 2 && EPI != EPI_BLOCK && KIND != KIND_FP4),
+                "two K tiles per step: two-stage ring, no per-K-tile scales");
   constexpr int MR = C::MR, NR = C::NR, NW = C::NW;
   // per-K-tile scale regions of a stage, in whole DMA instructions: 1 KB (16-byte lanes) for
   // MXFP4, 256 bytes (4-byte lanes) for blockscale
@@ -160,9 +165,9 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   constexpr int SB_BYTES = KIND == KIND_FP4 ? (BN / 32 * 256 + 1023) / 1024 * 1024 : (EPI == EPI_BLOCK ? 256 : 0);
   constexpr int SA_DMA = SA_BYTES / SC_INSTR, SB_DMA = SB_BYTES / SC_INSTR;
   static_assert(EPI != EPI_BLOCK || BN / 128 <= 64, "one w_scale per lane");
-  constexpr int STAGE = C::STAGE + SA_BYTES + SB_BYTES;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
+  constexpr int STAGE = C::STAGE + SA_BYTES + SB_BYTES;  // one K tile
+  __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE * KSUB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE * KSUB];
 
   const int M = p.M, N = p.N, K = p.K;
   const int nbm = (M + BM - 1) / BM;
@@ -215,8 +220,12 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   const sgpr4 rsrc_sa = buf_desc(p.sa, (SA_DMA + SB_DMA > 0) ? (uint32_t)sa_bytes : 0u);
   const sgpr4 rsrc_sb = buf_desc(p.sb, (SA_DMA + SB_DMA > 0) ? (uint32_t)sb_bytes : 0u);
 
-  auto issue = [&](uint8_t* s, int m0, int n0, int kt) {
-    const sgpr4 rsrc_a = buf_desc(p.a + (size_t)kt * KT, (uint32_t)(M * K - kt * KT));
+  // one K tile kt into the stage region s; a K tile past the end (the second K tile of a last
+  // step with KSUB = 2 and an odd K tile count) reads zeros: an empty A range, B lanes past
+  // the buffer
+  auto issue_tile = [&](uint8_t* s, int m0, int n0, int kt) {
+    const bool live = KSUB == 1 || kt < nk;
+    const sgpr4 rsrc_a = buf_desc(p.a + (size_t)(live ? kt : 0) * KT, live ? (uint32_t)(M * K - kt * KT) : 0u);
     const uint32_t mo = (uint32_t)m0 * (uint32_t)K;
     const bool half = half_k && kt == nk - 1;
 #pragma unroll
@@ -226,8 +235,8 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       const int q = wave + j * NW;
       const int nb = min(n0 / 16 + q / PARTS, nblk_max);
       const uint32_t so = (uint32_t)nb * (uint32_t)(C::B_BLK / KT) * (uint32_t)K + (uint32_t)((q % PARTS) * 1024) +
-                          (uint32_t)kt * C::B_BLK;
-      const uint32_t vo = !half ? vb : (PARTS == 1 ? vbh : (q % PARTS == 1 ? kPast : vb));
+                          (uint32_t)(live ? kt : 0) * C::B_BLK;
+      const uint32_t vo = !live ? kPast : (!half ? vb : (PARTS == 1 ? vbh : (q % PARTS == 1 ? kPast : vb)));
       dma16(rsrc_b, s + C::A_BYTES + q * 1024, vo, __builtin_amdgcn_readfirstlane(so));
     }
     // this K tile's scales: scale instruction q = wave, wave + NW, ... (q < SA_DMA: A region,
@@ -262,6 +271,11 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         }
       }
     }
+  };
+  // one pipeline step (KSUB K tiles) into stage s
+  auto issue = [&](uint8_t* s, int m0, int n0, int step_k) {
+#pragma unroll
+    for (int u = 0; u < KSUB; ++u) issue_tile(s + u * STAGE, m0, n0, step_k * KSUB + u);
   };
 
   typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
@@ -537,7 +551,7 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     m0_ = bm * BM;
     n0_ = bn * BN;
     kb_ = 0;
-    ke_ = nk;
+    ke_ = (nk + KSUB - 1) / KSUB;  // pipeline steps
   };
   if constexpr (C::NS == 3) {
     // Three LDS stages, the DMA two steps ahead (the 4-wave tiles, whose steps are short
@@ -622,7 +636,8 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
         issue(nxt, m0, n0, kt + 1);
       else if (wnext < nitems)
         issue(nxt, nm0, nn0, nkb);
-      compute(cur, kt != kb);
+#pragma unroll
+      for (int u = 0; u < KSUB; ++u) compute(cur + u * STAGE, kt != kb || u > 0);
     }
     if constexpr (EPI == EPI_BLOCK) flush_pending();
     // the stage the last step computed from; the DMA issued after the next step's barrier is the

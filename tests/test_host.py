@@ -57,7 +57,7 @@ def test_variant_table():
     # 65-144 tiles of 64x128: 64x64 tiles (twice the workgroups); at most 64: the row-blocked
     # kernel; above 144: 64x128; never 64x64 for MXFP4
     for args in [(256, 4096, 4096, 0, 0), (128, 8192, 8192, 0, 0), (192, 4096, 4096, 0, 0), (128, 7168, 2048, 1, 0),
-                 (256, 4096, 4096, 2, 0), (256, 4096, 4096, 3, 0), (128, 7168, 7168, 0, 1), (96, 8192, 8192, 0, 0)]:
+                 (256, 4096, 4096, 3, 0), (128, 7168, 7168, 0, 1), (96, 8192, 8192, 0, 0)]:
         assert names[lib.flygemm_select_variant(*args)] == "main_64x64_w1x4", args
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 1, 0)] == "rows_m2_nb4_w8_u3"    # 64 tiles
     assert names[lib.flygemm_select_variant(320, 4096, 4096, 0, 0)] == "main_64x128_w1x4"     # 160 tiles
@@ -92,7 +92,14 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(512, 4096, 7168, 0, 0)] == "main_128x64_w2x2"
     assert names[lib.flygemm_select_variant(384, 5120, 7168, 1, 0)] == "main_128x64_w2x2"
     assert names[lib.flygemm_select_variant(512, 4096, 4096, 3, 0)] == "main_128x64_w2x2"
-    assert names[lib.flygemm_select_variant(512, 4096, 4096, 2, 0)] == "main_64x128_w1x4"   # int4
+    # int4 with 65-512 tiles of 64x128: two K tiles per step -- 64x64 tiles up to 352, 64x128
+    # tiles above with K of at least 8192 (the one-K-tile 64x128 below that)
+    for args, want in {(256, 4096, 4096, 2, 0): "main_64x64_w1x4_k2", (512, 4096, 4096, 2, 0): "main_64x64_w1x4_k2",
+                       (64, 14336, 4096, 2, 0): "main_64x64_w1x4_k2", (320, 8192, 8192, 2, 0): "main_64x64_w1x4_k2",
+                       (256, 14336, 8192, 2, 0): "main_64x128_w1x4_k2", (256, 14336, 4096, 2, 0): "main_64x128_w1x4",
+                       (128, 4096, 4096, 2, 0): "rows_m2_nb4_w8_u3", (512, 14336, 8192, 2, 0): "main_128x128_w2x2",
+                       (256, 4096, 4096, 0, 0): "main_64x64_w1x4"}.items():
+        assert names[lib.flygemm_select_variant(*args)] == want, args
     assert names[lib.flygemm_select_variant(320, 4096, 4096, 0, 0)] == "main_64x128_w1x4"   # ragged 128-row tiles
     assert names[lib.flygemm_select_variant(768, 4096, 4096, 0, 0)] == "main_64x128_w1x4"   # 384 tiles
     # the row-blocked kernel where the 64x128 tiles leave CUs idle (at most 64 tiles; 96 with
