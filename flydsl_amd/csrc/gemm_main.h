@@ -36,6 +36,9 @@
 #ifndef FLY_GROUP_M
 #define FLY_GROUP_M 8
 #endif
+#ifndef FLY_ROLES
+#define FLY_ROLES 1
+#endif
 
 namespace flygemm {
 
@@ -188,6 +191,27 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   const int l16 = lane & 15;
   const int lq = lane >> 4;  // 0..3
 
+  // Staged epilogue (2-byte outputs, see epilogue_staged below): each wave's rows go through an
+  // LDS stage in two halves, then whole 128-byte lines are stored.  Not where its registers
+  // would spill (more than 4 column blocks per wave, or the blockscale epilogue's partials next
+  // to 32 accumulator tiles), nor for 64-column tiles, whose 128-byte rows gain less than the
+  // two barriers cost (256x4096x4096 fp8 on 64x64 tiles 13.9 us staged against 13.6 direct).
+  constexpr int RB = BN * 2, CPR = RB / 16, HR = C::TM / 2, HMR = MR / 2;
+  constexpr bool kStage = EPI != EPI_RAW && MR % 2 == 0 && NR <= 4 && BN >= 128 && !(EPI == EPI_BLOCK && MR * NR >= 32) &&
+                          BM / 2 * RB <= C::STAGE && (BM / 2 * CPR) % C::NT == 0;
+  // Split roles (8-wave tiles on the two-stage ring with the staged epilogue): waves NW/2..NW-1
+  // issue every LDS-DMA, waves 0..NW/2-1 every epilogue store.  A wave's wait for its DMA
+  // (vector memory counter, retired in issue order) then never includes stores, so a tile's
+  // output write drains while the next tile's first K steps run instead of stalling the
+  // second one.  Graph-timed on MI355X, split against shared roles: FP8 8192^3 395.5 us against
+  // 408, fp8 9728x8192x8320 476 against 498, int8 9728x8192x8320 496 against 517, bf16
+  // 5120x5120x8320 364 against 380, bf16 8192^3 781 against 813; level with one tile per CU
+  // (int8 4096^3 59.0 against 59.1); int4 9728x8192x8320 0.7% slower (kept shared there).
+  constexpr bool ROLES = FLY_ROLES && C::NS == 2 && NW == 8 && kStage && KSUB == 1 && KIND != KIND_INT4;
+  constexpr int DW = ROLES ? NW / 2 : NW;              // waves that issue DMA
+  const int dwave = ROLES ? wave - NW / 2 : wave;      // this wave's index among them (< 0: none)
+  constexpr int A_DMA_W = C::A_DMA * NW / DW, B_DMA_W = C::B_DMA * NW / DW;  // per DMA wave
+
   // ---- DMA addressing ----
   // A: buffer resource over the rows still ahead of this K tile; the per-lane VGPR offset
   // carries the row, so rows >= M fall outside num_records and read as zero.  The swizzled
@@ -199,10 +223,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   // every buffer, so the range check writes zeros there and those MFMA halves add nothing
   // (va0h / vbh; 0x80000000 plus any row offset stays past the 2^31-byte operands).
   constexpr uint32_t kPast = 0x80000000u;
-  uint32_t va0[C::A_DMA], va0h[C::A_DMA];
+  uint32_t va0[A_DMA_W], va0h[A_DMA_W];
 #pragma unroll
-  for (int j = 0; j < C::A_DMA; ++j) {
-    const int rloc = (wave + j * NW) * 8 + (lane >> 3);
+  for (int j = 0; j < A_DMA_W; ++j) {
+    const int rloc = (dwave + j * DW) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ ((rloc >> 1) & 7);
     va0[j] = (uint32_t)rloc * (uint32_t)K + (uint32_t)(c * 16);
     va0h[j] = (kHalfOk && c >= 4) ? kPast : va0[j];
@@ -224,15 +248,16 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   // step with KSUB = 2 and an odd K tile count) reads zeros: an empty A range, B lanes past
   // the buffer
   auto issue_tile = [&](uint8_t* s, int m0, int n0, int kt) {
+    if (ROLES && dwave < 0) return;  // a store wave
     const bool live = KSUB == 1 || kt < nk;
     const sgpr4 rsrc_a = buf_desc(p.a + (size_t)(live ? kt : 0) * KT, live ? (uint32_t)(M * K - kt * KT) : 0u);
     const uint32_t mo = (uint32_t)m0 * (uint32_t)K;
     const bool half = half_k && kt == nk - 1;
 #pragma unroll
-    for (int j = 0; j < C::A_DMA; ++j) dma16(rsrc_a, s + (wave + j * NW) * 1024, (half ? va0h[j] : va0[j]) + mo, 0);
+    for (int j = 0; j < A_DMA_W; ++j) dma16(rsrc_a, s + (dwave + j * DW) * 1024, (half ? va0h[j] : va0[j]) + mo, 0);
 #pragma unroll
-    for (int j = 0; j < C::B_DMA; ++j) {
-      const int q = wave + j * NW;
+    for (int j = 0; j < B_DMA_W; ++j) {
+      const int q = dwave + j * DW;
       const int nb = min(n0 / 16 + q / PARTS, nblk_max);
       const uint32_t so = (uint32_t)nb * (uint32_t)(C::B_BLK / KT) * (uint32_t)K + (uint32_t)((q % PARTS) * 1024) +
                           (uint32_t)(live ? kt : 0) * C::B_BLK;
@@ -244,8 +269,8 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
     if constexpr (SA_DMA + SB_DMA > 0) {
       uint8_t* sc = s + C::STAGE;
 #pragma unroll
-      for (int j = 0; j < (SA_DMA + SB_DMA + NW - 1) / NW; ++j) {
-        const int q = wave + j * NW;
+      for (int j = 0; j < (SA_DMA + SB_DMA + DW - 1) / DW; ++j) {
+        const int q = dwave + j * DW;
         if (q < SA_DMA) {
           if constexpr (KIND == KIND_FP4) {
             const uint32_t b = (uint32_t)q * 1024u + (uint32_t)lane * 16u;  // byte in the region
@@ -441,22 +466,19 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
   const __amdgpu_buffer_rsrc_t rsrc_c = make_rsrc(p.c, M * N * ESZ);
   // Staged epilogue (2-byte outputs): in two rounds, each wave's first and then second half of
   // its rows go through the LDS stage `stg` (free once every wave is past the first barrier),
-  // then every thread stores 16-byte chunks so that each wave instruction writes whole
+  // then every thread (every thread of the store waves, with split roles) stores 16-byte
+  // chunks so that each wave instruction writes whole
   // 128-byte lines (the MFMA layout writes 16 rows x 32 bytes per instruction, which the memory
   // system takes at about 2/3 of the rate of whole lines).  Staged row sr holds row
   // (sr / HR) * TM + h * HR + sr % HR of the tile in round h (HR = TM / 2); its chunk c sits at
   // chunk c ^ (sr % CPR).
-  constexpr int RB = BN * 2, CPR = RB / 16, HR = C::TM / 2, HMR = MR / 2;
-  // (not where its registers would spill: more than 4 column blocks per wave, or the blockscale
-  // epilogue's partials next to 32 accumulator tiles; nor for 64-column tiles, whose 128-byte
-  // rows gain less than the two barriers cost: 256x4096x4096 fp8 on 64x64 tiles 13.9 us staged
-  // against 13.6 direct -- those keep the direct stores).  Measured against the direct stores:
+  // (the tiles and conditions are in kStage above).  Measured against the direct stores:
   // C3 59.8 us against 62.1, C4 64.4 against 66.0, C5 20.9 against 21.8, T 412 against 418,
   // 1024x7168x7168 fp8 56.3 against 58.0, MXFP4 4096^3 35.5 against 38.5.
-  constexpr bool kStage = EPI != EPI_RAW && MR % 2 == 0 && NR <= 4 && BN >= 128 && !(EPI == EPI_BLOCK && MR * NR >= 32) &&
-                          BM / 2 * RB <= C::STAGE && (BM / 2 * CPR) % C::NT == 0;
   constexpr int SCH = kStage ? (BM / 2 * CPR) / C::NT : 0;
-  constexpr int NSTORE = SCH > 0 ? 2 * SCH : MR * NR;   // buffer stores per lane per tile
+  constexpr int NSTORE = SCH > 0 ? 2 * SCH : MR * NR;   // buffer stores per lane per tile (without roles)
+  constexpr int ST_T = ROLES ? C::NT / 2 : C::NT;        // threads that store
+  constexpr int SCH_W = ROLES ? 2 * SCH : SCH;           // 16-byte stores per storing thread per half
   auto epilogue_staged = [&](int m0, int n0, uint8_t* stg) {
 #pragma unroll
     for (int mi = 0; mi < MR; ++mi)
@@ -492,9 +514,10 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       }
       workgroup_barrier();
       __builtin_amdgcn_sched_barrier(0);
+      if (ROLES && wave >= NW / 2) continue;  // a DMA wave: the store waves write the lines
 #pragma unroll 2
-      for (int i = 0; i < SCH; ++i) {
-        const int cc = tid + i * C::NT;
+      for (int i = 0; i < SCH_W; ++i) {
+        const int cc = tid + i * ST_T;
         const int sr = cc / CPR, ch = cc % CPR;
         const i32x4 val = *(const i32x4*)(stg + sr * RB + ((ch ^ (sr % CPR)) << 4));
         const int row = m0 + (sr / HR) * C::TM + h * HR + sr % HR, col = n0 + ch * 8;
@@ -621,10 +644,13 @@ __global__ void __launch_bounds__(WM * WN * 64, 1) gemm_main_kernel(GemmArgs p) 
       // wait for this wave's loads of this step; at a tile's first step the previous
       // tile's MR*NR epilogue stores were issued after them and may still be in flight
       // (vector memory operations retire in issue order).
-      if (kt == kb && step > 0)
+      if constexpr (ROLES) {
+        if (dwave >= 0) wait_dma();  // DMA waves hold no stores; store waves issue no DMA
+      } else if (kt == kb && step > 0) {
         wait_vmem_leaving<NSTORE>();
-      else
+      } else {
         wait_dma();
+      }
       // this step's tile has landed; every wave is done with the other stage.  A bare
       // s_barrier: __syncthreads() would add a fence that waits for every outstanding vector
       // memory operation, i.e. also for the previous tile's epilogue stores kept in flight above.
