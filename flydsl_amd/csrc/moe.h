@@ -65,20 +65,19 @@ constexpr int moe_b_blk(int k) { return k == KIND_W4A16 ? 512 : (k == KIND_INT4 
 
 // Eight packed int4 weights of one 32-bit word (byte j holds element j in its low nibble and
 // element j + 4 in its high nibble, the dense int4 packing) -> eight bf16 in element order,
-// each times `s` when `scaled` (rounded to nearest even).
+// each times `s` when `scaled`.  The fp32 product becomes bf16 by truncation (its upper 16
+// bits), as the reference's conversion does (kernels/mfma_preshuffle_pipeline.py:111-141:
+// `bits >> 16` and `bits & 0xFFFF0000`); unscaled nibbles are exact either way.
 __device__ __forceinline__ i32x4 int4x8_to_bf16(uint32_t p, float s, bool scaled) {
-  float f[8];
+  uint32_t f[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const int off = k < 4 ? 8 * k : 8 * (k - 4) + 4;
     const int v = ((int)(p << (28 - off))) >> 28;   // sign-extended nibble
-    f[k] = scaled ? (float)v * s : (float)v;
+    f[k] = __builtin_bit_cast(uint32_t, scaled ? (float)v * s : (float)v);
   }
-  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-  bf16x8 o;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) o[k] = (__bf16)f[k];
-  return __builtin_bit_cast(i32x4, o);
+  return i32x4{(int)((f[0] >> 16) | (f[1] & 0xFFFF0000u)), (int)((f[2] >> 16) | (f[3] & 0xFFFF0000u)),
+               (int)((f[4] >> 16) | (f[5] & 0xFFFF0000u)), (int)((f[6] >> 16) | (f[7] & 0xFFFF0000u))};
 }
 
 // Stage-2 outputs: F16/BF16/F32 accumulate into out[token] with atomics; *_ROWS store each

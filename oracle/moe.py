@@ -85,8 +85,10 @@ def silu(x: np.ndarray) -> np.ndarray:
 def _expert_w(wq, sw, kind, rows: int, e: int, w_groups=None, w_round=None) -> np.ndarray:
     """Dequantized float64 weight rows [e*rows, (e+1)*rows) (one expert, on demand); with
     ``w_groups`` [E, K/g, rows] each (row, K group) has its own scale instead of ``sw``;
-    ``w_round="bf16"`` rounds those dequantized weights to bf16 (nearest even), the operand a
-    bf16 matrix instruction can take."""
+    ``w_round="bf16_trunc"`` turns those dequantized weights into bf16 by truncation, the bf16
+    matrix-instruction operand the reference's kernel forms from them
+    (``kernels/mfma_preshuffle_pipeline.py:111-141``); ``w_round="bf16"`` rounds to nearest
+    even instead."""
     lo, hi = e * rows, (e + 1) * rows
     if w_groups is not None:
         # the reference multiplies in float32 (an fp32 weight tensor scaled in place)
@@ -94,9 +96,9 @@ def _expert_w(wq, sw, kind, rows: int, e: int, w_groups=None, w_round=None) -> n
         gs = np.asarray(w_groups, dtype=np.float32)[e]            # [K/g, rows]
         g = v.shape[1] // gs.shape[0]
         wd = (v * np.repeat(gs.T, g, axis=1)).astype(np.float32)
-        if w_round == "bf16":
-            from .numerics import bf16_rne, bf16_to_f32
-            wd = bf16_to_f32(bf16_rne(wd))
+        if w_round in ("bf16", "bf16_trunc"):
+            from .numerics import bf16_rne, bf16_to_f32, bf16_trunc
+            wd = bf16_to_f32(bf16_rne(wd) if w_round == "bf16" else bf16_trunc(wd))
         return wd.astype(np.float64)
     return dequant_rows(np.asarray(wq)[lo:hi], None if sw is None else np.asarray(sw).reshape(-1)[lo:hi], kind,
                         np.float64)
@@ -142,9 +144,13 @@ def gemm1(x_q, w1_q, sx, sw1, topk_ids, topk_weights, inter_dim: int, doweight: 
 
 
 def gemm2(a2_q, w2_q, sa2, sw2, topk_ids, topk_weights, model_dim: int, doweight: bool, kind: str,
-          tokens_subset=None, w_kind=None, w_groups=None, w_round=None) -> np.ndarray:
+          tokens_subset=None, w_kind=None, w_groups=None, w_round=None, route_round=None) -> np.ndarray:
     """[tokens, model_dim] float64.  a2_q [tokens*topk, K] (row t*topk + s); w2_q [E*D, K]
-    unshuffled; sa2 [tokens*topk]; sw2 [E*D]; ``w_kind`` / ``w_groups`` [E, K/g, D] as in gemm1."""
+    unshuffled; sa2 [tokens*topk]; sw2 [E*D]; ``w_kind`` / ``w_groups`` [E, K/g, D] as in gemm1.
+    ``route_round`` ("bf16" / "f16"): the reduce mode -- each route's (weighted) row is written in
+    that type before the top-k sum (reference ``compile_moe_gemm2`` with ``accumulate=False``,
+    ``kernels/moe_gemm_2stage.py:1267-2481``, then ``compile_moe_reduction``, ``:2484-2604``,
+    which sums the rows in fp32)."""
     ids = np.asarray(topk_ids).astype(np.int64)
     T, topk = ids.shape
     E = np.asarray(w2_q).shape[0] // model_dim
@@ -161,8 +167,21 @@ def gemm2(a2_q, w2_q, sa2, sw2, topk_ids, topk_weights, model_dim: int, doweight
         y = a2[t_idx * topk + s_idx] @ _expert_w(w2_q, sw2, w_kind or kind, model_dim, e, w_groups, w_round).T
         if doweight:
             y = y * np.asarray(topk_weights, np.float64)[t_idx, s_idx][:, None]
+        if route_round is not None:
+            y = _round_rows(y, route_round)
         np.add.at(out, t_idx, y)
     return out
+
+
+def _round_rows(y: np.ndarray, dtype: str) -> np.ndarray:
+    """fp32 rows as the kernel holds them, rounded to bf16 / fp16 (nearest even)."""
+    from .numerics import bf16_rne, bf16_to_f32
+    y32 = np.asarray(y, dtype=np.float32)
+    if dtype == "bf16":
+        return bf16_to_f32(bf16_rne(y32)).astype(np.float64)
+    if dtype == "f16":
+        return y32.astype(np.float16).astype(np.float64)
+    raise ValueError(f"route_round {dtype!r}")
 
 
 def _sorted_routes(sorted_ids, sorted_eids, num_valid, block_size, tokens, topk):

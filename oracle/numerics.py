@@ -78,6 +78,13 @@ def bf16_rne(x: np.ndarray) -> np.ndarray:
     return out.astype(np.uint16)
 
 
+def bf16_trunc(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns (uint16) by truncation: the upper 16 bits, the
+    conversion of the reference's int8/int4 -> bf16 weight path
+    (``kernels/mfma_preshuffle_pipeline.py:111-141``, ``bits >> 16``)."""
+    return (np.asarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
 def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
     """bfloat16 bit patterns (uint16) -> float32."""
     return (np.asarray(bits).view(np.uint16).astype(np.uint32) << 16).view(np.float32)

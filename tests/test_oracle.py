@@ -73,6 +73,29 @@ def test_bf16_rne_matches_torch():
     assert np.array_equal(on.bf16_rne(exact), ref)
 
 
+def test_bf16_trunc_is_round_toward_zero():
+    """Truncation to bf16 (the reference's weight conversion) is rounding toward zero on the
+    bf16 grid: the result is the bf16 value of largest magnitude not above |x| with x's sign --
+    checked against math.frexp-based rounding of every value -- it keeps bf16 values unchanged,
+    and its relative error stays below 2^-7."""
+    import math
+    rng = np.random.default_rng(11)
+    x = np.concatenate([rng.standard_normal(20_000).astype(np.float32) * 37.0,
+                        np.array([1.0, -1.0, 3.0, 0.0, -0.0, 1.0 + 2 ** -7, 1.0 + 2 ** -8, -(1.0 + 2 ** -8)],
+                                 dtype=np.float32)])
+    got = on.bf16_to_f32(on.bf16_trunc(x))
+    for v, t in zip(x[:2000].tolist() + x[-8:].tolist(), got[:2000].tolist() + got[-8:].tolist()):
+        if v == 0:
+            assert t == 0
+            continue
+        m, e = math.frexp(abs(v))                     # |v| = m * 2^e, m in [0.5, 1)
+        want = math.floor(m * 256) / 256 * 2.0 ** e   # 8 significant bits, toward zero
+        assert t == math.copysign(want, v), (v, t)
+    assert np.array_equal(on.bf16_trunc(got), on.bf16_trunc(x))
+    nz = x != 0
+    assert np.all(np.abs(got[nz]) <= np.abs(x[nz])) and np.all(np.abs(got[nz] - x[nz]) < 2.0 ** -7 * np.abs(x[nz]))
+
+
 # ---------------------------------------------------------------- quantizers
 @pytest.mark.parametrize("kind", ["fp8", "int8", "int4"])
 def test_quant_rows_invariants(kind):
@@ -838,6 +861,35 @@ def test_moe_per_route_activations_reduce_to_per_token():
     ref = omoe.gemm1(x3, w1q, sx3, sw1, ids, w, I, False, "int8")
     diff = np.abs(c - ref).sum(axis=-1)
     assert diff[2, 1] > 0 and np.count_nonzero(diff) == 1
+
+
+def test_moe_gemm2_reduce_mode_rounds_each_route_row():
+    """Reduce mode: each route's weighted row is written in the output type and the rows are then
+    summed (compile_moe_gemm2(accumulate=False) + compile_moe_reduction).  Checked against a
+    brute-force loop over (token, slot) that rounds every row with torch's own conversion; with
+    float64 rows (no rounding) it is the atomic-mode sum."""
+    rng = np.random.default_rng(5)
+    T, k, E, D, I = 7, 3, 4, 32, 64
+    a2 = rng.integers(-127, 128, (T * k, I), dtype=np.int8)
+    w2 = rng.integers(-127, 128, (E * D, I), dtype=np.int8)
+    sa2 = rng.random(T * k).astype(np.float32) * 0.01
+    sw2 = rng.random(E * D).astype(np.float32) * 0.01
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    tw = rng.random((T, k)).astype(np.float32)
+    for rr, tdt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        got = omoe.gemm2(a2, w2, sa2, sw2, ids, tw, D, True, "int8", route_round=rr)
+        want = np.zeros((T, D))
+        for t in range(T):
+            for s_ in range(k):
+                e = ids[t, s_]
+                row = np.zeros(D)
+                for n in range(D):
+                    acc = sum(float(a2[t * k + s_, j]) * float(w2[e * D + n, j]) for j in range(I))
+                    row[n] = acc * float(sa2[t * k + s_]) * float(sw2[e * D + n]) * float(tw[t, s_])
+                want[t] += torch.from_numpy(row.astype(np.float32)).to(tdt).double().numpy()
+        assert np.allclose(got, want, rtol=1e-12, atol=0)
+    plain = omoe.gemm2(a2, w2, sa2, sw2, ids, tw, D, True, "int8")
+    assert not np.array_equal(plain, got) and np.allclose(plain, got, rtol=2e-3, atol=1e-3)
 
 
 def test_moe_group_scales_brute_force_and_per_row_reduction():
