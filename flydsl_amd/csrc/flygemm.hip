@@ -416,45 +416,6 @@ int launch(int kind, int epi, int out_dtype, int variant, const GemmArgs& args, 
   return 0;
 }
 
-// ---- GEMM with the activations quantized inside (the one-row-block decode shapes) ----------
-template <int MR, int NBW, int NW, int U, int KIND, bool BF16, int AQI>
-constexpr KernelFn aq_fn() {
-  if constexpr (MR == 1)
-    return gemm_decode_kernel<MR, NBW, NW, U, KIND, EPI_ROWCOL, BF16, true, AQI>;
-  else
-    return nullptr;
-}
-
-// one entry per decode shape (null for those of more than one 16-row block)
-template <int KIND, bool BF16, int AQI>
-const KernelFn* aq_row() {
-  static const KernelFn fns[] = {
-#define DQ(MR, NBW, NW, U) aq_fn<MR, NBW, NW, U, KIND, BF16, AQI>(),
-      DECODE_SHAPES(DQ)
-#undef DQ
-  };
-  return fns;
-}
-
-template <int KIND>
-const KernelFn* aq_rows(bool bf16_out, int aqi) {
-  if (aqi == AQ_F16) return bf16_out ? aq_row<KIND, true, AQ_F16>() : aq_row<KIND, false, AQ_F16>();
-  return bf16_out ? aq_row<KIND, true, AQ_BF16>() : aq_row<KIND, false, AQ_BF16>();
-}
-
-// The fused kernel for variant v, or null: fp16 / bf16 activations, the kind's fused mode
-// (aq_mode) and a decode shape of 16-row blocks.
-KernelFn aq_kernel(int kind, bool bf16_out, int x_dtype, int mode, int v) {
-  if (v < kFirstDecode || v >= kFirstRows) return nullptr;
-  if (x_dtype != FLYGEMM_QIN_F16 && x_dtype != FLYGEMM_QIN_BF16) return nullptr;
-  if (mode != aq_mode(kind)) return nullptr;
-  const int aqi = x_dtype == FLYGEMM_QIN_F16 ? AQ_F16 : AQ_BF16;
-  const KernelFn* row = kind == KIND_FP8    ? aq_rows<KIND_FP8>(bf16_out, aqi)
-                        : kind == KIND_INT8 ? aq_rows<KIND_INT8>(bf16_out, aqi)
-                                            : aq_rows<KIND_INT4>(bf16_out, aqi);
-  return row[v - kFirstDecode];
-}
-
 // ---- per-row quantization ------------------------------------------------------------
 typedef void (*QuantFn)(QuantArgs);
 
@@ -602,45 +563,25 @@ int flygemm_preshuffle_quant_a(void* c, void* a_q, float* scale_a, const void* x
   if (in_dtype == FLYGEMM_IN_INT4 && K >= kInt4KLimit)
     return fail(hipErrorInvalidValue, "K=%d: int4 weights take K < %d (int32 accumulators of 16x the dot product)", K,
                 kInt4KLimit);
-  const int xsz = x_dtype == FLYGEMM_QIN_F32 ? 4 : 2;
-  if ((long)(M + 16) * K * xsz >= (1L << 31))
-    return fail(hipErrorInvalidValue, "activations too large for 32-bit offsets (M=%d K=%d)", M, K);
   if (out_dtype != FLYGEMM_OUT_BF16 && out_dtype != FLYGEMM_OUT_FP16)
     return fail(hipErrorInvalidValue, "out_dtype %d not supported", out_dtype);
   if (M > 0 && !scale_b) return fail(hipErrorInvalidValue, "null scale pointer");
   if (M == 0) return 0;
-  // the same alignment on both paths below: 16-byte activation loads, 8-byte code stores
+  if (!a_q || !scale_a)
+    return fail(hipErrorInvalidValue, "a_q [M][K] and scale_a [M] are required: the quantization and the GEMM run as two "
+                "launches through them");
   if (((uintptr_t)x & 15) || ((uintptr_t)a_q & 7) || ((uintptr_t)scale_a & 3))
     return fail(hipErrorInvalidValue, "misaligned pointer (x needs 16-byte, a_q 8-byte, scale_a 4-byte alignment)");
   const int qout = in_dtype == FLYGEMM_IN_FP8 ? FLYGEMM_QOUT_FP8 : FLYGEMM_QOUT_INT8;
-  const int v = variant >= 0 ? variant : select_variant(M, N, kb, in_dtype, EPI_ROWCOL);
-  if (v < 0 || v >= kNumShapes) return fail(hipErrorInvalidValue, "no kernel variant for M=%d N=%d K=%d", M, N, K);
-  // One fused launch when the caller forces a fused decode variant or gives no buffers for the
-  // codes and scales; otherwise the quant kernel and the GEMM, through those buffers.  Measured
-  // on MI355X (graph replay, bf16 activations): the two launches are as fast or faster --
-  // int8 16x28672x8192 41.2 us against 41.7 fused, 1x7168x2048 5.2 against 7.8; fp8, whose
-  // codes need a true division per element, 42.8 against 77.8 -- because every column group's
-  // workgroup re-derives its rows' scales and codes, which the quant kernel does once.
-  const KernelFn fn = aq_kernel(in_dtype, out_dtype == FLYGEMM_OUT_BF16, x_dtype, mode, v);
-  const bool buffers = a_q != nullptr && scale_a != nullptr;
-  if (!fn || (buffers && variant < 0)) {
-    if (!buffers)
-      return fail(hipErrorInvalidValue,
-                  "M=%d with variant %s, x_dtype %d and mode %d has no fused kernel: the quantization and the "
-                  "GEMM run as two launches, which need a_q [M][K] and scale_a [M]", M, kShapes[v].name, x_dtype,
-                  mode);
-    rc = flygemm_quant_rows(a_q, scale_a, x, M, K, x_dtype, qout, mode, stream);
-    if (rc) return rc;
-    return flygemm_preshuffle(c, a_q, b, scale_a, scale_b, M, N, K, in_dtype, out_dtype, v, stream);
-  }
-  GemmArgs args{c, (const uint8_t*)x, (const uint8_t*)b, nullptr, scale_b, M, N, kb, (uint8_t*)a_q, scale_a};
-  const Shape& s = kShapes[v];
-  const long nrb = (M + s.bm - 1) / s.bm;
-  const long ncg = (N / 16 + s.bn / 16 - 1) / (s.bn / 16);
-  hipLaunchKernelGGL(fn, dim3((unsigned)(nrb * ncg)), dim3(s.threads), 0, (hipStream_t)stream, args);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(e, "launch of %s (fused quantization) failed: %s", s.name, hipGetErrorString(e));
-  return 0;
+  // Two launches: the quant kernel writes the codes and row scales once, then the GEMM reads
+  // them.  A single kernel that quantized A inside the decode GEMM was built and measured on
+  // MI355X (graph replay, bf16 activations): every column group's workgroup re-derives the
+  // codes and scales of all its rows, work the quant kernel does once, so it never won --
+  // int8 16x28672x8192 41.7 us against 41.2 for the pair, 1x7168x2048 7.8 against 5.2, fp8
+  // (a true division per element) 77.8 against 42.8 -- and it was removed.
+  rc = flygemm_quant_rows(a_q, scale_a, x, M, K, x_dtype, qout, mode, stream);
+  if (rc) return rc;
+  return flygemm_preshuffle(c, a_q, b, scale_a, scale_b, M, N, K, in_dtype, out_dtype, variant, stream);
 }
 
 int flygemm_mxfp4(void* c, const void* a, const void* b, const void* scale_a, const void* scale_b, int32_t M,

@@ -170,11 +170,6 @@ struct GemmArgs {
   const float* sa;    // EPI_ROWCOL: [M]; EPI_BLOCK: [K/128][M]
   const float* sb;    // EPI_ROWCOL: [N]; EPI_BLOCK: [ceil(N/128)][K/128]
   int M, N, K;
-  // kernels that quantize A themselves (the fused decode kernel): `a` holds 16-bit
-  // activations, quantized per row as the quant_rows kernel does; the codes and scales they
-  // produce also go to a_q / sa_out when those are set
-  uint8_t* a_q;
-  float* sa_out;
 };
 
 }  // namespace flygemm

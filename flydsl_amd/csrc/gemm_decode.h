@@ -20,16 +20,8 @@
 // matching two chunks of A row (lane%16).  As in the large-M kernel, B is the MFMA's first
 // operand, so a lane ends with row (lane%16) and four consecutive columns.
 //
-// AQ (fused activation quantization, one row block of 16 rows): A arrives as fp16/bf16
-// activations.  Each workgroup first takes its rows' amax and per-row scale exactly as the
-// quant_rows kernel does (the same conversion, scrubbing and scale expressions), then its
-// pipeline loads 16-bit A chunks (twice the bytes of the codes, from L2: A is a few hundred
-// KB) and quantizes each K tile in registers right before the MFMAs, so the codes and the
-// epilogue's row scales are those of quant_rows followed by the GEMM.  The workgroup of the
-// first column group also writes the codes and scales out when asked.
 #pragma once
 #include "gemm_common.h"
-#include "quant_rows.h"
 
 namespace flygemm {
 
@@ -43,22 +35,8 @@ __device__ __forceinline__ T load_b(const T* p) {
     return *p;
 }
 
-// AQ_NONE: A holds codes; AQ_F16 / AQ_BF16: A holds activations of that type, quantized in the
-// kernel with the kind's mode (aq_mode).
-enum AqIn : int { AQ_NONE = 0, AQ_F16 = 1, AQ_BF16 = 2 };
-// the quantization a fused kernel performs: fp8 codes round to nearest (the only fp8 rule);
-// int8 codes as the reference's quant kernel makes them, fptosi of x * (1 / scale)
-constexpr int aq_mode(int kind) { return kind == KIND_FP8 ? QMODE_DIV_NEAREST : QMODE_RECIP_TRUNC; }
-
-template <int MR, int NBW, int NW, int UNROLL, int KIND, int EPI, bool OUT_BF16, bool NT_B = true,
-          int AQI = AQ_NONE>
+template <int MR, int NBW, int NW, int UNROLL, int KIND, int EPI, bool OUT_BF16, bool NT_B = true>
 __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
-  constexpr bool AQ = AQI != AQ_NONE;
-  static_assert(!AQ || (MR == 1 && EPI == EPI_ROWCOL && (KIND == KIND_FP8 || KIND == KIND_INT8 || KIND == KIND_INT4)),
-                "fused activation quantization: one row block, fp8 / int8 codes, row-column scaling");
-  constexpr int QI = AQI == AQ_F16 ? QIN_F16 : QIN_BF16;   // the activations' QuantIn
-  constexpr int QM = aq_mode(KIND);
-  constexpr int AES = AQ ? 2 : 1;  // bytes per A element as loaded
   const int M = p.M, N = p.N, K = p.K;
   // full 128-byte K tiles; K (bytes) is a multiple of 64, and when K % 128 == 64 the last 64
   // bytes form a half tile, taken after the pipeline (see below)
@@ -99,7 +77,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
 
   const uint8_t* arow[MR];
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) arow[mi] = p.a + ((size_t)min(m0 + mi * 16 + l16, M - 1) * K + lq * 16) * AES;
+  for (int mi = 0; mi < MR; ++mi) arow[mi] = p.a + (size_t)min(m0 + mi * 16 + l16, M - 1) * K + lq * 16;
   const uint8_t* bblk[NBW];
 #pragma unroll
   for (int j = 0; j < NBW; ++j) {
@@ -115,7 +93,6 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
   // multiplied; the stage index is a compile-time constant inside the unrolled body.
   struct Stage {
     i32x4 alo[MR], ahi[MR];
-    i32x4 alo2[AQ ? MR : 1], ahi2[AQ ? MR : 1];  // AQ: the second 16 bytes of each 16-bit chunk
     i32x4 blo[NBW], bhi[NBW];
     i32x2 b4lo[NBW], b4hi[NBW];
     float sa[MR], sb[NBW];  // blockscale: this K tile's A scale per row block, B scale per column block
@@ -136,15 +113,9 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int mi = 0; mi < MR; ++mi) {
-      const uint8_t* src = arow[mi] + (size_t)kt * KT * AES;
+      const uint8_t* src = arow[mi] + (size_t)kt * KT;
       s.alo[mi] = *(const i32x4*)src;
-      if constexpr (AQ) {
-        s.alo2[mi] = *(const i32x4*)(src + 16);
-        s.ahi[mi] = *(const i32x4*)(src + 128);
-        s.ahi2[mi] = *(const i32x4*)(src + 144);
-      } else {
-        s.ahi[mi] = *(const i32x4*)(src + 64);
-      }
+      s.ahi[mi] = *(const i32x4*)(src + 64);
     }
     // blockscale / MXFP4 scales travel with the stage, so their latency hides behind the pipeline
     if constexpr (KIND == KIND_FP4) {
@@ -169,45 +140,9 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       for (int j = 0; j < NBW; ++j) s.sb[j] = p.sb[(size_t)(min((nb0 + j) * 16, N - 1) >> 7) * nk + kt];
     }
   };
-  // AQ: this lane's row scale and its reciprocal (quant_rows' expressions), set below
-  float q_scale[MR], q_inv[MR];
-  // AQ: the codes of this lane's two 16-element chunks of K tile kt (hi only for a whole K
-  // tile).  No memory operation here: a store under a condition in the pipeline makes the
-  // compiler's wait counting drain every load in flight (the codes a caller asks for are
-  // written before the pipeline, below).
-  auto quantize = [&](const Stage& s, int kt, i32x4* qlo, i32x4* qhi) {
-    if constexpr (AQ) {
-      constexpr int QO = KIND == KIND_FP8 ? QOUT_FP8 : QOUT_INT8;
-      constexpr float QMAX = KIND == KIND_FP8 ? 448.f : 127.f;
-      auto q16 = [&](i32x4 w0, i32x4 w1, float sc, float inv) -> i32x4 {
-        const f32x8 v0 = prepare8<QM>(cvt8_16<QI>(__builtin_bit_cast(u32x4q, w0)), QMAX);
-        const f32x8 v1 = prepare8<QM>(cvt8_16<QI>(__builtin_bit_cast(u32x4q, w1)), QMAX);
-        const uint2 c0 = quant8<QO, QM>(v0, sc, inv), c1 = quant8<QO, QM>(v1, sc, inv);
-        return i32x4{(int)c0.x, (int)c0.y, (int)c1.x, (int)c1.y};
-      };
-      const bool whole = (kt + 1) * KT <= K;
-#pragma unroll
-      for (int mi = 0; mi < MR; ++mi) {
-        const int row = m0 + mi * 16 + l16;
-        // lanes of rows past M (never stored) give zero codes without converting
-        qlo[mi] = qhi[mi] = i32x4{0, 0, 0, 0};
-        if (row < M) {
-          qlo[mi] = q16(s.alo[mi], s.alo2[mi], q_scale[mi], q_inv[mi]);
-          if (whole) qhi[mi] = q16(s.ahi[mi], s.ahi2[mi], q_scale[mi], q_inv[mi]);
-        }
-      }
-    }
-  };
   auto compute = [&](const Stage& s, int kt) {
-    // A fragments: the stage's codes, or (AQ) the codes quantized from its 16-bit chunks
-    i32x4 qlo[AQ ? MR : 1], qhi[AQ ? MR : 1];
-    if constexpr (AQ) quantize(s, kt, qlo, qhi);
-    auto a_lo = [&](int mi) -> const i32x4& {
-      if constexpr (AQ) return qlo[mi]; else return s.alo[mi];
-    };
-    auto a_hi = [&](int mi) -> const i32x4& {
-      if constexpr (AQ) return qhi[mi]; else return s.ahi[mi];
-    };
+    auto a_lo = [&](int mi) -> const i32x4& { return s.alo[mi]; };
+    auto a_hi = [&](int mi) -> const i32x4& { return s.ahi[mi]; };
     if constexpr (KIND == KIND_FP8) {
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) {
@@ -256,60 +191,6 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
     }
   };
 
-  // AQ: each row's amax over K and its scale, as quant_rows takes them (NaN / inf scrubbed for
-  // the host quantizer's modes, amax / qmax, 1 for an all-zero row).  The NW*64 threads split
-  // the 16 rows 32 threads a row (two rows a wave), each thread keeping 8 independent 16-byte
-  // loads in flight; the max is order-free, so the scales are quant_rows' own.  The first
-  // column group's workgroup also writes the scales out.
-  if constexpr (AQ) {
-    static_assert(NW * 64 == 16 * MR * 32, "32 threads per row of the block");
-    constexpr float QMAX = KIND == KIND_FP8 ? 448.f : 127.f;
-    __shared__ float q_rows[16 * MR];
-    const int r = tid >> 5, sub = tid & 31;
-    const uint8_t* base = p.a + (size_t)min(m0 + r, M - 1) * K * 2;
-    float mx[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    // rows past M (never stored) take no pass: scale 1.  Loads past K re-read the row's first
-    // chunk (unconditional loads keep the compiler's wait counting exact)
-    for (int col0 = sub * 8; col0 < (m0 + r < M ? K : 0); col0 += 8 * 256) {
-      u32x4q w[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int col = col0 + u * 256;
-        w[u] = *(const u32x4q*)(base + (size_t)(col < K ? col : sub * 8) * 2);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) mx[u] = __builtin_fmaxf(mx[u], absmax8(prepare8<QM>(cvt8_16<QI>(w[u]), QMAX)));
-    }
-    float m = mx[0];
-#pragma unroll
-    for (int u = 1; u < 8; ++u) m = __builtin_fmaxf(m, mx[u]);
-#pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off, 64));
-    float scale = m / QMAX;
-    if (scale == 0.f) scale = 1.f;
-    if (sub == 0) {
-      q_rows[r] = scale;
-      if (p.sa_out != nullptr && nb0 == 0 && m0 + r < M) p.sa_out[m0 + r] = scale;
-    }
-    // the codes, when asked for: the first column group's workgroup quantizes its rows once
-    // more with the same functions (the pipeline below recomputes the same codes)
-    if (p.a_q != nullptr && nb0 == 0 && m0 + r < M) {
-      const float inv = 1.f / scale;
-      uint8_t* qrow = p.a_q + (size_t)(m0 + r) * K;
-      for (int col = sub * 8; col < K; col += 256) {
-        const u32x4q w = *(const u32x4q*)(base + (size_t)col * 2);
-        constexpr int QO = KIND == KIND_FP8 ? QOUT_FP8 : QOUT_INT8;
-        *(uint2*)(qrow + col) = quant8<QO, QM>(prepare8<QM>(cvt8_16<QI>(w), QMAX), scale, inv);
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mi = 0; mi < MR; ++mi) {
-      q_scale[mi] = q_rows[mi * 16 + l16];
-      q_inv[mi] = 1.f / q_scale[mi];
-    }
-  }
-
   // The half K tile (index nk), taken first by the wave whose K tiles it continues (nk % NW),
   // before the pipeline's registers are in use: its lower 64 bytes (A chunks 0-3, B chunks 0-3)
   // are loaded and the upper halves are zeros, so the second 64-deep MFMA (and the upper half
@@ -331,11 +212,9 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
       }
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) {
-        const uint8_t* src = arow[mi] + (size_t)nk * KT * AES;
+        const uint8_t* src = arow[mi] + (size_t)nk * KT;
         s.alo[mi] = *(const i32x4*)src;
-        if constexpr (AQ) s.alo2[mi] = *(const i32x4*)(src + 16);
         s.ahi[mi] = i32x4{0, 0, 0, 0};
-        if constexpr (AQ) s.ahi2[mi] = i32x4{0, 0, 0, 0};
       }
       compute(s, nk);
     }
@@ -383,10 +262,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
         *(AccT*)((AccE*)p.c + idx) = s;
       } else {
         float s_a = 1.f;
-        if constexpr (AQ)
-          s_a = q_scale[mi];
-        else if constexpr (kScaled)
-          s_a = p.sa[row];
+        if constexpr (kScaled) s_a = p.sa[row];
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {

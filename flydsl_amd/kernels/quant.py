@@ -14,9 +14,8 @@ Two interfaces over ``flygemm_quant_rows`` (``include/flygemm.h``):
   reference's ``.to(torch.int8)``); fp8 (``torch.float8_e4m3fn``) rounds to nearest even.
 
 * ``quant_gemm(x, b, scale_b, N, in_dtype=...)`` -- the GEMM of activations quantized on the
-  way in (``flygemm_preshuffle_quant_a``): the same result as ``per_token_quant`` followed by
-  the preshuffle GEMM launcher, bit for bit, with one kernel for decode-sized M that quantizes
-  A in registers while it streams B.
+  way in (``flygemm_preshuffle_quant_a``): ``per_token_quant`` (or the reference kernel's
+  mode) followed by the preshuffle GEMM launcher, in one call.
 
 All fail loudly if the HIP library is missing; there is no host fallback.
 """
@@ -109,17 +108,14 @@ _GEMM_OUT = {"bf16": torch.bfloat16, "fp16": torch.float16}
 
 
 def quant_gemm(x: torch.Tensor, b, scale_b, N: int, *, in_dtype: str = "fp8", out_dtype: str = "bf16",
-               mode: str = "div_nearest", out=None, a_q=None, scale_a=None, fused: bool = False,
-               variant: int = -1, stream=None):
+               mode: str = "div_nearest", out=None, a_q=None, scale_a=None, variant: int = -1, stream=None):
     """``C[M, N] = GEMM(quant(x), B)`` with ``x`` [M, K] fp16 / bf16 / fp32 quantized per row to
     fp8 (``in_dtype="fp8"``) or int8 codes (``"int8"``, or ``"int4"`` for packed int4 weights),
-    ``b`` the preshuffled weight bytes and ``scale_b`` [N] fp32, as ``per_token_quant`` (mode
+    ``b`` the preshuffled weight bytes and ``scale_b`` [N] fp32: ``per_token_quant`` (mode
     ``"div_nearest"`` / ``"div_trunc"``) or the reference's quant kernel (``"recip_trunc"``)
-    followed by ``compile_preshuffle_gemm_a8``'s launcher.  Returns ``(out, a_q, scale_a)``.
-    With ``fused=True`` no code or scale buffers are passed (unless given) and the library runs
-    its one-launch kernel (decode-sized M, fp16/bf16 x, the kind's fused mode: fp8
-    ``"div_nearest"``, int8/int4 ``"recip_trunc"``); otherwise ``a_q`` [M, K] and ``scale_a``
-    [M, 1] are allocated when not given and the quant kernel and the GEMM run as two launches."""
+    followed by ``compile_preshuffle_gemm_a8``'s launcher, in one call to the library (two
+    launches on ``stream``).  ``a_q`` [M, K] and ``scale_a`` [M, 1] receive the codes and the
+    row scales; they are allocated when not given.  Returns ``(out, a_q, scale_a)``."""
     if x.dim() != 2:
         raise ValueError(f"x must be 2-D [M, K], got shape {tuple(x.shape)}")
     if x.dtype not in _QIN:
@@ -135,14 +131,14 @@ def quant_gemm(x: torch.Tensor, b, scale_b, N: int, *, in_dtype: str = "fp8", ou
     qdt = torch.float8_e4m3fn if in_dtype == "fp8" else torch.int8
     if out is None:
         out = torch.empty(M, N, dtype=_GEMM_OUT[out_dtype], device=x.device)
-    if a_q is None and not fused:
+    if a_q is None:
         a_q = torch.empty(M, K, dtype=qdt, device=x.device)
-    if scale_a is None and not fused:
+    if scale_a is None:
         scale_a = torch.empty(M, 1, dtype=torch.float32, device=x.device)
     b_elems = N * K // 2 if in_dtype == "int4" else N * K
     c = device_ptr(out, "out", M * N, dtypes=(_GEMM_OUT[out_dtype],))
-    q = device_ptr(a_q, "a_q", M * K, elem_bytes=1) if a_q is not None else None
-    sa = device_ptr(scale_a, "scale_a", M, dtypes=(torch.float32,)) if scale_a is not None else None
+    q = device_ptr(a_q, "a_q", M * K, elem_bytes=1)
+    sa = device_ptr(scale_a, "scale_a", M, dtypes=(torch.float32,))
     xi = device_ptr(x, "x", M * K, dtypes=(x.dtype,))
     bp = device_ptr(b, "b", b_elems, elem_bytes=1)
     sb = device_ptr(scale_b, "scale_b", N, dtypes=(torch.float32,))

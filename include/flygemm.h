@@ -10,8 +10,9 @@
  *  - All pointers are device pointers the caller allocated.  Launches are asynchronous on
  *    `stream` (a hipStream_t, NULL = default stream).  Callers keep buffers alive until the
  *    stream has finished.  Nothing is allocated, freed or synchronized here, and every GEMM is
- *    one kernel launch (a K split over the waves of a workgroup is summed in LDS), so every
- *    entry point may be captured into a HIP graph on any stream.
+ *    one kernel launch (a K split over the waves of a workgroup is summed in LDS;
+ *    flygemm_preshuffle_quant_a launches the quant kernel and then the GEMM), so every entry
+ *    point may be captured into a HIP graph on any stream.
  *  - A is row-major [M][K] bytes.  B is the preshuffled [N][K] buffer produced by the
  *    reference's `shuffle_weight(b, layout=(16, 16))` (tests/utils.py:76-96): element
  *    (n, k) at byte (n/16)*16*K + (k/16)*256 + (n%16)*16 + (k%16).  INT4 B is that buffer
@@ -106,20 +107,15 @@ enum { FLYGEMM_QMODE_RECIP_TRUNC = 0, FLYGEMM_QMODE_DIV_TRUNC = 1, FLYGEMM_QMODE
 int flygemm_quant_rows(void* out, float* scales, const void* in, int32_t M, int32_t N, int32_t in_dtype,
                        int32_t out_dtype, int32_t mode, void* stream);
 
-/* The GEMM of activations quantized per row on the way in: the result equals
- *   flygemm_quant_rows(a_q, scale_a, x, M, K, x_dtype, fp8 or int8 codes, mode) followed by
+/* The GEMM of activations quantized per row on the way in, in one call:
+ *   flygemm_quant_rows(a_q, scale_a, x, M, K, x_dtype, fp8 or int8 codes, mode), then
  *   flygemm_preshuffle(c, a_q, b, scale_a, scale_b, M, N, K, in_dtype, out_dtype, variant)
- * bit for bit (the quant kernel of tests/kernels/test_quant.py:81-265 or pertoken_quant of
+ * on `stream` (the quant kernel of tests/kernels/test_quant.py:81-265 or pertoken_quant of
  * tests/utils.py:29-73, then the launcher of kernels/preshuffle_gemm.py:1268-1301).  x: [M][K]
- * FLYGEMM_QIN_* activations; in_dtype FLYGEMM_IN_FP8 (mode must be _DIV_NEAREST), _INT8 or
- * _INT4 (int8 codes); mode and scale_b as for those entries.  Fused kernel: for a decode
- * variant of 16-row blocks, fp16/bf16 x and the kind's fused mode (fp8: _DIV_NEAREST; int8 and
- * int4: _RECIP_TRUNC, the reference's quant kernel), one launch in which each workgroup derives
- * its rows' scales and quantizes A in registers as it streams B.  It runs when the caller
- * forces such a variant or passes a_q / scale_a as NULL; otherwise (the faster path on MI355X
- * wherever measured) the quant kernel and the GEMM run as two launches through a_q [M][K] and
- * scale_a [M], which are then required.  a_q / scale_a, when given, receive the codes and
- * scales either way.  No allocation; asynchronous on `stream`. */
+ * FLYGEMM_QIN_* activations, 16-byte aligned; in_dtype FLYGEMM_IN_FP8 (mode must be
+ * _DIV_NEAREST), _INT8 or _INT4 (int8 codes); mode and scale_b as for those entries; a_q [M][K]
+ * (8-byte aligned) and scale_a [M] receive the codes and the row scales and are required.
+ * No allocation; asynchronous on `stream`.  Every check runs before the first launch. */
 int flygemm_preshuffle_quant_a(void* c, void* a_q, float* scale_a, const void* x, const void* b, const float* scale_b,
                                int32_t M, int32_t N, int32_t K, int32_t x_dtype, int32_t in_dtype, int32_t mode,
                                int32_t out_dtype, int32_t variant, void* stream);

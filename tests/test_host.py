@@ -182,11 +182,13 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc != 0 and b"in_dtype" in lib.flygemm_last_error()
     rc = lib.flygemm_quant_rows(ctypes.c_void_p(17), p, p, 4, 64, 0, 1, 0, None)
     assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
-    # the GEMM that quantizes its activations checks alignment before it picks its path (fused
-    # kernel or quant + GEMM): x 16 bytes, a_q 8, scale_a 4
+    # the GEMM that quantizes its activations checks its buffers and their alignment before its
+    # first launch: x 16 bytes, a_q 8, scale_a 4; the code and scale buffers are required
     for x, aq, sa in [(ctypes.c_void_p(24), p, p), (p, ctypes.c_void_p(20), p), (p, p, ctypes.c_void_p(18))]:
         rc = lib.flygemm_preshuffle_quant_a(p, aq, sa, x, p, p, 16, 128, 256, 0, 1, 0, 0, -1, None)
         assert rc != 0 and b"misaligned" in lib.flygemm_last_error()
+    rc = lib.flygemm_preshuffle_quant_a(p, None, None, p, p, p, 16, 128, 256, 0, 1, 0, 0, -1, None)
+    assert rc != 0 and b"required" in lib.flygemm_last_error()
     assert lib.flygemm_quant_rows(p, p, p, 0, 64, 0, 1, 0, None) == 0
     # 16-bit inputs: K counts elements and must be a multiple of 32; scales are not needed
     rc = lib.flygemm_preshuffle(p, p, p, None, None, 16, 128, 80, 3, 0, -1, None)
