@@ -342,13 +342,14 @@ def traffic_from_profile(name: str):
     return None
 
 
-def gfx_clock_under(work, dev, seconds=0.5):
-    """Median shader clock (MHz) while ``work`` (a graph replay on the current stream) runs: a
-    one-wave probe on a side stream counts core cycles (s_memtime) against the 100 MHz constant
-    counter for 100 us (``flydsl_amd/_clockprobe.so``).  A sample counts only if the probe ended
-    before the replay did (a second, one-tick probe queued behind the replay on its stream
-    gives the replay's end), so the clock is the one under load.  None if the probe is not built
-    or no sample overlapped."""
+def gfx_clock_under(work, dev, work_ms, seconds=0.5):
+    """Median shader clock (MHz) while ``work`` (a graph replay on the current stream, about
+    ``work_ms`` long) runs: a one-wave probe on a side stream counts core cycles (s_memtime)
+    against the 100 MHz constant counter over half the replay, at most 2 ms, so each sample
+    averages the clock over many launches (``flydsl_amd/_clockprobe.so``).  A sample counts
+    only if the probe ended before the replay did (a second, one-tick probe queued behind the
+    replay on its stream gives the replay's end), so the clock is the one under load.  None if
+    the probe is not built or no sample overlapped."""
     import ctypes
 
     from flydsl_amd.build import PROBE_OUT
@@ -365,7 +366,8 @@ def gfx_clock_under(work, dev, seconds=0.5):
     while (time.perf_counter() - t0 < seconds or len(vals) < 5) and tries < 200:
         tries += 1
         work()
-        if probe(out.data_ptr(), 10000, side.cuda_stream) or probe(end.data_ptr(), 1, main.cuda_stream):
+        ticks = max(1000, min(200000, int(work_ms * 0.5 * 1e5)))   # 100 MHz ticks
+        if probe(out.data_ptr(), ticks, side.cuda_stream) or probe(end.data_ptr(), 1, main.cuda_stream):
             return None
         torch.cuda.synchronize()
         cyc, ticks, _, r_end = out.tolist()
@@ -579,7 +581,7 @@ def main():
                 cap = torch.cuda.current_stream()
                 for i in range(n2):
                     r2.launch(i, cap)
-            clk = gfx_clock_under(g.replay, dev)
+            clk = gfx_clock_under(g.replay, dev, ms2 * n2)
             del g
             if clk:
                 # the dense peak assumes 2.4 GHz; under sustained MFMA load the chip holds less
