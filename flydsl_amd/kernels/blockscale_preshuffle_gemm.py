@@ -52,14 +52,23 @@ class BlockscaleGemm:
         _lib.check(rc, "flygemm_blockscale")
 
     def _bind(self):
-        """The launch without the per-call checks, for ``flydsl_amd.compile`` (as
+        """The launch with only its bounds checks, for ``flydsl_amd.compile`` (as
         ``PreshuffleGemm._bind``)."""
         fn = _lib.load().flygemm_blockscale
         K, sbk, out, var = self.K, self.scale_block_k, _lib.FLYGEMM_OUT[self.out_dtype], self.variant
+        sk = K // sbk
         check = _lib.check
+
+        last = [None] * 7
 
         def call(c, a, b, sa, sb, M, N, stream=None):
             s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
+            if not (c is last[0] and a is last[1] and b is last[2] and sa is last[3] and sb is last[4]
+                    and M == last[5] and N == last[6]):
+                if (c.numel() < M * N or a.numel() < M * K or b.numel() < N * K or sa.numel() < M * sk
+                        or sb.numel() < (N + 127) // 128 * sk):
+                    raise ValueError(f"a tensor is too small for M={M}, N={N}, K={K}")
+                last[:] = (c, a, b, sa, sb, M, N)
             rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, sbk, out, var, s)
             if rc:
                 check(rc, "flygemm_blockscale")

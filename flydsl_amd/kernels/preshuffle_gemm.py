@@ -90,37 +90,44 @@ class PreshuffleGemm:
         _lib.check(rc, "flygemm_preshuffle")
 
     def _bind(self):
-        """The launch without the per-call checks, for ``flydsl_amd.compile``: tensor data
-        pointers, M, N and the stream are read per call and go straight to the C entry point
-        (which still checks the sizes); dtypes, contiguity and capacities are the caller's, as
-        in the reference's ``CompiledFunction`` (python/flydsl/compiler/jit_function.py:895-915)."""
+        """The launch with only the checks that keep it in bounds, for ``flydsl_amd.compile``:
+        tensor data pointers, M, N and the stream are read per call and go straight to the C
+        entry point (which checks the sizes), after one comparison of each tensor's element
+        count with what M, N and K need (skipped when the same tensor objects and sizes come
+        again); dtypes and contiguity are the caller's, as in the reference's
+        ``CompiledFunction`` (python/flydsl/compiler/jit_function.py:895-915)."""
         lib = _lib.load()
         K, var, out = self.K, self.variant, _lib.FLYGEMM_OUT[self.out_dtype]
         check = _lib.check
-        if self.in_dtype == "fp4":
-            fn = lib.flygemm_mxfp4
+        fp4 = self.in_dtype == "fp4"
+        scaled = self.in_dtype not in _IN_TORCH16
+        fn = lib.flygemm_mxfp4 if fp4 else lib.flygemm_preshuffle
+        what = "flygemm_mxfp4" if fp4 else "flygemm_preshuffle"
+        ind = None if fp4 else _lib.FLYGEMM_IN[self.in_dtype]
+        # elements per row of A and B, and scale elements per row of A / of B, as the launcher
+        # checks them (MXFP4 scales: bytes over rows padded to 32)
+        ka = K // 2 if fp4 else K
+        kb = K // 2 if fp4 or self.in_dtype == "int4" else K
+        ks = K // 32 if fp4 else 1
 
-            def call(c, a, b, sa, sb, M, N, stream=None):
-                s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
-                rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, out, var, s)
-                if rc:
-                    check(rc, "flygemm_mxfp4")
-            return call
-        fn = lib.flygemm_preshuffle
-        ind = _lib.FLYGEMM_IN[self.in_dtype]
-        if self.in_dtype in _IN_TORCH16:
-            def call(c, a, b, sa, sb, M, N, stream=None):
-                s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
-                rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), None, None, M, N, K, ind, out, var, s)
-                if rc:
-                    check(rc, "flygemm_preshuffle")
-            return call
+        last = [None] * 7   # the tensors and sizes of the last call that passed the checks
 
         def call(c, a, b, sa, sb, M, N, stream=None):
             s = 0 if stream is None else (stream if type(stream) is int else stream.cuda_stream)
-            rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, ind, out, var, s)
+            if not (c is last[0] and a is last[1] and b is last[2] and sa is last[3] and sb is last[4]
+                    and M == last[5] and N == last[6]):
+                if (c.numel() < M * N or a.numel() < M * ka or b.numel() < N * kb
+                        or (scaled and (sa.numel() < ((M + 31) // 32 * 32 if fp4 else M) * ks
+                                        or sb.numel() < N * ks))):
+                    raise ValueError(f"a tensor is too small for M={M}, N={N}, K={K}")
+                last[:] = (c, a, b, sa, sb, M, N)
+            if fp4:
+                rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr(), sb.data_ptr(), M, N, K, out, var, s)
+            else:
+                rc = fn(c.data_ptr(), a.data_ptr(), b.data_ptr(), sa.data_ptr() if scaled else None,
+                        sb.data_ptr() if scaled else None, M, N, K, ind, out, var, s)
             if rc:
-                check(rc, "flygemm_preshuffle")
+                check(rc, what)
         return call
 
     def _call_fp4(self, arg_c, arg_a, arg_b, arg_scale_a, arg_scale_b, M, N, stream=None):

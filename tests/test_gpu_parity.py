@@ -353,3 +353,5 @@ def test_compiled_fast_path_matches_launcher(gpu):
         assert torch.equal(c1, want1)
     with pytest.raises(RuntimeError, match="multiple of 16"):   # the C entry still checks sizes
         cf(*args(first, c1), 64, 100, None)
+    with pytest.raises(ValueError, match="too small"):          # and every tensor's capacity
+        cf(*args(first, c1), 65, N, None)
