@@ -26,9 +26,9 @@ def compile(launch_fn, *args):
     """The reference's ``flyc.compile(fn, *args)`` (``python/flydsl/compiler/jit_function.py:
     917-954``): run ``launch_fn(*args)`` once -- with every argument check -- and return a
     :class:`CompiledFunction` that repeats the launch for new tensors, M, N and stream with only
-    a capacity check of each tensor (no dtype, device or layout checks).  The kernels are built ahead of time, so nothing is compiled here;
-    launchers of this package are pre-bound to their C entry point, any other callable is
-    returned as it is after the first call."""
+    a capacity check of each tensor (no dtype, device or layout checks).  The kernels are built
+    ahead of time, so nothing is compiled here; launchers of this package are pre-bound to their
+    C entry point, any other callable is returned as it is after the first call."""
     launch_fn(*args)
     bind = getattr(launch_fn, "_bind", None)
     if bind is None:
