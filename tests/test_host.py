@@ -462,3 +462,15 @@ def test_compile_validates_on_first_call():
     plain = lambda *a: seen.append(a)   # noqa: E731
     assert flydsl_amd.compile(plain, 1, 2) is plain and seen == [(1, 2)]
 
+
+
+def test_cpu_baseline_dispatches_on_the_kind():
+    """bench.py's CPU baseline runs the reference's CPU path for each kind: per-row scales
+    (fp8, int8, int4), the 1x128 / 128x128 block expansion (blockscale), no scales (bf16), and
+    refuses MXFP4 with a clear error instead of timing wrong math."""
+    import bench
+    for kind in ("fp8", "int8", "int4", "fp8_block", "bf16"):
+        r = bench.cpu_baseline(workloads.custom(kind, 32, 256, 256, seed=1, b_std=0.02 if kind == "int4" else 1.0))
+        assert r["value"] > 0 and r["kind"] == "port" and r["cores"] >= 1, kind
+    with pytest.raises(ValueError, match="no CPU baseline"):
+        bench.cpu_baseline(workloads.custom("mxfp4", 32, 256, 256, seed=1))

@@ -77,6 +77,43 @@ def _same(a, b, what):
     assert torch.isfinite(a.float()).all(), f"{what}: non-finite output"
 
 
+def test_first_call_under_capture_is_refused(gpu):
+    """The scratch address is resolved on a device's first call, which must not run under graph
+    capture: such a call returns an error naming the rule and launches nothing (the capture ends
+    empty, the output untouched); an eager call then resolves the address, and a captured call
+    replays to the two-call result.  (Kept first in this file: it needs the process's first call.)"""
+    p = _problem("MS", "fp8", gpu, seed=5)
+    w = p["workload"]
+    lib = _lib.load()
+    out = torch.full((w.tokens, w.model_dim), float("nan"), dtype=torch.float16, device=gpu)
+    torch.cuda.synchronize()
+    _say("no-alloc: first call under capture")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.flygemm_moe_gemm2_reduce_noalloc(out.data_ptr(), *_args(p, "fp16", True, -1), -1, None, 1,
+                                                  torch.cuda.current_stream().cuda_stream)
+    if rc == 0:
+        pytest.skip("the scratch address was already resolved in this process (not its first call)")
+    assert b"graph capture" in lib.flygemm_last_error()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all(), "the refused call wrote the output"
+    want = two_calls(p, "fp16")
+    rc, eager = noalloc(p, "fp16")      # resolves the address
+    _lib.check(rc, "flygemm_moe_gemm2_reduce_noalloc")
+    _same(eager, want, "eager after the refused capture")
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        rc = lib.flygemm_moe_gemm2_reduce_noalloc(out.data_ptr(), *_args(p, "fp16", True, -1), -1, None, 1,
+                                                  torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.flygemm_last_error()
+    for i in range(2):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g2.replay()
+        _same(out, want, f"captured replay {i}")
+
+
 CASES = [  # (first shape, kind, group, out dtype, second (smaller) tokens)
     ("MM", "fp8", -1, "fp16", 40),
     ("MM", "bf16", -1, "bf16", 17),
