@@ -11,12 +11,13 @@
 
 using namespace flygemm;
 
-// Kernel tables, one per stage (stage 2 lives in moe_stage2.hip, compiled in parallel).
-// Instantiated tiles: runs of one routing block (R = 1, 4 waves) for every (tile_m, tile_n);
-// runs of 128 rows (stage 1, 128 columns) and, for 16-row blocks, of 256 rows (stage 2, 256
-// columns) with 8 waves.
+// Kernel tables (stage 2 lives in moe_stage2.hip and the stage-1 stream kernel of 1-byte and
+// 16-bit weights in moe_stream.hip, compiled in parallel).  Here: stage 1 of int4 weights (W4A8,
+// W4A16) and of blockscale fp8 -- runs of one routing block (R = 1, 4 waves) for every (tile_m,
+// tile_n), and for W4A8 runs of 128 rows (128 columns, 8 waves).
 namespace flygemm {
 MoeKernel moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
+MoeKernel moe_stage1_stream_kernel(int kind, int tm);
 }
 
 namespace {
@@ -29,24 +30,35 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
   T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
   T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)
   T(64, 1, 256, 1, 4, 2)
-  // run tiles: not for blockscale (its partials and factors do not fit next to them) nor W4A16
-  // (its group scales ride the two-slot pipeline)
-  if constexpr (!BS && KIND != KIND_W4A16) {
+  // run tiles, for W4A8 (the other kinds without block scales take the stream kernel): not for
+  // blockscale (its partials and factors do not fit next to them) nor W4A16 (its group scales
+  // ride the two-slot pipeline)
+  if constexpr (!BS && KIND == KIND_INT4) {
     T(16, 8, 128, 2, 4, 3) T(32, 4, 128, 2, 4, 3) T(64, 2, 128, 2, 4, 3)
   }
 #undef T
   return MoeKernel{nullptr, 0};
 }
 
+// Stage 1 of fp8, int8 (int8smooth included), bf16 and fp16 runs the stream kernel
+// (moe_stream.h) for every routing: DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256),
+// fp8, graph-timed against the kernels it replaced (64-column single-block tiles for 64-row
+// blocks, 128-row run tiles with weights in LDS for 16- and 32-row blocks), bit-equal outputs:
+// 64-row blocks 2048 / 4096 / 8192 / 16384 tokens 134 / 181 / 298 / 527 us against 160 / 216 /
+// 424 / 722; 32-row 146 / 198 / 307 / 528 against 164 / 264 / 518 / 1728; 16-row 146 / 200 / 313
+// / 549 against 211 / 313 / 525 / 1743; decode-sized routings (16 to 1024 tokens) level or up
+// to 10% faster.
+bool moe_stream_stage1(int stage, int kind, bool bs) {
+  return stage == 1 && !bs && (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_BF16 || kind == KIND_F16);
+}
+
 MoeKernel moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
   if (bs) return kind == KIND_FP8 ? moe_stage1_tile<KIND_FP8, true>(tm, r, tn) : MoeKernel{nullptr, 0};
+  if (moe_stream_stage1(1, kind, bs))
+    return r * tm == 128 && tn == 64 ? moe_stage1_stream_kernel(kind, tm) : MoeKernel{nullptr, 0};
   switch (kind) {
-    case KIND_FP8: return moe_stage1_tile<KIND_FP8, false>(tm, r, tn);
-    case KIND_INT8: return moe_stage1_tile<KIND_INT8, false>(tm, r, tn);
     case KIND_INT4: return moe_stage1_tile<KIND_INT4, false>(tm, r, tn);
     case KIND_W4A16: return moe_stage1_tile<KIND_W4A16, false>(tm, r, tn);
-    case KIND_BF16: return moe_stage1_tile<KIND_BF16, false>(tm, r, tn);
-    case KIND_F16: return moe_stage1_tile<KIND_F16, false>(tm, r, tn);
     default: return MoeKernel{nullptr, 0};
   }
 }
@@ -71,11 +83,18 @@ int pick_tile_n(int N, long runs) {
 int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
               const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
+  // Stage 1 of 1-byte and 16-bit weights: the stream kernel, 128-row runs of 64 columns (every
+  // N here is a multiple of 64: tile_n, checked by the callers, divides it).  The caller's
+  // tile_n is a hint throughout: tiling does not change results.
+  if (moe_stream_stage1(stage, kind, bs)) {
+    *r_out = 128 / tile_m;
+    *tn_out = 64;
+    return 0;
+  }
   // Runs of several routing blocks when experts hold two or more blocks on average, on 2 x 4
-  // waves: stage 1 128 rows x 128 output columns (128 gate + 128 up weight rows) with a 3-slot
-  // DMA ring; stage 2 256 rows x 256 columns with 2 slots.  The caller's tile_n is then
-  // overridden: tiling does not change results.  Not for blockscale nor W4A16 (their scales
-  // do not fit next to the run tiles).
+  // waves: stage 1 (W4A8) 128 rows x 128 output columns (128 gate + 128 up weight rows) with a
+  // 3-slot DMA ring; stage 2 256 rows x 256 columns with 2 slots.  Not for blockscale nor W4A16
+  // (their scales do not fit next to the run tiles).
   int R = 1;
   const int run_tn = stage == 1 ? 128 : 256;
   // Stage 2 of 32- and 64-row blocks keeps single-block tiles (128 columns, below): with three
@@ -93,9 +112,9 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
     // Stage 1 of 64-row blocks with four or more blocks per expert on average and a narrow
     // inter_dim: single-block tiles of 64 columns instead (4 waves, 48 KB of LDS, so up to three
     // workgroups share a CU and one's epilogue -- silu, the scales, the stores -- runs beside
-    // another's MFMAs).  DS-TP8 dims (128 experts, inter_dim 256), fp8: 4096 tokens 213 us
-    // against 259 for the run tile, 8192 422 against 466, 16384 714 against 908; at 2048 tokens
-    // (two blocks per expert) 167 against 162.  Not measured as better for 16- or 32-row blocks.
+    // another's MFMAs).  Measured on fp8 when these kernels ran it, DS-TP8 dims (128 experts,
+    // inter_dim 256): 4096 tokens 213 us against 259 for the run tile, 8192 422 against 466,
+    // 16384 714 against 908; at 2048 tokens (two blocks per expert) 167 against 162.
     if (stage == 1 && tile_m == 64 && N <= 256 && N % 64 == 0 && routes >= 4L * tile_m * experts) {
       R = 1;
       tile_n = 64;
@@ -214,11 +233,12 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
                                  : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
   if (!k.fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
 
-  // column ranges per run: about 1024 workgroups in all
+  // column ranges per run: about 1024 workgroups in all (the stream kernel: one column tile each)
   const long ntn = N / tile_n;
   const long runs = est_runs(tokens, topk, experts, tile_m, R);
   long nsplit = (1024 + runs - 1) / runs;
   nsplit = nsplit < 1 ? 1 : (nsplit > ntn ? ntn : nsplit);
+  if (moe_stream_stage1(stage, kind, bs)) nsplit = ntn;
   MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
                sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
                doweight ? 1 : 0, blocks, (int)nsplit, mout, (uint32_t)out_bytes, token_slot ? 1 : 0,

@@ -1,0 +1,243 @@
+// MoE stage 1 (gate/up projection) for gfx950 with the weights streamed straight into registers.
+//
+// The stage-1 product of the 2-stage MoE GEMM (semantics and routing metadata as moe.h; reference
+// kernels/moe_gemm_2stage.py compile_moe_gemm1 :93-1264) for 1-byte (fp8, int8, int8smooth) and
+// 16-bit (bf16, fp16) weights.
+//
+// One workgroup (4 waves) owns a run of up to R routing blocks of one expert (TM * R = 128 rows;
+// a block starts a run when its index is a multiple of R or its expert differs from the previous
+// block's) and one 64-column tile of the output: 64 gate and 64 up weight rows.  Wave w owns
+// output columns [16w, 16w + 16) for all 128 rows, so no weight byte is shared between waves and
+// the weights skip LDS: each wave loads its gate and up fragments from the preshuffled weights
+// straight into registers (two coalesced 1 KB loads per 16-column block per 128-byte K step, each
+// lane's 16 bytes being its MFMA operand), Lb = D - 1 steps ahead in D register sets.  Only the
+// gathered activation rows, which all four waves read, go global -> LDS by DMA (each lane's
+// buffer offset names its own row; padding rows read zeros past the buffer), one step ahead in a
+// 2-slot ring.  A workgroup then needs 32 KB of LDS and two share a CU (8 waves, at most 256
+// VGPRs each).  The kernel it replaces for these kinds kept the weights in LDS: the weights'
+// L2 -> LDS DMA bounded its single-block tiles, and its 128-row tiles, whose two LDS stages
+// filled a CU, waited out their loads one workgroup per CU.
+//
+// Wait discipline.  Loads retire in issue order on one vector memory counter.  A step s issues,
+// after its barrier, the A DMA of step s+1, then the weights of step s+Lb, then computes.  The
+// A DMA is inline assembly that the compiler does not track; its wait is explicit: at the top
+// of step s the only operations issued after A(s) are the weights of step s-1+Lb (LPS of them).
+// The compiler waits for a weight set counting only the later weight loads it knows of, so the
+// untracked DMAs issued after that set make it also wait for the oldest Lb*AQ operations issued
+// after the set: A(s) (already waited for) and some weights of step s+1, issued a step earlier.
+// The loop runs whole groups of D steps (the register set of each step is static there and
+// every path through a group issues every load); the last nk % D steps form a tail in which the
+// weight loads of steps past the end are dead and removed by the compiler, so each tail step
+// waits for everything instead.
+#pragma once
+#include "moe.h"
+
+namespace flygemm {
+
+// f(integral_constant<int, U>) for U = B .. E-1, each call inlined with U a constant
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <int KIND, int TM, int R, int D>
+__global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
+  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "1-byte or 16-bit weights");
+  constexpr int NW = 4, TN = 64, NB = 2;               // waves, output columns, weight halves
+  constexpr int TME = TM * R, MR = TME / 16;           // rows of a run, 16-row blocks
+  constexpr int A_BYTES = TME * KT, AQ = A_BYTES / 1024 / NW;
+  constexpr int LPS = NB * 2;                          // weight loads per wave per step
+  constexpr int Lb = D - 1;
+  static_assert(TME % 16 == 0 && A_BYTES % (1024 * NW) == 0 && D >= 3, "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * A_BYTES];
+
+  // ---- which run and column tile: logical id L = block * nsplit + column tile (nsplit = N / 64)
+  // over the blocks below num_valid_ids, dealt to the 8 XCDs in contiguous ranges, as moe.h ----
+  const int nv = p.num_valid[0];
+  const int nbv = min((nv + TM - 1) / TM, p.blocks);
+  const int V = nbv * p.nsplit;
+  const int chunk = (V + 7) >> 3;
+  const int L = (blockIdx.x & 7) * chunk + (blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= chunk || L >= V) return;
+  const int b0 = L / p.nsplit;
+  const int jt = L - b0 * p.nsplit;
+  const int e = p.expert_ids[b0];
+  if (e < 0 || e >= p.experts) return;
+  if (R > 1 && b0 % R != 0 && p.expert_ids[b0 - 1] == e) return;   // inside another run
+  int nblk = 1;
+  if constexpr (R > 1) {
+    const int lim = min((b0 / R + 1) * R, nbv);
+    while (b0 + nblk < lim && p.expert_ids[b0 + nblk] == e) ++nblk;
+  }
+  const int rows_valid = nblk * TM;
+  const int K = p.K, nk = K / KT;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const bool a_ts = p.a_token_slot;
+  const int a_rows = !a_ts ? p.tokens : p.tokens * p.topk;
+  constexpr bool kScaled = !kind_is_16bit(KIND);
+
+  // ---- per-row facts, fixed for the workgroup's life (as moe.h) ----
+  // A gather: DMA instruction q fills run rows 8q .. 8q+7; lane l brings the chunk that belongs
+  // in slot l%8 of row 8q + l/8 (XOR chunk swizzle of the large-M kernel).
+  uint32_t va[AQ];
+  int ida[AQ], idr[MR];
+#pragma unroll
+  for (int j = 0; j < AQ; ++j)
+    ida[j] = p.sorted_ids[b0 * TM + min(min((wave + j * NW) * 8 + (lane >> 3), TME - 1), rows_valid - 1)];
+#pragma unroll
+  for (int mi = 0; mi < MR; ++mi) idr[mi] = p.sorted_ids[b0 * TM + min(mi * 16 + l16, rows_valid - 1)];
+#pragma unroll
+  for (int j = 0; j < AQ; ++j) {
+    const int rloc = min((wave + j * NW) * 8 + (lane >> 3), TME - 1);
+    const int id = ida[j];
+    const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+    const bool ok = rloc < rows_valid && t < p.tokens && s < p.topk;
+    const int row = a_ts ? s * p.tokens + t : t;
+    const int c = (lane & 7) ^ ((rloc >> 1) & 7);
+    va[j] = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
+  }
+  // this lane's rows mi*16 + l16: activation scale, routing weight, destination (-1: padding)
+  float sx_r[MR], rw_r[MR];
+  int dst_r[MR];
+#pragma unroll
+  for (int mi = 0; mi < MR; ++mi) {
+    const int r = mi * 16 + l16;
+    const int id = idr[mi];
+    const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+    const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
+    dst_r[mi] = ok ? t * p.topk + s : -1;
+    const int arow = ok ? (a_ts ? s * p.tokens + t : t) : 0;
+    const float sxv = kScaled ? p.sa[arow] : 1.f;
+    const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
+    sx_r[mi] = ok ? sxv : 0.f;  // 0 keeps padding rows finite; 1 for unscaled kinds
+    rw_r[mi] = ok ? rwv : 0.f;
+  }
+  const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
+  // this expert's gate/up rows only (the whole array may exceed 32-bit offsets)
+  const int wrows = 2 * p.N;
+  const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc(p.w + (size_t)e * (size_t)wrows * (size_t)K, wrows * K);
+  const __amdgpu_buffer_rsrc_t rsrc_s = make_rsrc(p.sw + (size_t)e * wrows, kScaled ? wrows * 4 : 0);
+  const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
+
+  typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
+  AccT acc[NB][MR];
+  i32x4 bw[D][NB][2];   // weight fragments of D steps: [set][gate/up][K half]
+  f32x4 sc[NB];         // this lane's 4 column scales of the gate and of the up half
+
+  // weights of step s into register set U: this wave's gate block (16 rows jt*64 + 16*wave ..)
+  // and up block (the same rows + N), 2 KB per K step each in the preshuffled layout; steps past
+  // the end load zeros from past the buffer
+  auto load_b = [&](auto u_tag, int s) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_tag)::value;
+    const uint32_t vo = (uint32_t)lane * 16u + (s < nk ? 0u : 0x80000000u);
+    const int kt = s < nk ? s : 0;
+#pragma unroll
+    for (int h = 0; h < NB; ++h) {
+      const int gblk = (h ? p.N / 16 : 0) + jt * (TN / 16) + wave;
+      const uint32_t so = (uint32_t)gblk * 16u * (uint32_t)K + (uint32_t)kt * 2048u;
+      bw[U][h][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
+      bw[U][h][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 1024u), 0);
+    }
+  };
+  // A of step s into ring slot s & 1
+  auto issue_a = [&](int s) __attribute__((always_inline)) {
+    uint8_t* st = ring + (s & 1) * A_BYTES;
+#pragma unroll
+    for (int j = 0; j < AQ; ++j) dma16(rsrc_a, st + (wave + j * NW) * 1024, va[j], (uint32_t)s * KT);
+  };
+  // One K step from register set U and the A slot sA: row block by row block, the next row's A
+  // fragment read ahead of this row's MFMAs.  B is the MFMA's first operand, so each accumulator
+  // tile holds its 16x16 output block transposed.
+  auto compute = [&](auto u_tag, const uint8_t* sA) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_tag)::value;
+    auto load_a = [&](int mi, i32x4& lo, i32x4& hi) __attribute__((always_inline)) {
+      const int row = mi * 16 + l16;
+      const int sw = (row >> 1) & 7;
+      lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
+      hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
+    };
+    i32x4 alo, ahi;
+    load_a(0, alo, ahi);
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) {
+      const i32x4 lo = alo, hi = ahi;
+      if (mi + 1 < MR) load_a(mi + 1, alo, ahi);
+#pragma unroll
+      for (int h = 0; h < NB; ++h) {
+        const i32x4 bl = bw[U][h][0], bh = bw[U][h][1];
+        if constexpr (KIND == KIND_FP8) {
+          acc[h][mi] = mfma_fp8(__builtin_shufflevector(bl, bh, 0, 1, 2, 3, 4, 5, 6, 7),
+                                __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[h][mi]);
+        } else {
+          acc[h][mi] = mfma_k64<KIND>(bl, lo, acc[h][mi]);
+          acc[h][mi] = mfma_k64<KIND>(bh, hi, acc[h][mi]);
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int h = 0; h < NB; ++h)
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) acc[h][mi] = AccT{0, 0, 0, 0};
+  // prologue: weights of steps 0 .. Lb-1, this lane's column scales, A of step 0 (the first
+  // step waits for all of them)
+  static_for<0, Lb>([&](auto u) __attribute__((always_inline)) { load_b(u, decltype(u)::value); });
+#pragma unroll
+  for (int h = 0; h < NB; ++h) {
+    const uint32_t col = (uint32_t)(h * p.N + jt * TN + wave * 16 + lq * 4);
+    sc[h] = kScaled ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_s, col * 4u, 0, 0))
+                    : f32x4{1.f, 1.f, 1.f, 1.f};
+  }
+  issue_a(0);
+  // Epilogue: out1[t][s][n] = silu(gate) * up (* routing weight), gate/up = accumulator *
+  // activation scale * weight-row scale; lane (l16, lq) holds row mi*16 + l16, columns 4*lq ..
+  // 4*lq+3 of this wave's 16; 8-byte row stores, padding rows at an offset past the buffer.  It
+  // runs inside the last step: placed after the loop, the fp8 instances spilled 63-70 VGPRs.
+  auto epilogue = [&]() __attribute__((always_inline)) {
+    const bool obf16 = moe_out_bf16(p.out_mode);
+    const int c = jt * TN + wave * 16 + lq * 4;
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) {
+      const int d = dst_r[mi];
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float g = ((float)acc[0][mi][q] * sx_r[mi]) * sc[0][q];
+        const float up = ((float)acc[1][mi][q] * sx_r[mi]) * sc[1][q];
+        v[q] = (silu_f(g) * up) * rw_r[mi];
+      }
+      const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)c) * 2u;
+      const i32x2 pk = obf16 ? pack_out4<true>(v) : pack_out4<false>(v);
+      __builtin_amdgcn_raw_buffer_store_b64(pk, rsrc_o, off, 0, 0);
+    }
+  };
+  auto step = [&](auto u_tag, int s, auto tail_tag) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_tag)::value;
+    if (decltype(tail_tag)::value || s == 0)
+      waitcnt<0>();
+    else
+      waitcnt<LPS>();   // A(s); only the weights of step s-1+Lb were issued after it
+    workgroup_barrier();  // A(s) published; every wave is done with slot (s+1) & 1
+    if (s + 1 < nk) issue_a(s + 1);
+    load_b(std::integral_constant<int, (U + Lb) % D>{}, s + Lb);
+    __builtin_amdgcn_sched_barrier(0);   // the loads go out before the MFMAs
+    compute(u_tag, ring + (s & 1) * A_BYTES);
+    if (s == nk - 1) epilogue();
+  };
+  int s0 = 0;
+  for (; s0 + D <= nk; s0 += D)
+    static_for<0, D>([&](auto u) __attribute__((always_inline)) {
+      step(u, s0 + decltype(u)::value, std::false_type{});
+    });
+  static_for<0, D - 1>([&](auto u) __attribute__((always_inline)) {
+    if (s0 + decltype(u)::value < nk) step(u, s0 + decltype(u)::value, std::true_type{});
+  });
+}
+
+}  // namespace flygemm

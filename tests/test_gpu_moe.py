@@ -39,7 +39,9 @@ def _np(t):
 
 
 def _tile_k(kind):
-    return 128
+    # the launchers validate model_dim % tile_k (elements); 64 for 16-bit inputs admits every
+    # K of whole 128-byte steps, the kernels' own granularity
+    return 64 if kind in ("bf16", "fp16", "int4_bf16") else 128
 
 
 def run_stage1(p, dev, out_dtype="f16", doweight=False, tile_n=None):
@@ -238,6 +240,46 @@ def test_large_and_decode_shapes_sampled(gpu, name):
     o2 = run_stage2(p, gpu, "f16", doweight=True)
     torch.cuda.synchronize()
     _check(o2, ref_stage2(p, True, rows), rows, what=f"{name} stage2")
+
+
+# ---- stage 1 of 1-byte and 16-bit weights: the stream kernel ------------------------------------
+STREAM_KINDS = ["fp8", "int8", "int8smooth", "bf16", "fp16"]
+
+
+@pytest.mark.parametrize("kind", STREAM_KINDS)
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+def test_stage1_stream_steps_and_runs(gpu, kind, tile_m):
+    """Stage 1 of these kinds runs the stream kernel (runs of 128 rows, one 64-column tile per
+    workgroup, the weights loaded into registers two 128-byte K steps ahead in three register
+    sets, whole groups of three steps then a tail).  K of 1 to 5 steps covers a loop with no
+    whole group, whole groups with no tail and tails of one and two steps; 300 tokens top-3 of 5
+    experts over inter_dim 192 (three column tiles) give runs cut at expert boundaries and
+    partial last runs; routing weights on and off, fp16 and bf16 outputs."""
+    for nk in (1, 2, 3, 4, 5):
+        model_dim = nk * 128 // (2 if kind in ("bf16", "fp16") else 1)
+        w = W.moe_custom(300, model_dim, 192, 5, 3, tile_m, 64, 64, kind, seed=nk * 10 + tile_m)
+        assert _chosen_tile(1, w, kind) == (128 // tile_m, 64)
+        p = W.moe_problem(w, gpu)
+        for doweight, out_dtype in ((False, "f16"), (True, "bf16")):
+            _say(f"stream stage1 {kind} tile_m={tile_m} K steps={nk} doweight={doweight} out={out_dtype}")
+            o1 = run_stage1(p, gpu, out_dtype, doweight=doweight)
+            torch.cuda.synchronize()
+            check_stage1(p, o1, doweight, what=f"stream {kind} tm{tile_m} nk{nk} w{int(doweight)} {out_dtype}")
+
+
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+def test_stage1_stream_prefill_sampled(gpu, tile_m):
+    """DS-TP8 prefill stage 1 (8192 tokens top-8 of 128 experts, 7168 x 256: 56 K steps, a tail
+    of two) at every routing block size: all routes computed, a sample of tokens checked."""
+    w = W.MOE_WORKLOADS["DSP"]
+    p = _problem(W.MoeWorkload(w.name, w.tokens, w.model_dim, w.inter_dim, w.experts, w.topk, tile_m, w.tile_n1,
+                               w.tile_n2, "fp8", w.seed), "fp8", gpu)
+    rows = np.unique(np.r_[np.linspace(0, w.tokens - 1, 16).astype(int), w.tokens - 1])
+    _say(f"DSP stage1 tile_m={tile_m}")
+    o1 = run_stage1(p, gpu, "f16", doweight=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o1.float()).all()
+    _check(o1, ref_stage1(p, True, rows), rows, what=f"DSP stage1 tm{tile_m}")
 
 
 def test_two_stage_chain(gpu):
@@ -617,10 +659,13 @@ WIDE_KINDS = [("fp8", -1), ("int8", -1), ("bf16", -1), ("fp16", -1), ("int4", -1
 def test_single_block_wide_tiles(gpu, kind, group):
     """Routings with fewer than two blocks per expert but enough routes that the launcher keeps
     wide single-block tiles: 160 tokens, top-4 of 64 experts, D = 512, I = 1024, tile_m 32,
-    tile_n 256 -> stage 1 runs the 256-column single-block kernel, stage 2 the 128-column one
-    (checked through flygemm_moe_select_tile first).  Stage 2 in atomic and reduce modes."""
+    tile_n 256 -> stage 1 of int4 weights runs the 256-column single-block kernel (the other
+    kinds the stream kernel), stage 2 the 128-column one (checked through
+    flygemm_moe_select_tile first).  Stage 2 in atomic and reduce modes."""
     w = W.moe_custom(160, 512, 1024, 64, 4, 32, 256, 256, kind, seed=11)
-    assert _chosen_tile(1, w, kind) == (1, 256) and _chosen_tile(2, w, kind) == (1, 128)
+    # (stage 1 of 1-byte and 16-bit weights: the stream kernel's 128-row runs of 64 columns)
+    assert _chosen_tile(1, w, kind) == ((1, 256) if kind.startswith("int4") else (4, 64))
+    assert _chosen_tile(2, w, kind) == (1, 128)
     p = W.moe_problem(w, gpu, group_size=group)
     p["group_size"] = group
     _say(f"wide single-block tiles {kind} g={group}")
