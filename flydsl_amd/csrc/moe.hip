@@ -11,10 +11,9 @@
 
 using namespace flygemm;
 
-// Kernel tables (stage 2 lives in moe_stage2.hip and the stage-1 stream kernel of 1-byte and
-// 16-bit weights in moe_stream.hip, compiled in parallel).  Here: stage 1 of int4 weights (W4A8,
-// W4A16) and of blockscale fp8 -- runs of one routing block (R = 1, 4 waves) for every (tile_m,
-// tile_n), and for W4A8 runs of 128 rows (128 columns, 8 waves).
+// Kernel tables (stage 2 lives in moe_stage2.hip and the stage-1 stream kernel of 1-byte,
+// 16-bit and W4A8 weights in moe_stream.hip, compiled in parallel).  Here: stage 1 of W4A16 and
+// of blockscale fp8 -- runs of one routing block (R = 1, 4 waves) for every (tile_m, tile_n).
 namespace flygemm {
 MoeKernel moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
 MoeKernel moe_stage1_stream_kernel(int kind, int tm);
@@ -30,18 +29,12 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
   T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
   T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)
   T(64, 1, 256, 1, 4, 2)
-  // run tiles, for W4A8 (the other kinds without block scales take the stream kernel): not for
-  // blockscale (its partials and factors do not fit next to them) nor W4A16 (its group scales
-  // ride the two-slot pipeline)
-  if constexpr (!BS && KIND == KIND_INT4) {
-    T(16, 8, 128, 2, 4, 3) T(32, 4, 128, 2, 4, 3) T(64, 2, 128, 2, 4, 3)
-  }
 #undef T
   return MoeKernel{nullptr, 0};
 }
 
-// Stage 1 of fp8, int8 (int8smooth included), bf16 and fp16 runs the stream kernel
-// (moe_stream.h) for every routing: DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256),
+// Stage 1 of fp8, int8 (int8smooth included), int4 weights with int8 activations (W4A8), bf16
+// and fp16 runs the stream kernel (moe_stream.h) for every routing: DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256),
 // fp8, graph-timed against the kernels it replaced (64-column single-block tiles for 64-row
 // blocks, 128-row run tiles with weights in LDS for 16- and 32-row blocks), bit-equal outputs:
 // 64-row blocks 2048 / 4096 / 8192 / 16384 tokens 134 / 181 / 298 / 527 us against 160 / 216 /
@@ -49,18 +42,15 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
 // / 549 against 211 / 313 / 525 / 1743; decode-sized routings (16 to 1024 tokens) level or up
 // to 10% faster.
 bool moe_stream_stage1(int stage, int kind, bool bs) {
-  return stage == 1 && !bs && (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_BF16 || kind == KIND_F16);
+  return stage == 1 && !bs &&
+         (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_INT4 || kind == KIND_BF16 || kind == KIND_F16);
 }
 
 MoeKernel moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
   if (bs) return kind == KIND_FP8 ? moe_stage1_tile<KIND_FP8, true>(tm, r, tn) : MoeKernel{nullptr, 0};
   if (moe_stream_stage1(1, kind, bs))
     return r * tm == 128 && tn == 64 ? moe_stage1_stream_kernel(kind, tm) : MoeKernel{nullptr, 0};
-  switch (kind) {
-    case KIND_INT4: return moe_stage1_tile<KIND_INT4, false>(tm, r, tn);
-    case KIND_W4A16: return moe_stage1_tile<KIND_W4A16, false>(tm, r, tn);
-    default: return MoeKernel{nullptr, 0};
-  }
+  return kind == KIND_W4A16 ? moe_stage1_tile<KIND_W4A16, false>(tm, r, tn) : MoeKernel{nullptr, 0};
 }
 
 // Estimated runs (workgroups before column splitting): routing blocks grouped R at a time, plus
@@ -83,20 +73,17 @@ int pick_tile_n(int N, long runs) {
 int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
               const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
-  // Stage 1 of 1-byte and 16-bit weights: the stream kernel, 128-row runs of 64 columns (every
-  // N here is a multiple of 64: tile_n, checked by the callers, divides it).  The caller's
-  // tile_n is a hint throughout: tiling does not change results.
+  // Stage 1 of 1-byte, 16-bit and W4A8 weights: the stream kernel, 128-row runs of 64 columns
+  // (every N here is a multiple of 64: tile_n, checked by the callers, divides it).  The
+  // caller's tile_n is a hint throughout: tiling does not change results.
   if (moe_stream_stage1(stage, kind, bs)) {
     *r_out = 128 / tile_m;
     *tn_out = 64;
     return 0;
   }
-  // Runs of several routing blocks when experts hold two or more blocks on average, on 2 x 4
-  // waves: stage 1 (W4A8) 128 rows x 128 output columns (128 gate + 128 up weight rows) with a
-  // 3-slot DMA ring; stage 2 256 rows x 256 columns with 2 slots.  Not for blockscale nor W4A16
-  // (their scales do not fit next to the run tiles).
-  int R = 1;
-  const int run_tn = stage == 1 ? 128 : 256;
+  // Stage 2 of 16-row blocks: runs of 256 rows x 256 columns on 2 x 4 waves when experts hold two
+  // or more blocks on average.  Not for blockscale nor W4A16 (their scales do not fit next to the
+  // run tiles); stage 1 of those two kinds keeps single-block tiles.
   // Stage 2 of 32- and 64-row blocks keeps single-block tiles (128 columns, below): with three
   // workgroups per CU their epilogues and row stores overlap each other's MFMAs.  DS-TP8 dims
   // (128 experts, model_dim 7168, inter_dim 256), fp8, graph-timed: 64-row blocks, reduce mode
@@ -105,20 +92,11 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
   // blocks reduce 189 / 381 / 702 / 1369 against 277 / 374 / 723 / 1512, atomics 254 / 502 /
   // 835 / 1701 against 385 / 454 / 991 / 2185.  16-row blocks keep the runs (reduce mode 1.0-1.3x
   // slower single-block from 4096 tokens).
-  const bool runs_ok = !(stage == 2 && tile_m >= 32);
-  if (!bs && kind != KIND_W4A16 && runs_ok && routes >= 2L * tile_m * experts && N % run_tn == 0 && tile_n != 64) {
-    R = (stage == 1 ? 128 : 256) / tile_m;
-    tile_n = run_tn;
-    // Stage 1 of 64-row blocks with four or more blocks per expert on average and a narrow
-    // inter_dim: single-block tiles of 64 columns instead (4 waves, 48 KB of LDS, so up to three
-    // workgroups share a CU and one's epilogue -- silu, the scales, the stores -- runs beside
-    // another's MFMAs).  Measured on fp8 when these kernels ran it, DS-TP8 dims (128 experts,
-    // inter_dim 256): 4096 tokens 213 us against 259 for the run tile, 8192 422 against 466,
-    // 16384 714 against 908; at 2048 tokens (two blocks per expert) 167 against 162.
-    if (stage == 1 && tile_m == 64 && N <= 256 && N % 64 == 0 && routes >= 4L * tile_m * experts) {
-      R = 1;
-      tile_n = 64;
-    }
+  int R = 1;
+  if (stage == 2 && tile_m == 16 && !bs && kind != KIND_W4A16 && routes >= 2L * tile_m * experts && N % 256 == 0 &&
+      tile_n != 64) {
+    R = 256 / tile_m;
+    tile_n = 256;
   }
   if (tile_n <= 0) tile_n = pick_tile_n(N, est_runs(tokens, topk, experts, tile_m, R));
   // Few runs (decode): narrower column tiles until there are workgroups for every CU (each

@@ -1,16 +1,18 @@
 // MoE stage 1 (gate/up projection) for gfx950 with the weights streamed straight into registers.
 //
 // The stage-1 product of the 2-stage MoE GEMM (semantics and routing metadata as moe.h; reference
-// kernels/moe_gemm_2stage.py compile_moe_gemm1 :93-1264) for 1-byte (fp8, int8, int8smooth) and
-// 16-bit (bf16, fp16) weights.
+// kernels/moe_gemm_2stage.py compile_moe_gemm1 :93-1264) for 1-byte (fp8, int8, int8smooth),
+// 16-bit (bf16, fp16) and int4 weights with int8 activations (W4A8: the packed preshuffled bytes
+// of the dense int4 path, unpacked to int8 in registers).
 //
 // One workgroup (4 waves) owns a run of up to R routing blocks of one expert (TM * R = 128 rows;
 // a block starts a run when its index is a multiple of R or its expert differs from the previous
 // block's) and one 64-column tile of the output: 64 gate and 64 up weight rows.  Wave w owns
 // output columns [16w, 16w + 16) for all 128 rows, so no weight byte is shared between waves and
 // the weights skip LDS: each wave loads its gate and up fragments from the preshuffled weights
-// straight into registers (two coalesced 1 KB loads per 16-column block per 128-byte K step, each
-// lane's 16 bytes being its MFMA operand), Lb = D - 1 steps ahead in D register sets.  Only the
+// straight into registers (two coalesced loads per 16-column block per 128-byte K step, 1 KB
+// each -- 512 bytes for int4 -- each lane's bytes being its MFMA operand), Lb = D - 1 steps ahead
+// in D register sets.  Only the
 // gathered activation rows, which all four waves read, go global -> LDS by DMA (each lane's
 // buffer offset names its own row; padding rows read zeros past the buffer), one step ahead in a
 // 2-slot ring.  A workgroup then needs 32 KB of LDS and two share a CU (8 waves, at most 256
@@ -45,7 +47,10 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 template <int KIND, int TM, int R, int D>
 __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
-  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "1-byte or 16-bit weights");
+  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || KIND == KIND_INT4 || kind_is_16bit(KIND),
+                "1-byte, 16-bit or int4 weights");
+  constexpr bool I4 = KIND == KIND_INT4;
+  constexpr uint32_t B_BLK = I4 ? 1024u : 2048u;     // bytes of one 16-row weight block per K step
   constexpr int NW = 4, TN = 64, NB = 2;               // waves, output columns, weight halves
   constexpr int TME = TM * R, MR = TME / 16;           // rows of a run, 16-row blocks
   constexpr int A_BYTES = TME * KT, AQ = A_BYTES / 1024 / NW;
@@ -120,28 +125,39 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
   const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
   // this expert's gate/up rows only (the whole array may exceed 32-bit offsets)
   const int wrows = 2 * p.N;
-  const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc(p.w + (size_t)e * (size_t)wrows * (size_t)K, wrows * K);
+  const uint32_t wrb = I4 ? (uint32_t)K / 2u : (uint32_t)K;   // weight bytes per row
+  const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc(p.w + (size_t)e * (size_t)wrows * wrb, (int)(wrows * wrb));
   const __amdgpu_buffer_rsrc_t rsrc_s = make_rsrc(p.sw + (size_t)e * wrows, kScaled ? wrows * 4 : 0);
   const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
 
   typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
   AccT acc[NB][MR];
-  i32x4 bw[D][NB][2];   // weight fragments of D steps: [set][gate/up][K half]
+  typedef typename std::conditional<I4, i32x2, i32x4>::type BT;
+  BT bw[D][NB][2];      // weight fragments of D steps: [set][gate/up][K half]
   f32x4 sc[NB];         // this lane's 4 column scales of the gate and of the up half
 
   // weights of step s into register set U: this wave's gate block (16 rows jt*64 + 16*wave ..)
-  // and up block (the same rows + N), 2 KB per K step each in the preshuffled layout; steps past
-  // the end load zeros from past the buffer
+  // and up block (the same rows + N), B_BLK bytes per K step each in the preshuffled layout
+  // (lane (l16, lq) holds K bytes 16*lq .. of its row's first and second 64-byte halves: at
+  // 16*lane and 1024 + 16*lane; int4: 8 packed bytes at 128*lq + 8*l16 and 512 past that);
+  // steps past the end load zeros from past the buffer
   auto load_b = [&](auto u_tag, int s) __attribute__((always_inline)) {
     constexpr int U = decltype(u_tag)::value;
-    const uint32_t vo = (uint32_t)lane * 16u + (s < nk ? 0u : 0x80000000u);
+    const uint32_t past = s < nk ? 0u : 0x80000000u;
     const int kt = s < nk ? s : 0;
 #pragma unroll
     for (int h = 0; h < NB; ++h) {
       const int gblk = (h ? p.N / 16 : 0) + jt * (TN / 16) + wave;
-      const uint32_t so = (uint32_t)gblk * 16u * (uint32_t)K + (uint32_t)kt * 2048u;
-      bw[U][h][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
-      bw[U][h][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 1024u), 0);
+      const uint32_t so = (uint32_t)gblk * 16u * wrb + (uint32_t)kt * B_BLK;
+      if constexpr (I4) {
+        const uint32_t vo = (uint32_t)(lq * 128 + l16 * 8) + past;
+        bw[U][h][0] = __builtin_amdgcn_raw_buffer_load_b64(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
+        bw[U][h][1] = __builtin_amdgcn_raw_buffer_load_b64(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 512u), 0);
+      } else {
+        const uint32_t vo = (uint32_t)lane * 16u + past;
+        bw[U][h][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
+        bw[U][h][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 1024u), 0);
+      }
     }
   };
   // A of step s into ring slot s & 1
@@ -169,13 +185,21 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
       if (mi + 1 < MR) load_a(mi + 1, alo, ahi);
 #pragma unroll
       for (int h = 0; h < NB; ++h) {
-        const i32x4 bl = bw[U][h][0], bh = bw[U][h][1];
+        i32x4 bl, bh;
+        if constexpr (I4) {
+          bl = unpack_int4x16(bw[U][h][0]);
+          bh = unpack_int4x16(bw[U][h][1]);
+        } else {
+          bl = bw[U][h][0];
+          bh = bw[U][h][1];
+        }
         if constexpr (KIND == KIND_FP8) {
           acc[h][mi] = mfma_fp8(__builtin_shufflevector(bl, bh, 0, 1, 2, 3, 4, 5, 6, 7),
                                 __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[h][mi]);
         } else {
-          acc[h][mi] = mfma_k64<KIND>(bl, lo, acc[h][mi]);
-          acc[h][mi] = mfma_k64<KIND>(bh, hi, acc[h][mi]);
+          constexpr int MK = I4 ? KIND_INT8 : KIND;   // int4 weights: the int8 MFMA
+          acc[h][mi] = mfma_k64<MK>(bl, lo, acc[h][mi]);
+          acc[h][mi] = mfma_k64<MK>(bh, hi, acc[h][mi]);
         }
       }
     }
@@ -208,8 +232,8 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float g = ((float)acc[0][mi][q] * sx_r[mi]) * sc[0][q];
-        const float up = ((float)acc[1][mi][q] * sx_r[mi]) * sc[1][q];
+        const float g = ((float)int4_acc<KIND>(acc[0][mi][q]) * sx_r[mi]) * sc[0][q];
+        const float up = ((float)int4_acc<KIND>(acc[1][mi][q]) * sx_r[mi]) * sc[1][q];
         v[q] = (silu_f(g) * up) * rw_r[mi];
       }
       const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)c) * 2u;

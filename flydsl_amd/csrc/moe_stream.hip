@@ -24,6 +24,7 @@ MoeKernel moe_stage1_stream_kernel(int kind, int tm) {
   switch (kind) {
     case KIND_FP8: return stream_tile<KIND_FP8>(tm);
     case KIND_INT8: return stream_tile<KIND_INT8>(tm);
+    case KIND_INT4: return stream_tile<KIND_INT4>(tm);
     case KIND_BF16: return stream_tile<KIND_BF16>(tm);
     case KIND_F16: return stream_tile<KIND_F16>(tm);
     default: return MoeKernel{nullptr, 0};

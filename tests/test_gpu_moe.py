@@ -243,7 +243,7 @@ def test_large_and_decode_shapes_sampled(gpu, name):
 
 
 # ---- stage 1 of 1-byte and 16-bit weights: the stream kernel ------------------------------------
-STREAM_KINDS = ["fp8", "int8", "int8smooth", "bf16", "fp16"]
+STREAM_KINDS = ["fp8", "int8", "int8smooth", "int4", "bf16", "fp16"]
 
 
 @pytest.mark.parametrize("kind", STREAM_KINDS)
@@ -659,12 +659,12 @@ WIDE_KINDS = [("fp8", -1), ("int8", -1), ("bf16", -1), ("fp16", -1), ("int4", -1
 def test_single_block_wide_tiles(gpu, kind, group):
     """Routings with fewer than two blocks per expert but enough routes that the launcher keeps
     wide single-block tiles: 160 tokens, top-4 of 64 experts, D = 512, I = 1024, tile_m 32,
-    tile_n 256 -> stage 1 of int4 weights runs the 256-column single-block kernel (the other
-    kinds the stream kernel), stage 2 the 128-column one (checked through
-    flygemm_moe_select_tile first).  Stage 2 in atomic and reduce modes."""
+    tile_n 256 -> stage 1 of W4A16 runs the 256-column single-block kernel (the other kinds
+    the stream kernel), stage 2 the 128-column one (checked through flygemm_moe_select_tile
+    first).  Stage 2 in atomic and reduce modes."""
     w = W.moe_custom(160, 512, 1024, 64, 4, 32, 256, 256, kind, seed=11)
-    # (stage 1 of 1-byte and 16-bit weights: the stream kernel's 128-row runs of 64 columns)
-    assert _chosen_tile(1, w, kind) == ((1, 256) if kind.startswith("int4") else (4, 64))
+    # (stage 1 of the other kinds: the stream kernel's 128-row runs of 64 columns)
+    assert _chosen_tile(1, w, kind) == ((1, 256) if kind == "int4_bf16" else (4, 64))
     assert _chosen_tile(2, w, kind) == (1, 128)
     p = W.moe_problem(w, gpu, group_size=group)
     p["group_size"] = group

@@ -406,10 +406,10 @@ def test_moe_blockscale_validation():
 
 def test_moe_tile_choice_pinned():
     """flygemm_moe_select_tile gives the launchers' tile choice without a device: stage 1 of
-    1-byte and 16-bit weights always runs the stream kernel (runs of 128 rows, 64 columns); W4A8,
-    W4A16 and blockscale stage 1 and every stage 2 keep run tiles for prefill routings, 64
-    columns for decode-sized ones, wide single-block tiles in between (the reachable kernel set
-    the GPU tests cover), and the launchers' validation."""
+    1-byte, 16-bit and W4A8 weights always runs the stream kernel (runs of 128 rows, 64
+    columns); W4A16 and blockscale stage 1 keep single-block tiles; stage 2 takes runs for
+    16-row blocks of prefill routings, 64 columns for decode-sized ones, wide single-block tiles
+    in between (the reachable kernel set the GPU tests cover), and the launchers' validation."""
     import ctypes
     lib = _lib.load()
 
@@ -421,28 +421,21 @@ def test_moe_tile_choice_pinned():
 
     # stage 1 stream kernel: 128 / tile_m blocks per run, 64 columns, whatever the routing and the
     # caller's tile_n
-    for kind in ("fp8", "int8", "bf16", "fp16", "int8smooth"):
+    for kind in ("fp8", "int8", "bf16", "fp16", "int8smooth", "int4"):
         for tokens, n, experts, topk in ((8192, 256, 128, 8), (8, 256, 256, 8), (160, 1024, 64, 4), (64, 256, 4, 2)):
             for tm in (16, 32, 64):
                 assert sel(1, tokens, n, experts, topk, tm, 256, kind) == (128 // tm, 64), (kind, tokens, tm)
-    # W4A8 stage 1 on DS-TP8 prefill: four or more 64-row blocks per expert: 64-column
-    # single-block tiles; with two or three: runs of 128 rows and 128 columns; stage 2:
-    # 128-column single-block tiles for 32- and 64-row blocks, runs of 256 rows and 256 columns
-    # for 16-row blocks
-    assert sel(1, 8192, 256, 128, 8, 64, 256, "int4") == (1, 64)
-    assert sel(1, 4096, 256, 128, 8, 64, 256, "int4") == (1, 64)
-    assert sel(1, 2048, 256, 128, 8, 64, 256, "int4") == (2, 128)
-    assert sel(1, 8192, 256, 128, 8, 32, 256, "int4") == (4, 128)
-    assert sel(1, 8192, 1024, 128, 8, 64, 256, "int4") == (2, 128)
+    # stage 2 on DS-TP8 prefill: 128-column single-block tiles for 32- and 64-row blocks, runs of
+    # 256 rows and 256 columns for 16-row blocks
     assert sel(2, 8192, 7168, 128, 8, 64, 256) == (1, 128)
     assert sel(2, 8192, 7168, 128, 8, 32, 256) == (1, 128)
     assert sel(2, 8192, 7168, 128, 8, 16, 256) == (16, 256)
+    assert sel(2, 8192, 7168, 128, 8, 16, 256, "int4") == (16, 256)
     # decode: 64-column single-block tiles whatever the caller asked
-    assert sel(1, 8, 256, 256, 8, 32, 256, "int4") == (1, 64)
+    assert sel(1, 8, 256, 256, 8, 32, 256, "int4_bf16") == (1, 64)
     assert sel(2, 8, 7168, 256, 8, 32, 256) == (1, 64)
     # in between: the wide single-block tiles; stage 2 never keeps 256 single-block columns
-    for kind in ("int4", "int4_bf16"):
-        assert sel(1, 160, 1024, 64, 4, 32, 256, kind) == (1, 256), kind
+    assert sel(1, 160, 1024, 64, 4, 32, 256, "int4_bf16") == (1, 256)
     for kind in ("fp8", "int8", "bf16", "fp16", "int4", "int8smooth", "int4_bf16"):
         assert sel(2, 160, 512, 64, 4, 32, 256, kind) == (1, 128), kind
     assert sel(1, 160, 1024, 64, 4, 32, 256, "fp8", 1) == (1, 256)
