@@ -10,7 +10,7 @@ import subprocess
 import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-SOURCES = [os.path.join(PKG_DIR, "csrc", f) for f in ("flygemm.hip", "moe.hip", "moe_stage2.hip", "moe_stream.hip")]
+SOURCES = [os.path.join(PKG_DIR, "csrc", f) for f in ("flygemm.hip", "moe.hip", "moe_stage2.hip", "moe_stream.hip", "moe_stream2.hip")]
 OUT = os.path.join(PKG_DIR, "_flygemm.so")
 ARCH = "gfx950"
 

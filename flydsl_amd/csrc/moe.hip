@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/flygemm.h"
@@ -17,6 +18,7 @@ using namespace flygemm;
 namespace flygemm {
 MoeKernel moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
 MoeKernel moe_stage1_stream_kernel(int kind, int tm);
+MoeKernel moe_stage2_stream_kernel(int kind, int tm, int nk);
 }
 
 namespace {
@@ -207,8 +209,30 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
   if (bs && (2L * N) % (stage == 1 ? 128 : 256) != 0)
     return fail(hipErrorInvalidValue, "%s: %s=%d must be a multiple of 128 (weight scale blocks)", what,
                 stage == 1 ? "2*inter_dim" : "model_dim", stage == 1 ? 2 * N : N);
-  const MoeKernel k = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n, bs)
-                                 : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
+  MoeKernel k = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n, bs)
+                           : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
+  // Stage 2 per-route rows (the reduce mode's GEMM) of 1-byte and 16-bit weights with inter_dim
+  // of 1, 2 or 4 128-byte K steps: the stream kernel (moe_stream.h), runs of 128 rows, 64-column
+  // tiles, A resident, the next tile's weights loaded before this tile's stores -- for routings
+  // with a full 128-row run per expert on average, and for 16-row blocks wherever the kernel
+  // above takes 256-row runs.  DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256), fp8,
+  // reduce mode (GEMM + reduction), graph-timed, bit-equal: 64-row blocks 2048 / 4096 / 8192
+  // tokens 146 / 246 / 438 us against 164 / 279 / 586, 32-row 163 / 259 against 186 / 382,
+  // 16-row 512 / 1024 / 2048 / 4096 tokens 70 / 115 / 162 / 258 against 199 / 217 / 286 / 372;
+  // below that the kernel above (1024 tokens, 64-row blocks: 89 against 96; 8 tokens: 20 against
+  // 27-47).
+  bool stream2 = false;
+  const long routes_all = (long)tokens * topk;
+  if (stage == 2 && rows && !bs && kb <= 512 &&
+      (routes_all >= 128L * experts || (tile_m == 16 && routes_all >= 32L * experts))) {
+    const MoeKernel k2 = moe_stage2_stream_kernel(kind, tile_m, (int)(kb / 128));
+    if (k2.fn) {
+      k = k2;
+      R = 128 / tile_m;
+      tile_n = 64;
+      stream2 = true;
+    }
+  }
   if (!k.fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
 
   // column ranges per run: about 1024 workgroups in all (the stream kernel: one column tile each)
@@ -217,6 +241,10 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
   long nsplit = (1024 + runs - 1) / runs;
   nsplit = nsplit < 1 ? 1 : (nsplit > ntn ? ntn : nsplit);
   if (moe_stream_stage1(stage, kind, bs)) nsplit = ntn;
+  // the stage-2 stream kernel: 4 column ranges per run (DS-TP8 prefill, 2 / 3 / 4 / 6 / 8: 574 /
+  // 470 / 438 / 468 / 444 us), more when the runs are few (about 1024 workgroups; 1024 tokens,
+  // 32-row blocks: 16 ranges 111 us against 117 for 4)
+  if (stream2) nsplit = std::min(ntn, std::max(4L, (1024 + runs - 1) / runs));
   MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
                sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
                doweight ? 1 : 0, blocks, (int)nsplit, mout, (uint32_t)out_bytes, token_slot ? 1 : 0,

@@ -265,3 +265,201 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
 }
 
 }  // namespace flygemm
+
+namespace flygemm {
+
+// MoE stage 2 with per-route row outputs (the reduce mode's GEMM; reference
+// kernels/moe_gemm_2stage.py compile_moe_gemm2 :1267-2481 with accumulate = False, summed by
+// moe_reduce_kernel) for 1-byte and 16-bit weights and inter_dim of NK <= 4 128-byte K steps.
+//
+// One workgroup (4 waves) owns a run of up to R routing blocks of one expert (128 rows) and a
+// range of 64-column output tiles (nsplit ranges per run).  The run's gathered A rows -- all NK
+// K steps -- go to LDS once and stay there.  Wave w owns output columns [16w, 16w + 16) of each
+// tile and loads their weight fragments (NK steps x two coalesced 1 KB loads) and column scales
+// straight into registers, one column tile ahead: the loads of tile j+1 are issued before tile
+// j's stores, so the compiler's wait for them (vector memory operations retire in issue order)
+// never covers a store, and each tile's 16 KB of row stores drain while the next tile computes.
+// The epilogue stages the tile through LDS in two rounds of 64 rows (16-byte chunk c of row r at
+// chunk c ^ (r % 8)) and stores whole 128-byte row segments.  40 KB of LDS and at most 128 VGPRs
+// let four workgroups share a CU.  DS-TP8 prefill (65536 routes, 7168 x 256, fp8), the GEMM and
+// the reduction: 438 us against 586 for the single-block kernel with A resident (bit-equal);
+// variants measured and not kept: three workgroups per CU with one staging round 453 us, the A
+// fragments held in registers (two workgroups per CU) 478, 64-row runs 486-494, 2 / 3 / 6 / 8
+// column ranges per run 574 / 470 / 468 / 444.
+template <int KIND, int TM, int R, int NK>
+__global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
+  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "1-byte or 16-bit weights");
+  constexpr int NW = 4, TN = 64, HALVES = 2;
+  constexpr int TME = TM * R, MR = TME / 16;
+  constexpr int A_STEP = TME * KT, AQ = A_STEP / 1024 / NW;
+  constexpr int RB = TN * 2;                  // bytes of one output row of the tile
+  constexpr int CPR = RB / 16;                // 16-byte chunks per row
+  constexpr int HR = TME / HALVES;            // rows staged per round
+  constexpr int SCH = HR * CPR / (NW * 64);   // store chunks per thread per round
+  static_assert(SCH * NW * 64 == HR * CPR && MR % HALVES == 0 && NK >= 1 && NK <= 4, "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t sa_lds[NK * A_STEP];
+  __shared__ __attribute__((aligned(1024))) uint8_t stg[HR * RB];
+
+  // ---- which run and column range (as moe.h) ----
+  const int nv = p.num_valid[0];
+  const int nbv = min((nv + TM - 1) / TM, p.blocks);
+  const int V = nbv * p.nsplit;
+  const int chunk = (V + 7) >> 3;
+  const int L = (blockIdx.x & 7) * chunk + (blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= chunk || L >= V) return;
+  const int b0 = L / p.nsplit;
+  const int split = L - b0 * p.nsplit;
+  const int e = p.expert_ids[b0];
+  if (e < 0 || e >= p.experts) return;
+  if (R > 1 && b0 % R != 0 && p.expert_ids[b0 - 1] == e) return;   // inside another run
+  int nblk = 1;
+  if constexpr (R > 1) {
+    const int lim = min((b0 / R + 1) * R, nbv);
+    while (b0 + nblk < lim && p.expert_ids[b0 + nblk] == e) ++nblk;
+  }
+  const int rows_valid = nblk * TM;
+  const int ntn = p.N / TN;
+  const int j0 = split * ntn / p.nsplit, j1 = (split + 1) * ntn / p.nsplit;
+  if (j0 >= j1) return;
+  const int K = p.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
+  const int a_rows = p.tokens * p.topk;
+  constexpr bool kScaled = !kind_is_16bit(KIND);
+
+  // ---- the run's A rows, all NK steps, into LDS once (route row t*topk + s; padding rows read
+  // zeros past the buffer) ----
+  {
+    const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
+#pragma unroll
+    for (int j = 0; j < AQ; ++j) {
+      const int rloc = (wave + j * NW) * 8 + (lane >> 3);
+      const int id = p.sorted_ids[b0 * TM + min(rloc, rows_valid - 1)];
+      const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+      const bool ok = rloc < rows_valid && t < p.tokens && s < p.topk;
+      const int c = (lane & 7) ^ ((rloc >> 1) & 7);
+      const uint32_t va = ok ? (uint32_t)(t * p.topk + s) * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
+#pragma unroll
+      for (int kt = 0; kt < NK; ++kt)
+        dma16(rsrc_a, sa_lds + kt * A_STEP + (wave + j * NW) * 1024, va, (uint32_t)kt * KT);
+    }
+  }
+  // row factor (activation scale times routing weight) of this lane's rows mi*16 + l16, and the
+  // destinations of this thread's store chunks (the same rows for every tile)
+  float fr_r[MR];
+#pragma unroll
+  for (int mi = 0; mi < MR; ++mi) {
+    const int r = mi * 16 + l16;
+    const int id = p.sorted_ids[b0 * TM + min(r, rows_valid - 1)];
+    const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+    const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
+    const float sxv = kScaled ? p.sa[ok ? t * p.topk + s : 0] : 1.f;
+    const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
+    fr_r[mi] = ok ? sxv * rwv : 0.f;
+  }
+  int dst_c[HALVES][SCH];
+#pragma unroll
+  for (int h = 0; h < HALVES; ++h)
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+      const int r = h * HR + (tid + i * NW * 64) / CPR;
+      const int id = p.sorted_ids[b0 * TM + min(r, rows_valid - 1)];
+      const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
+      const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
+      dst_c[h][i] = ok ? t * p.topk + s : -1;
+    }
+  const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc(p.w + (size_t)e * (size_t)p.N * (size_t)K, p.N * K);
+  const __amdgpu_buffer_rsrc_t rsrc_s = make_rsrc(p.sw + (size_t)e * p.N, kScaled ? p.N * 4 : 0);
+  const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
+  const bool obf16 = moe_out_bf16(p.out_mode);
+
+  typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
+  i32x4 bw[2][NK][2];   // weight fragments of two column tiles: [set][K step][K half]
+  f32x4 sc[2];          // this lane's 4 column scales of each
+  // column scales and weights of column tile j into set U; every tile issues the same loads (a
+  // tile past the range reads zeros from past the buffers), so the compiler's counts hold
+  auto load_tile = [&](auto u_tag, int j) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_tag)::value;
+    const bool live = j < j1;
+    const uint32_t past = live ? 0u : 0x80000000u;
+    const int jj = live ? j : 0;
+    const uint32_t col = (uint32_t)(jj * TN + wave * 16 + lq * 4);
+    sc[U] = kScaled ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_s, col * 4u + past, 0, 0))
+                    : f32x4{1.f, 1.f, 1.f, 1.f};
+    const uint32_t so0 = (uint32_t)(jj * (TN / 16) + wave) * 16u * (uint32_t)K;
+    const uint32_t vo = (uint32_t)lane * 16u + past;
+#pragma unroll
+    for (int kt = 0; kt < NK; ++kt) {
+      const uint32_t so = so0 + (uint32_t)kt * 2048u;
+      bw[U][kt][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
+      bw[U][kt][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 1024u), 0);
+    }
+  };
+  auto tile = [&](auto u_tag, int j) __attribute__((always_inline)) {
+    constexpr int U = decltype(u_tag)::value;
+    load_tile(std::integral_constant<int, U ^ 1>{}, j + 1);   // before this tile's stores
+    AccT acc[MR];
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) acc[mi] = AccT{0, 0, 0, 0};
+#pragma unroll
+    for (int kt = 0; kt < NK; ++kt) {
+      const uint8_t* sA = sa_lds + kt * A_STEP;
+      const i32x4 bl = bw[U][kt][0], bh = bw[U][kt][1];
+#pragma unroll
+      for (int mi = 0; mi < MR; ++mi) {
+        const int row = mi * 16 + l16;
+        const int sw = (row >> 1) & 7;
+        const i32x4 lo = *(const i32x4*)(sA + row * KT + ((lq ^ sw) << 4));
+        const i32x4 hi = *(const i32x4*)(sA + row * KT + (((lq + 4) ^ sw) << 4));
+        if constexpr (KIND == KIND_FP8) {
+          acc[mi] = mfma_fp8(__builtin_shufflevector(bl, bh, 0, 1, 2, 3, 4, 5, 6, 7),
+                             __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[mi]);
+        } else {
+          acc[mi] = mfma_k64<KIND>(bl, lo, acc[mi]);
+          acc[mi] = mfma_k64<KIND>(bh, hi, acc[mi]);
+        }
+      }
+    }
+    // epilogue: value = accumulator * column scale * row factor (the order of moe.h's rows)
+    const uint32_t n0b = (uint32_t)(j * TN) * 2u;
+#pragma unroll
+    for (int h = 0; h < HALVES; ++h) {
+      workgroup_barrier();   // the staging rows have been read out
+#pragma unroll
+      for (int mh = 0; mh < MR / HALVES; ++mh) {
+        const int mi = h * (MR / HALVES) + mh;
+        const int r = mh * 16 + l16;
+        const int c = wave * 16 + lq * 4;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = ((float)acc[mi][q] * sc[U][q]) * fr_r[mi];
+        const i32x2 pk = obf16 ? pack_out4<true>(v) : pack_out4<false>(v);
+        *(i32x2*)(stg + r * RB + (((c >> 3) ^ (r % CPR)) << 4) + (c & 7) * 2) = pk;
+      }
+      workgroup_barrier();
+#pragma unroll
+      for (int i = 0; i < SCH; ++i) {
+        const int cc = tid + i * NW * 64;
+        const int r = cc / CPR, ch = cc % CPR;
+        const i32x4 val = *(const i32x4*)(stg + r * RB + ((ch ^ (r % CPR)) << 4));
+        const int d = dst_c[h][i];
+        // padding rows: an offset past the buffer (out_bytes <= 0xFFFFFF00) that a 16-byte
+        // store cannot wrap
+        const uint32_t off = d < 0 ? 0xFFFFFFE0u : (uint32_t)d * (uint32_t)p.N * 2u + n0b + (uint32_t)ch * 16u;
+        __builtin_amdgcn_raw_buffer_store_b128(val, rsrc_o, off, 0, 0);
+      }
+    }
+  };
+  load_tile(std::integral_constant<int, 0>{}, j0);
+  waitcnt<0>();
+  workgroup_barrier();   // the A rows are in LDS for every wave
+  int j = j0;
+  for (; j + 2 <= j1; j += 2) {
+    tile(std::integral_constant<int, 0>{}, j);
+    tile(std::integral_constant<int, 1>{}, j + 1);
+  }
+  if (j < j1) tile(std::integral_constant<int, 0>{}, j);
+}
+
+}  // namespace flygemm

@@ -383,6 +383,55 @@ def test_stage2_reduce_mode(gpu, kind, shape, out_dtype):
     _check(out, ref_stage2(p, True, route_round=out_dtype), what=f"reduce {shape} {kind} {out_dtype}")
 
 
+def _reduce(p, gpu, out_dtype, doweight=True, rows=None):
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+    w = p["workload"]
+    fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                              tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=_tile_k(w.kind), doweight_stage2=doweight,
+                              in_dtype=w.kind, out_dtype=out_dtype, mode=MoeGemm2Mode.REDUCE)
+    out = torch.full((w.tokens, w.model_dim), float("nan"), dtype=OUT_T[out_dtype], device=gpu)
+    empty = torch.empty(0, dtype=torch.float32, device=gpu)
+    fn(out, H.dev_flat(p["a2"], gpu), H.dev_flat(p["w2_shuf"], gpu), empty if p["sa2"] is None else p["sa2"],
+       empty if p["sw2"] is None else p["sw2"], p["sorted_ids"], p["sorted_expert_ids"], p["sorted_weights"],
+       p["num_valid_ids"], w.tokens, w.model_dim, w.inter_dim, p["blocks"])
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8", "bf16", "fp16"])
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+def test_stage2_stream_rows_depths(gpu, kind, tile_m):
+    """Reduce mode's GEMM for these kinds runs the stage-2 stream kernel when inter_dim is 1, 2 or
+    4 128-byte K steps (A resident for the run, the weights of the next 64-column tile loaded
+    before this tile's row stores, rows staged in two rounds); 3 steps keep the single-block
+    kernel.  300 tokens top-3 of 5 experts (runs cut at expert boundaries, partial runs), model_dim
+    320; routing weights on and off, fp16 and bf16 rows, judged after the top-k reduction
+    against the oracle with per-route rounding."""
+    for nk in (1, 2, 3, 4):
+        inter = nk * 128 // (2 if kind in ("bf16", "fp16") else 1)
+        w = W.moe_custom(300, 320, inter, 5, 3, tile_m, 64, 64, kind, seed=nk * 10 + tile_m + 3)
+        p = W.moe_problem(w, gpu)
+        for doweight, out_dtype in ((True, "f16"), (False, "bf16")):
+            _say(f"stream stage2 rows {kind} tile_m={tile_m} K steps={nk} doweight={doweight} out={out_dtype}")
+            out = _reduce(p, gpu, out_dtype, doweight)
+            _check(out, ref_stage2(p, doweight, route_round=out_dtype),
+                   what=f"stream2 {kind} tm{tile_m} nk{nk} w{int(doweight)} {out_dtype}")
+
+
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+def test_stage2_stream_rows_tile_walks(gpu, tile_m):
+    """A routing with many runs (4096 tokens top-8 of 16 experts): four column ranges per run over
+    model_dim 704 (11 column tiles), so each workgroup walks two or three tiles, its register sets
+    alternating and the last one alone; all routes computed, a sample of tokens checked."""
+    w = W.moe_custom(4096, 704, 256, 16, 8, tile_m, 64, 64, "fp8", seed=40 + tile_m)
+    p = W.moe_problem(w, gpu)
+    rows = np.unique(np.r_[np.linspace(0, w.tokens - 1, 24).astype(int), w.tokens - 1])
+    _say(f"stream stage2 tile walks tile_m={tile_m}")
+    out = _reduce(p, gpu, "f16", True)
+    assert torch.isfinite(out.float()).all()
+    _check(out, ref_stage2(p, True, rows, route_round="f16"), rows, what=f"stream2 walks tm{tile_m}")
+
+
 def test_stage2_reduce_mode_with_valid_mask(gpu):
     """Slots whose valid_mask is 0 are left out of the sum (the reference's masked reduction)."""
     from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
