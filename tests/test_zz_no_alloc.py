@@ -114,19 +114,22 @@ def test_first_call_under_capture_is_refused(gpu):
         _same(out, want, f"captured replay {i}")
 
 
-CASES = [  # (first shape, kind, group, out dtype, second (smaller) tokens)
-    ("MM", "fp8", -1, "fp16", 40),
-    ("MM", "bf16", -1, "bf16", 17),
-    ("MM", "int4_bf16", 32, "bf16", 64),
-    ("DSD", "fp8", -1, "bf16", 3),
+CASES = [  # (shape, kind, group, out dtype, first tokens (None: the shape's), second (smaller) tokens)
+    ("MM", "fp8", -1, "fp16", None, 40),
+    ("MM", "bf16", -1, "bf16", None, 17),
+    ("MM", "int4_bf16", 32, "bf16", None, 64),
+    ("DSD", "fp8", -1, "bf16", None, 3),
+    # 600 tokens top-2 of 8 experts: a full 128-row run per expert, so the GEMM runs the
+    # stage-2 stream kernel; the second call (100 tokens) the single-block kernel
+    ("MM", "fp8", -1, "bf16", 600, 100),
 ]
 
 
-@pytest.mark.parametrize("shape,kind,group,out_dtype,tokens2", CASES)
-def test_noalloc_matches_two_calls_twice(gpu, shape, kind, group, out_dtype, tokens2):
+@pytest.mark.parametrize("shape,kind,group,out_dtype,tokens1,tokens2", CASES)
+def test_noalloc_matches_two_calls_twice(gpu, shape, kind, group, out_dtype, tokens1, tokens2):
     """Two calls in a row, the second with fewer tokens (and other data), each equal to the
     existing two-call reduce mode bit for bit."""
-    for tokens, seed in ((None, 0), (tokens2, 7)):
+    for tokens, seed in ((tokens1, 0), (tokens2, 7)):
         p = _problem(shape, kind, gpu, tokens=tokens, group_size=group, seed=seed)
         w = p["workload"]
         _say(f"noalloc {shape} {kind} g={group} {out_dtype} tokens={w.tokens}")
