@@ -432,6 +432,37 @@ def test_stage2_stream_rows_tile_walks(gpu, tile_m):
     _check(out, ref_stage2(p, True, rows, route_round="f16"), rows, what=f"stream2 walks tm{tile_m}")
 
 
+def test_stage2_stream_rows_graph_capture(gpu):
+    """The reduce mode with its GEMM on the stage-2 stream kernel (600 tokens top-2 of 8 experts:
+    a full 128-row run per expert) captured with torch.cuda.graph after an eager run; every
+    replay, with eager work in between, equals the eager result bit for bit."""
+    from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
+    w = W.moe_custom(600, 1024, 256, 8, 2, 32, 128, 128, "fp8", seed=51)
+    p = W.moe_problem(w, gpu)
+    _say("stream stage2 rows under graph capture")
+    eager = _reduce(p, gpu, "bf16", True).clone()
+    _check(eager, ref_stage2(p, True, route_round="bf16"), what="stream2 graph eager")
+    fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
+                              tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=128, doweight_stage2=True, in_dtype="fp8",
+                              out_dtype="bf16", mode=MoeGemm2Mode.REDUCE)
+    out = torch.full((w.tokens, w.model_dim), float("nan"), dtype=torch.bfloat16, device=gpu)
+    args = (H.dev_flat(p["a2"], gpu), H.dev_flat(p["w2_shuf"], gpu), p["sa2"], p["sw2"], p["sorted_ids"],
+            p["sorted_expert_ids"], p["sorted_weights"], p["num_valid_ids"], w.tokens, w.model_dim, w.inter_dim,
+            p["blocks"])
+    fn(out, *args)   # eager first call on the capture's tensors
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn(out, *args, torch.cuda.current_stream())
+    for i in range(3):
+        out.fill_(float("nan"))
+        _reduce(p, gpu, "f16", False)   # eager use of the same kernels between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {i}"
+
+
 def test_stage2_reduce_mode_with_valid_mask(gpu):
     """Slots whose valid_mask is 0 are left out of the sum (the reference's masked reduction)."""
     from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
