@@ -27,10 +27,12 @@
 //
 // W1 and W2 are preshuffled like every B operand here.  A rows are gathered by the LDS-DMA:
 // each lane's buffer offset names its own row, and padding rows get an offset past the buffer,
-// which reads zeros.  One workgroup (4 waves) per (TN-column block, sorted block of TM rows);
-// wave w owns columns [w*TN/4, (w+1)*TN/4) of the block for all TM rows (stage 1: of the gate
-// and of the up projection).  Two LDS stages, one barrier per 128-byte K tile, LDS layouts as in
-// the large-M kernel (gemm_main.h): A rows with the XOR chunk swizzle, B copied verbatim.
+// which reads zeros.  The kernel below (moe_gemm_kernel) keeps A and B in a two-slot LDS ring,
+// one barrier per 128-byte K tile, LDS layouts as in the large-M kernel (gemm_main.h): A rows
+// with the XOR chunk swizzle, B copied verbatim.  It runs stage 2 (atomics; per-route rows of
+// decode-sized routings and of W4A16 / int4 / deeper inter_dim) and stage 1 of W4A16 and of
+// blockscale; moe_stream.h holds the kernels that stream the weights into registers (stage 1
+// of the other kinds, stage 2 per-route rows of prefill routings).
 #pragma once
 #include "gemm_main.h"
 
@@ -102,9 +104,9 @@ __device__ __forceinline__ float silu_f(float x) {
 
 // F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
 // bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
-template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, int NS_ = 2, bool SCW = false>
+template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, bool SCW = false>
 struct MoeCfg {
-  static constexpr int NS = NS_;                      // LDS ring slots: the DMA runs NS-1 steps ahead
+  static constexpr int NS = 2;                        // LDS ring slots: the DMA runs one step ahead
   static constexpr int NW = WM * WN;                  // waves: WM across the rows, WN across the columns
   static constexpr int TME = TM * R;                  // rows of one run: up to R routing blocks
   static constexpr int TMW = TME / WM;                // rows per wave
@@ -136,9 +138,6 @@ struct MoeCfg {
                 "tile shape");
   static_assert(B_BYTES % 1024 == 0, "B DMA in whole instructions");
   static_assert(CH >= 16 && NS * SLOT <= 160 * 1024, "LDS budget");
-  static_assert(NS == 2 || (NS == 3 && A_DMA % NW == 0 && B_DMA % NW == 0),
-                "a 3-slot ring counts equal DMA issues per wave");
-  static constexpr int DMA_PER_STEP = (NS == 3 ? A_DMA / NW : 0) + BQ;  // per wave (3-slot ring)
 };
 
 // One workgroup (WM x WN waves) per (run, column range): a run is up to R consecutive routing blocks of
@@ -156,20 +155,18 @@ struct MoeCfg {
 // [E*wrows/128][K/128] (one per 128x128 block); each K step's MFMA partial is scaled by
 // sa[kb][row] * sw[row block of the column][kb] and added to the accumulator (reference
 // kernels/moe_blockscale_2stage.py:677-777 for stage 1, :1836-1880 for stage 2).
-template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, bool BS = false, int NS = 2>
+template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, bool BS = false>
 __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
-  using C = MoeCfg<STAGE, KIND, TM, R, TN, WM, WN, F32, NS, !kind_is_16bit(KIND) && !BS>;
-  static_assert(NS == 2 || (!BS && STAGE == 1), "the 3-slot ring is for stage 1 row outputs");
+  using C = MoeCfg<STAGE, KIND, TM, R, TN, WM, WN, F32, !kind_is_16bit(KIND) && !BS>;
   constexpr int NW = C::NW, TMW = C::TMW;
   static_assert(!BS || KIND == KIND_FP8, "blockscale is fp8");
   static_assert(STAGE == 2 || !F32, "stage 1 writes 2-byte outputs");
   static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND) || moe_w_int4(KIND), "MoE input kinds");
-  static_assert(KIND != KIND_W4A16 || NS == 2, "W4A16 group scales ride the two-slot pipeline");
   constexpr int MR = C::MR, NR = C::NR, NB = C::NB, TME = C::TME, NT = NW * 64;
   const int mode = p.out_mode;
   const bool rows = STAGE == 1 || mode == MOE_OUT_F16_ROWS || mode == MOE_OUT_BF16_ROWS;
   const bool obf16 = moe_out_bf16(mode);
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[C::NS * C::SLOT];
   // Row outputs of tiles of 128+ columns go through the slot the tile's last K step computed
   // from, in two rounds of half of every wave's rows, and leave as 16-byte chunks so each wave
   // instruction writes whole 128-byte lines (the accumulator layout's direct stores cover 16
@@ -178,8 +175,8 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   // round h is tile row (sr / HR) * TMW + h * HR + sr % HR; its 16-byte chunk c sits at chunk
   // c ^ (sr % CPR).  NSTR: row stores per lane per tile.
   constexpr int RB = TN * 2, CPR = RB / 16, HR = TMW / 2, HMR = MR / 2;
-  // (stage 2 only: stage 1 writes a 2*I-times smaller output and its run tiles were 1.7% slower
-  // staged; DS-TP8 prefill stage 2 in reduce mode 0.71 ms against 0.77)
+  // (stage 2 only: stage 1 writes a 2*I-times smaller output, and 128-row stage-1 tiles were
+  // 1.7% slower staged; DS-TP8 prefill stage 2 in reduce mode 0.71 ms against 0.77)
   constexpr bool kStageRows = STAGE == 2 && !F32 && MR % 2 == 0 && TN >= 128 && TME / 2 * RB <= C::SLOT_DATA &&
                               (TME / 2 * CPR) % NT == 0;
   constexpr int SCHR = kStageRows ? TME / 2 * CPR / NT : 0;
@@ -189,7 +186,7 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   // every column tile has the same K tiles, so K tile kt's A rows stay in the A part of slot kt
   // (of both slots for a single K tile) after the first column tile (two for a single K tile),
   // and later steps DMA only B.  The row staging then uses the last slot's B part.
-  constexpr bool kAres = STAGE == 2 && NS == 2 && !F32 && !BS && (!kStageRows || TME / 2 * RB <= C::B_BYTES);
+  constexpr bool kAres = STAGE == 2 && !F32 && !BS && (!kStageRows || TME / 2 * RB <= C::B_BYTES);
 
   // ---- which run and which column tiles ----
   // Logical id L = block * nsplit + split over the blocks below num_valid_ids, dealt to the 8
@@ -591,43 +588,6 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   // barrier, issues the next step's DMA into the other slot -- the next K tile, or the first of
   // the next column tile -- and computes.  The epilogue's row stores go out after that DMA, so
   // the next step's wait leaves them in flight (vector memory operations retire in issue order).
-  if constexpr (NS == 3) {
-    // Three slots, the DMA two steps ahead (for stage 1, whose gathered rows miss the L2 and
-    // whose tiles are long).  A step's DMA is complete once no more than the next step's
-    // DMA_PER_STEP operations are outstanding; the last step waits for everything.  Row stores
-    // issued between, and the column-scale DMA that the last waves add to a tile's last step,
-    // may make that wait longer, never too short.
-    const int S = (j1 - j0) * nk;
-    int ij = j0, ik = 0;  // the next step to issue
-    auto issue_next = [&](int sl) {
-      issue(ij, ik, sl);
-      if (++ik == nk) { ik = 0; ++ij; }
-    };
-    issue_next(0);
-    if (S > 1) issue_next(1);
-    int s = 0, slot = 0, last = 0;
-    for (int jt = j0; jt < j1; ++jt) {
-#pragma unroll
-      for (int h = 0; h < NB; ++h)
-#pragma unroll
-        for (int i = 0; i < MR; ++i)
-#pragma unroll
-          for (int j = 0; j < NR; ++j) acc[h][i][j] = AccT{0, 0, 0, 0};
-      for (int kt = 0; kt < nk; ++kt, ++s) {
-        if (s + 1 < S)
-          waitcnt<C::DMA_PER_STEP>();
-        else
-          wait_dma();
-        workgroup_barrier();  // step s's slot is published; every wave is done with step s-1's
-        if (s + 2 < S) issue_next(slot == 0 ? 2 : slot - 1);   // the slot step s-1 used
-        compute(ring + slot * C::SLOT);
-        last = slot;
-        slot = slot == 2 ? 0 : slot + 1;
-      }
-      epilogue(jt, nullptr, ring + last * C::SLOT);   // row outputs: stored from registers
-    }
-    return;
-  }
   int slot = 0;
   bool keep_stores = false;
   load_bs(j0, 0);

@@ -25,12 +25,11 @@ namespace {
 
 template <int KIND, bool BS>
 MoeKernel moe_stage1_tile(int tm, int r, int tn) {
-#define T(M_, R_, N_, WM_, WN_, NS_) \
-  if (tm == M_ && r == R_ && tn == N_)  \
-    return MoeKernel{moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS, NS_>, WM_ * WN_ * 64};
-  T(16, 1, 64, 1, 4, 2) T(16, 1, 128, 1, 4, 2) T(16, 1, 256, 1, 4, 2) T(32, 1, 64, 1, 4, 2)
-  T(32, 1, 128, 1, 4, 2) T(32, 1, 256, 1, 4, 2) T(64, 1, 64, 1, 4, 2) T(64, 1, 128, 1, 4, 2)
-  T(64, 1, 256, 1, 4, 2)
+#define T(M_, R_, N_, WM_, WN_)        \
+  if (tm == M_ && r == R_ && tn == N_) \
+    return MoeKernel{moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS>, WM_ * WN_ * 64};
+  T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(16, 1, 256, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4)
+  T(32, 1, 256, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4) T(64, 1, 256, 1, 4)
 #undef T
   return MoeKernel{nullptr, 0};
 }
@@ -85,7 +84,7 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
   }
   // Stage 2 of 16-row blocks: runs of 256 rows x 256 columns on 2 x 4 waves when experts hold two
   // or more blocks on average.  Not for blockscale nor W4A16 (their scales do not fit next to the
-  // run tiles); stage 1 of those two kinds keeps single-block tiles.
+  // run tiles); stage 1 of those two kinds uses single-block tiles.
   // Stage 2 of 32- and 64-row blocks keeps single-block tiles (128 columns, below): with three
   // workgroups per CU their epilogues and row stores overlap each other's MFMAs.  DS-TP8 dims
   // (128 experts, model_dim 7168, inter_dim 256), fp8, graph-timed: 64-row blocks, reduce mode

@@ -664,7 +664,8 @@ def test_new_kinds_every_tile(gpu, kind, group, tile_m, tile_n):
 @pytest.mark.parametrize("kind", ["int4", "int8smooth"])
 @pytest.mark.parametrize("tile_m", [16, 64])
 def test_new_kinds_runs_of_blocks(gpu, kind, tile_m):
-    """Experts with many routing blocks take the 8-wave run tiles (W4A16 keeps single blocks)."""
+    """Experts with many routing blocks: stage 1 on the stream kernel's 128-row runs, stage 2 on
+    the 8-wave run tiles (16-row blocks) or single-block tiles."""
     w = W.moe_custom(600, 512, 256, 5, 2, tile_m, 128, 256, kind, seed=tile_m * 3)
     p = W.moe_problem(w, gpu)
     rows = np.unique(np.r_[np.arange(0, 600, 7), 599])
