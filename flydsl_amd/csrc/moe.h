@@ -102,6 +102,38 @@ __device__ __forceinline__ float silu_f(float x) {
   return x * __builtin_amdgcn_rcpf(1.f + e);
 }
 
+// Runs of up to R sorted blocks of one expert, counted from the expert's first block (the
+// sorting writes an expert's blocks contiguously): the block count of the run starting at
+// block b0 (expert e, nbv blocks in use), or 0 when b0 lies inside a run.  Counting from the
+// expert's first block rather than from multiples of R gives ceil(blocks / R) runs per expert;
+// runs aligned to multiples of R split an expert whose blocks start at an odd position into one
+// more run, which streams the expert's weights once more (DS-TP8 prefill, 64-row blocks, R = 2:
+// 608 runs against 577).  Every lane reads one expert id behind b0 (and one ahead); the ballots
+// make the result uniform over the wave and, all waves reading the same ids, the workgroup.
+template <int R>
+__device__ __forceinline__ int moe_run_blocks(const int32_t* expert_ids, int b0, int e, int nbv, int lane) {
+  if constexpr (R == 1) {
+    return 1;
+  } else {
+    static_assert(R < 64, "one ballot covers a run");
+    int before = 0;                           // blocks of expert e directly before b0
+    for (int base = b0;; base -= 64) {
+      const int b = base - 1 - lane;
+      const bool other = b < 0 || expert_ids[b] != e;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(other);
+      if (m != 0) {
+        before += __builtin_ctzll(m);
+        break;
+      }
+      before += 64;
+    }
+    if (before % R != 0) return 0;
+    const int lim = min(R, nbv - b0);         // blocks b0 .. b0 + lim - 1 may join the run
+    const bool other = lane >= lim || expert_ids[b0 + lane] != e;
+    return __builtin_ctzll(__builtin_amdgcn_ballot_w64(other) | (1ull << 63));
+  }
+}
+
 // F32: fp32 output (stage 2 with atomics only); otherwise 2-byte outputs, whose type (fp16 or
 // bf16) and mode (rows or atomics) are run-time facts of MoeArgs::out_mode.
 template <int STAGE, int KIND, int TM, int R, int TN, int WM, int WN, bool F32, bool SCW = false>
@@ -202,12 +234,8 @@ __global__ void __launch_bounds__(WM * WN * 64) moe_gemm_kernel(MoeArgs p) {
   const int split = L - b0 * p.nsplit;
   const int e = p.expert_ids[b0];
   if (e < 0 || e >= p.experts) return;
-  if (R > 1 && b0 % R != 0 && p.expert_ids[b0 - 1] == e) return;   // inside another run
-  int nblk = 1;
-  if constexpr (R > 1) {
-    const int lim = min((b0 / R + 1) * R, nbv);
-    while (b0 + nblk < lim && p.expert_ids[b0 + nblk] == e) ++nblk;
-  }
+  const int nblk = moe_run_blocks<R>(p.expert_ids, b0, e, nbv, threadIdx.x & 63);
+  if (nblk == 0) return;                       // inside another run
   const int rows_valid = nblk * TM;
   const int ntn = p.N / TN;
   const int j0 = split * ntn / p.nsplit, j1 = (split + 1) * ntn / p.nsplit;

@@ -71,12 +71,8 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
   const int jt = L - b0 * p.nsplit;
   const int e = p.expert_ids[b0];
   if (e < 0 || e >= p.experts) return;
-  if (R > 1 && b0 % R != 0 && p.expert_ids[b0 - 1] == e) return;   // inside another run
-  int nblk = 1;
-  if constexpr (R > 1) {
-    const int lim = min((b0 / R + 1) * R, nbv);
-    while (b0 + nblk < lim && p.expert_ids[b0 + nblk] == e) ++nblk;
-  }
+  const int nblk = moe_run_blocks<R>(p.expert_ids, b0, e, nbv, threadIdx.x & 63);
+  if (nblk == 0) return;                       // inside another run
   const int rows_valid = nblk * TM;
   const int K = p.K, nk = K / KT;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -311,12 +307,8 @@ __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
   const int split = L - b0 * p.nsplit;
   const int e = p.expert_ids[b0];
   if (e < 0 || e >= p.experts) return;
-  if (R > 1 && b0 % R != 0 && p.expert_ids[b0 - 1] == e) return;   // inside another run
-  int nblk = 1;
-  if constexpr (R > 1) {
-    const int lim = min((b0 / R + 1) * R, nbv);
-    while (b0 + nblk < lim && p.expert_ids[b0 + nblk] == e) ++nblk;
-  }
+  const int nblk = moe_run_blocks<R>(p.expert_ids, b0, e, nbv, threadIdx.x & 63);
+  if (nblk == 0) return;                       // inside another run
   const int rows_valid = nblk * TM;
   const int ntn = p.N / TN;
   const int j0 = split * ntn / p.nsplit, j1 = (split + 1) * ntn / p.nsplit;
