@@ -78,7 +78,11 @@ struct Shape {
   X(4, 1, 8, 3)          \
   X(4, 2, 8, 2)          \
   X(8, 1, 8, 2)          \
-  X(8, 2, 8, 1)
+  X(8, 2, 8, 1)          \
+  X(1, 2, 4, 4)          \
+  X(1, 4, 4, 4)          \
+  X(1, 5, 4, 3)          \
+  X(1, 7, 4, 2)
 
 // The streaming kernel over row blocks (plain B loads: the row blocks of a column group re-read
 // B from L2): for M too large for one row block but too small for the tiled kernel to give
@@ -208,23 +212,29 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     const int rows = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
     const int nblk = N / 16;
     // One 16-row block of fp8 / int8 / int4 codes: the most column blocks per workgroup whose
-    // workgroups fill their last round over the CUs to at least 85% -- a partly filled last
-    // round runs the tail on a fraction of the chip (graph-timed on MI355X, fp8 16 x N x K:
-    // 40960x5120 35.3 us with 5 blocks (512 workgroups, two full rounds) against 39.5 with 7
-    // (366, the last round 43% full); 24576x8192 32.8 with 7 (220, 86%) against 39.0 with 4
-    // (384, 50%); 14336x4096 11.7 with 4 (224) against 13.8 with 7 (128); int4 40960x5120 19.2
-    // with 10 blocks (256) against 23.9 with 7; the rule picks the fastest measured variant or
-    // one within 6% on 10 shapes per kind).  Ten blocks only for int4, whose blocks carry half
-    // the bytes (fp8 with ten spills registers: 77.6 us on 40960x5120).
+    // workgroups fill their last round over the 256 CUs to at least 75% -- a partly filled last
+    // round runs the tail on a fraction of the chip -- in 4-wave workgroups for fp8 and int8 (two
+    // share a CU, one's reduction and epilogue under the other's loads; one block per workgroup
+    // keeps 8 waves) and 8-wave ones for int4.  Graph-timed on MI355X, 16 x N x K for 12 N x K
+    // per kind against every variant, the rule lands within 4% of the fastest: fp8 40960x5120
+    // 33.7 us with 5 blocks on 4 waves (512 workgroups) against 35.4 on 8 waves and 38.6 with 7
+    // (366, the last round 43% full); 77824x5120 62.5 against 65.1 on 8 waves (fastest: 4 blocks,
+    // 60.1); 57344x8192 70.6 against 72.3; 12288x4096 10.5 with 4 blocks (192 workgroups)
+    // against 13.3 with 1 (the former 85% bar); 28672x8192 37.9 either way; int8 alike; int4
+    // 40960x5120 19.3 with 10 blocks (256), its 4-wave forms level or up to 11% slower.  Ten
+    // blocks only for int4, whose blocks carry half the bytes (fp8 with ten spills registers:
+    // 77.6 us on 40960x5120).
     if (rows == 16 && (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_INT4) && epi != EPI_BLOCK) {
       int best = -1;
       for (int v = kFirstDecode; v < kFirstRows; ++v) {
         if (kShapes[v].bm != 16) continue;
         const int nbw = kShapes[v].bn / 16;
+        const bool four = kShapes[v].threads == 256;
         if (nbw == 10 && kind != KIND_INT4) continue;
+        if (four != (kind != KIND_INT4 && nbw > 1)) continue;
         const long wg = (nblk + nbw - 1) / nbw;
         const long rounds = (wg + kCUs - 1) / kCUs;
-        if (wg * 100 >= rounds * kCUs * 85 && (best < 0 || nbw > kShapes[best].bn / 16)) best = v;
+        if (wg * 100 >= rounds * kCUs * 75 && (best < 0 || nbw > kShapes[best].bn / 16)) best = v;
       }
       if (best >= 0) return best;
     }
@@ -235,6 +245,7 @@ int select_variant(int M, int N, int K, int kind, int epi) {
       const int nbw = kShapes[v].bn / 16;
       if (kind == KIND_FP4 && nbw > 4) continue;  // MXFP4's scale words push 7 blocks past the register file
       if (nbw == 5 || nbw == 10) continue;        // measured only for the codes above
+      if (kShapes[v].threads == 256) continue;    // the 4-wave forms: likewise
       // int4 blocks carry half the bytes: 4 blocks per workgroup beat 2 even at 224 workgroups
       // (16x14336x4096: 7.6 us against 8.5)
       const int min_wg = kind == KIND_INT4 ? 200 : 240;

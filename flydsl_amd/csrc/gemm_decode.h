@@ -35,8 +35,10 @@ __device__ __forceinline__ T load_b(const T* p) {
     return *p;
 }
 
+// NW = 4: two workgroups share a CU (at most 256 registers per lane, as for 8 waves), so one
+// workgroup's reduction and epilogue run under the other's loads.
 template <int MR, int NBW, int NW, int UNROLL, int KIND, int EPI, bool OUT_BF16, bool NT_B = true>
-__global__ void __launch_bounds__(NW * 64) gemm_decode_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(NW * 64, 8 / NW) gemm_decode_kernel(GemmArgs p) {
   const int M = p.M, N = p.N, K = p.K;
   // full 128-byte K tiles; K (bytes) is a multiple of 64, and when K % 128 == 64 the last 64
   // bytes form a half tile, taken after the pipeline (see below)

@@ -38,7 +38,7 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(16, 28672, 8192, 0, 0)].startswith("decode_m1")
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 1, 0)].startswith("main_")
     # every shape gets a variant, and the five configurations get the tiles measured fastest
-    expect = {(128, 4096, 4096, 0, 0): "rows_m2_nb4_w8_u3", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w8_u2",
+    expect = {(128, 4096, 4096, 0, 0): "rows_m2_nb4_w8_u3", (16, 28672, 8192, 0, 0): "decode_m1_nb7_w4_u2",
               (4096, 4096, 4096, 1, 0): "main_256x256_w2x4", (1024, 7168, 7168, 0, 1): "main_128x256_w2x4",
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
@@ -113,15 +113,15 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(128, 4096, 4096, 5, 0)] == "rows_m1_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(128, 4096, 2048, 3, 0)] == "rows_m2_nb4_w8_u3"  # 2 bytes/elt
     # decode of one 16-row block (fp8 / int8 / int4 codes): the most column blocks per workgroup
-    # whose workgroups fill their last round over 256 CUs to at least 85%; ten blocks only for
-    # int4 (half-size blocks)
-    dec = {(16, 14336, 4096, 2): "nb4", (16, 14336, 4096, 1): "nb4", (16, 40960, 5120, 0): "nb5",
-           (16, 40960, 5120, 1): "nb5", (16, 40960, 5120, 2): "nb10", (16, 77824, 5120, 0): "nb7",
-           (16, 77824, 5120, 2): "nb10", (16, 24576, 8192, 0): "nb7", (16, 7168, 2048, 0): "nb2",
-           (16, 4096, 4096, 1): "nb1", (1, 57344, 8192, 0): "nb7", (16, 28672, 8192, 2): "nb7"}
+    # whose workgroups fill their last round over 256 CUs to at least 75%; 4-wave workgroups for
+    # fp8 / int8 with 2+ blocks, ten blocks only for int4 (half-size blocks)
+    dec = {(16, 14336, 4096, 2): "nb4_w8_u3", (16, 14336, 4096, 1): "nb4_w4_u4", (16, 40960, 5120, 0): "nb5_w4_u3",
+           (16, 40960, 5120, 1): "nb5_w4_u3", (16, 40960, 5120, 2): "nb10_w8_u2", (16, 77824, 5120, 0): "nb7_w4_u2",
+           (16, 77824, 5120, 2): "nb10_w8_u2", (16, 24576, 8192, 0): "nb7_w4_u2", (16, 7168, 2048, 0): "nb2_w4_u4",
+           (16, 4096, 4096, 1): "nb1_w8_u4", (1, 57344, 8192, 0): "nb7_w4_u2", (16, 28672, 8192, 2): "nb7_w8_u2",
+           (16, 12288, 4096, 0): "nb4_w4_u4", (16, 12288, 4096, 2): "nb4_w8_u3", (16, 28672, 8192, 1): "nb7_w4_u2"}
     for (m, n, k, ind), want in dec.items():
-        assert names[lib.flygemm_select_variant(m, n, k, ind, 0)] == f"decode_m1_{want}_w8_" + \
-            {"nb1": "u4", "nb2": "u4", "nb4": "u3", "nb5": "u3", "nb7": "u2", "nb10": "u2"}[want], (m, n, k, ind)
+        assert names[lib.flygemm_select_variant(m, n, k, ind, 0)] == f"decode_m1_{want}", (m, n, k, ind)
     # other kinds keep the rule of about one workgroup per CU (bf16 16x40960x5120: 2560 blocks)
     assert names[lib.flygemm_select_variant(16, 40960, 5120, 3, 0)] == "decode_m1_nb7_w8_u2"
     # MXFP4 decode keeps to at most 4 column blocks per workgroup
