@@ -211,28 +211,37 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // decode family: fewest rows that cover M, then the column blocks per workgroup
     const int rows = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
     const int nblk = N / 16;
-    // One 16-row block of fp8 / int8 / int4 codes: the most column blocks per workgroup whose
-    // workgroups fill their last round over the 256 CUs to at least 75% -- a partly filled last
-    // round runs the tail on a fraction of the chip -- in 4-wave workgroups for fp8 and int8 (two
-    // share a CU, one's reduction and epilogue under the other's loads; one block per workgroup
-    // keeps 8 waves) and 8-wave ones for int4.  Graph-timed on MI355X, 16 x N x K for 12 N x K
-    // per kind against every variant, the rule lands within 4% of the fastest: fp8 40960x5120
-    // 33.7 us with 5 blocks on 4 waves (512 workgroups) against 35.4 on 8 waves and 38.6 with 7
-    // (366, the last round 43% full); 77824x5120 62.5 against 65.1 on 8 waves (fastest: 4 blocks,
-    // 60.1); 57344x8192 70.6 against 72.3; 12288x4096 10.5 with 4 blocks (192 workgroups)
-    // against 13.3 with 1 (the former 85% bar); 28672x8192 37.9 either way; int8 alike; int4
-    // 40960x5120 19.3 with 10 blocks (256), its 4-wave forms level or up to 11% slower.  Ten
-    // blocks only for int4, whose blocks carry half the bytes (fp8 with ten spills registers:
-    // 77.6 us on 40960x5120).
-    if (rows == 16 && (kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_INT4) && epi != EPI_BLOCK) {
+    // One 16-row block: the most column blocks per workgroup whose workgroups fill their last
+    // round over the 256 CUs to at least 75% -- a partly filled last round runs the tail on a
+    // fraction of the chip.  Column groups of 2-7 blocks run in 4-wave workgroups (two share a
+    // CU, one's reduction and epilogue under the other's loads), one block in 8 waves; int4
+    // keeps 8 waves and alone takes ten blocks (half-size blocks; fp8 with ten spills registers:
+    // 77.6 us on 40960x5120); MXFP4 takes at most two (its scale words spill four on 4 waves),
+    // on 4 waves only above 256 workgroups.  Graph-timed on MI355X against every variant, 16 x N
+    // x K, 12 N x K per kind (10 for blockscale), the rule lands within 5% of the fastest on all
+    // but two (blockscale 24576x1536 and 32768x512, 25% / 7%): fp8 40960x5120 33.7 us (5 blocks,
+    // 512 workgroups) against 35.4 on 8 waves and 38.6 with 7 blocks (366, the last round 43%
+    // full); 77824x5120 62.5 against 65.1; 12288x4096 10.5 with 4 blocks (192 workgroups)
+    // against 13.3 with 1 (the former 85% bar); 28672x8192 37.9 either way; int8 alike; bf16
+    // 40960x5120 63.0 against 74.0 (the former rule for other kinds), 18432x7168 41.3 against
+    // 58.1; MXFP4 24576x8192 18.9 against 23.4; blockscale 36864x7168 41.9 against 61.1,
+    // 18432x7168 22.3 against 31.1; int4 40960x5120 19.3 with 10 blocks, its 4-wave forms level
+    // or up to 11% slower.  Without a choice that fills 75% (few columns), the rule below.
+    if (rows == 16) {
       int best = -1;
       for (int v = kFirstDecode; v < kFirstRows; ++v) {
         if (kShapes[v].bm != 16) continue;
         const int nbw = kShapes[v].bn / 16;
         const bool four = kShapes[v].threads == 256;
-        if (nbw == 10 && kind != KIND_INT4) continue;
-        if (four != (kind != KIND_INT4 && nbw > 1)) continue;
         const long wg = (nblk + nbw - 1) / nbw;
+        bool ok;
+        if (kind == KIND_INT4)
+          ok = !four;
+        else if (kind == KIND_FP4)
+          ok = nbw <= 2 && four == (nbw == 2 && wg > kCUs);
+        else
+          ok = nbw != 10 && four == (nbw > 1);
+        if (!ok) continue;
         const long rounds = (wg + kCUs - 1) / kCUs;
         if (wg * 100 >= rounds * kCUs * 75 && (best < 0 || nbw > kShapes[best].bn / 16)) best = v;
       }
@@ -244,8 +253,8 @@ int select_variant(int M, int N, int K, int kind, int epi) {
       if (kShapes[v].bm != rows) continue;
       const int nbw = kShapes[v].bn / 16;
       if (kind == KIND_FP4 && nbw > 4) continue;  // MXFP4's scale words push 7 blocks past the register file
-      if (nbw == 5 || nbw == 10) continue;        // measured only for the codes above
-      if (kShapes[v].threads == 256) continue;    // the 4-wave forms: likewise
+      if (nbw == 5 || nbw == 10) continue;        // these and the 4-wave forms serve the 16-row rule
+      if (kShapes[v].threads == 256) continue;
       // int4 blocks carry half the bytes: 4 blocks per workgroup beat 2 even at 224 workgroups
       // (16x14336x4096: 7.6 us against 8.5)
       const int min_wg = kind == KIND_INT4 ? 200 : 240;

@@ -122,10 +122,17 @@ def test_variant_table():
            (16, 12288, 4096, 0): "nb4_w4_u4", (16, 12288, 4096, 2): "nb4_w8_u3", (16, 28672, 8192, 1): "nb7_w4_u2"}
     for (m, n, k, ind), want in dec.items():
         assert names[lib.flygemm_select_variant(m, n, k, ind, 0)] == f"decode_m1_{want}", (m, n, k, ind)
-    # other kinds keep the rule of about one workgroup per CU (bf16 16x40960x5120: 2560 blocks)
-    assert names[lib.flygemm_select_variant(16, 40960, 5120, 3, 0)] == "decode_m1_nb7_w8_u2"
-    # MXFP4 decode keeps to at most 4 column blocks per workgroup
-    assert names[lib.flygemm_select_variant(16, 28672, 8192, 5, 0)] == "decode_m1_nb4_w8_u3"
+    # the same rule for 16-bit inputs and blockscale; MXFP4 at most two blocks, on 4 waves only
+    # above 256 workgroups
+    more = {(16, 40960, 5120, 3, 0): "nb5_w4_u3", (16, 18432, 7168, 4, 0): "nb5_w4_u3",
+            (16, 36864, 7168, 0, 1): "nb5_w4_u3", (16, 7168, 7168, 0, 1): "nb2_w4_u4",
+            (16, 28672, 8192, 5, 0): "nb2_w4_u4", (16, 8192, 8192, 5, 0): "nb2_w8_u4",
+            (16, 4096, 4096, 5, 0): "nb1_w8_u4"}
+    for (m, n, k, ind, bs), want in more.items():
+        assert names[lib.flygemm_select_variant(m, n, k, ind, bs)] == f"decode_m1_{want}", (m, n, k, ind, bs)
+    # without a choice that fills 75% of the last round: the most blocks leaving 240 workgroups
+    # (blockscale 16x2112x7168: 132 blocks)
+    assert names[lib.flygemm_select_variant(16, 2112, 7168, 0, 1)] == "decode_m1_nb1_w8_u4"
     for m in (1, 17, 64, 65, 100, 1000, 5000):
         for n in (16, 128, 2048, 30000):
             for bs in (0, 1):
