@@ -85,13 +85,17 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
   // ---- per-row facts, fixed for the workgroup's life (as moe.h) ----
   // A gather: DMA instruction q fills run rows 8q .. 8q+7; lane l brings the chunk that belongs
   // in slot l%8 of row 8q + l/8 (XOR chunk swizzle of the large-M kernel).
+  // (int4 keeps the per-row facts in LDS, below; idr: this lane's rows' ids otherwise)
+  constexpr bool kLdsRows = I4;
   uint32_t va[AQ];
-  int ida[AQ], idr[MR];
+  int ida[AQ], idr[kLdsRows ? 1 : MR];
 #pragma unroll
   for (int j = 0; j < AQ; ++j)
     ida[j] = p.sorted_ids[b0 * TM + min(min((wave + j * NW) * 8 + (lane >> 3), TME - 1), rows_valid - 1)];
+  if constexpr (!kLdsRows) {
 #pragma unroll
-  for (int mi = 0; mi < MR; ++mi) idr[mi] = p.sorted_ids[b0 * TM + min(mi * 16 + l16, rows_valid - 1)];
+    for (int mi = 0; mi < MR; ++mi) idr[mi] = p.sorted_ids[b0 * TM + min(mi * 16 + l16, rows_valid - 1)];
+  }
 #pragma unroll
   for (int j = 0; j < AQ; ++j) {
     const int rloc = min((wave + j * NW) * 8 + (lane >> 3), TME - 1);
@@ -102,21 +106,33 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
     const int c = (lane & 7) ^ ((rloc >> 1) & 7);
     va[j] = ok ? (uint32_t)row * (uint32_t)K + (uint32_t)(c * 16) : 0x80000000u;
   }
-  // this lane's rows mi*16 + l16: activation scale, routing weight, destination (-1: padding)
+  // Per-row facts -- activation scale, routing weight, destination (-1: padding) -- and the
+  // column scales, read by the epilogue.  int4 keeps them in LDS (row r's by thread r, read
+  // after the first step's barrier): 158 instead of 192 VGPRs, so three workgroups share a CU,
+  // graph-timed 4-8% faster (DS-TP8 dims, 64-row blocks, 2048 / 8192 / 16384 tokens 89-89.4 /
+  // 235-238.5 / 420-422 us against 92.6-93.0 / 248-253 / 455-457, bit-equal).  The other kinds
+  // keep them in registers: at three workgroups per CU int8 and bf16 were 5-22% slower and fp8
+  // spills.
+  __shared__ float s_sx[kLdsRows ? TME : 1], s_rw[kLdsRows ? TME : 1], s_sc[kLdsRows ? NB * TN : 1];
+  __shared__ int s_dst[kLdsRows ? TME : 1];
   float sx_r[MR], rw_r[MR];
   int dst_r[MR];
-#pragma unroll
-  for (int mi = 0; mi < MR; ++mi) {
-    const int r = mi * 16 + l16;
-    const int id = idr[mi];
+  auto row_facts = [&](int r, int id, float& sxo, float& rwo, int& dsto) __attribute__((always_inline)) {
     const int t = id & 0xFFFFFF, s = (int)((uint32_t)id >> 24);
     const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
-    dst_r[mi] = ok ? t * p.topk + s : -1;
+    dsto = ok ? t * p.topk + s : -1;
     const int arow = ok ? (a_ts ? s * p.tokens + t : t) : 0;
     const float sxv = kScaled ? p.sa[arow] : 1.f;
     const float rwv = p.doweight ? p.sorted_w[b0 * TM + min(r, rows_valid - 1)] : 1.f;
-    sx_r[mi] = ok ? sxv : 0.f;  // 0 keeps padding rows finite; 1 for unscaled kinds
-    rw_r[mi] = ok ? rwv : 0.f;
+    sxo = ok ? sxv : 0.f;  // 0 keeps padding rows finite; 1 for unscaled kinds
+    rwo = ok ? rwv : 0.f;
+  };
+  if constexpr (kLdsRows) {
+    if (tid < TME)
+      row_facts(tid, p.sorted_ids[b0 * TM + min(tid, rows_valid - 1)], s_sx[tid], s_rw[tid], s_dst[tid]);
+  } else {
+#pragma unroll
+    for (int mi = 0; mi < MR; ++mi) row_facts(mi * 16 + l16, idr[mi], sx_r[mi], rw_r[mi], dst_r[mi]);
   }
   const sgpr4 rsrc_a = buf_desc(p.a, (uint32_t)a_rows * (uint32_t)K);
   // this expert's gate/up rows only (the whole array may exceed 32-bit offsets)
@@ -208,11 +224,18 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
   // prologue: weights of steps 0 .. Lb-1, this lane's column scales, A of step 0 (the first
   // step waits for all of them)
   static_for<0, Lb>([&](auto u) __attribute__((always_inline)) { load_b(u, decltype(u)::value); });
+  if constexpr (kLdsRows) {
+    if (tid < NB * TN) {
+      const uint32_t col = (uint32_t)((tid / TN) * p.N + jt * TN + tid % TN);
+      s_sc[tid] = kScaled ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc_s, col * 4u, 0, 0)) : 1.f;
+    }
+  } else {
 #pragma unroll
-  for (int h = 0; h < NB; ++h) {
-    const uint32_t col = (uint32_t)(h * p.N + jt * TN + wave * 16 + lq * 4);
-    sc[h] = kScaled ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_s, col * 4u, 0, 0))
-                    : f32x4{1.f, 1.f, 1.f, 1.f};
+    for (int h = 0; h < NB; ++h) {
+      const uint32_t col = (uint32_t)(h * p.N + jt * TN + wave * 16 + lq * 4);
+      sc[h] = kScaled ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_s, col * 4u, 0, 0))
+                      : f32x4{1.f, 1.f, 1.f, 1.f};
+    }
   }
   issue_a(0);
   // Epilogue: out1[t][s][n] = silu(gate) * up (* routing weight), gate/up = accumulator *
@@ -222,15 +245,21 @@ __global__ void __launch_bounds__(256, 2) moe_stream_kernel(MoeArgs p) {
   auto epilogue = [&]() __attribute__((always_inline)) {
     const bool obf16 = moe_out_bf16(p.out_mode);
     const int c = jt * TN + wave * 16 + lq * 4;
+    if constexpr (kLdsRows) {
+#pragma unroll
+      for (int h = 0; h < NB; ++h) sc[h] = *(const f32x4*)(s_sc + h * TN + wave * 16 + lq * 4);
+    }
 #pragma unroll
     for (int mi = 0; mi < MR; ++mi) {
-      const int d = dst_r[mi];
+      const int r = mi * 16 + l16;
+      const int d = kLdsRows ? s_dst[r] : dst_r[mi];
+      const float sxm = kLdsRows ? s_sx[r] : sx_r[mi], rwm = kLdsRows ? s_rw[r] : rw_r[mi];
       float v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float g = ((float)int4_acc<KIND>(acc[0][mi][q]) * sx_r[mi]) * sc[0][q];
-        const float up = ((float)int4_acc<KIND>(acc[1][mi][q]) * sx_r[mi]) * sc[1][q];
-        v[q] = (silu_f(g) * up) * rw_r[mi];
+        const float g = ((float)int4_acc<KIND>(acc[0][mi][q]) * sxm) * sc[0][q];
+        const float up = ((float)int4_acc<KIND>(acc[1][mi][q]) * sxm) * sc[1][q];
+        v[q] = (silu_f(g) * up) * rwm;
       }
       const uint32_t off = d < 0 ? 0xFFFFFFF0u : ((uint32_t)d * (uint32_t)p.N + (uint32_t)c) * 2u;
       const i32x2 pk = obf16 ? pack_out4<true>(v) : pack_out4<false>(v);
