@@ -18,7 +18,7 @@ using namespace flygemm;
 namespace flygemm {
 MoeKernel moe_stage2_kernel(int kind, int tm, int r, int tn, bool f32, bool bs);
 MoeKernel moe_stage1_stream_kernel(int kind, int tm);
-MoeKernel moe_stage2_stream_kernel(int kind, int tm, int nk);
+MoeKernel moe_stage2_stream_kernel(int kind, int tm, int nk, bool single);
 }
 
 namespace {
@@ -211,25 +211,33 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
   MoeKernel k = stage == 1 ? moe_stage1_kernel(kind, tile_m, R, tile_n, bs)
                            : moe_stage2_kernel(kind, tile_m, R, tile_n, mout == MOE_OUT_F32, bs);
   // Stage 2 per-route rows (the reduce mode's GEMM) of 1-byte and 16-bit weights with inter_dim
-  // of 1, 2 or 4 128-byte K steps: the stream kernel (moe_stream.h), runs of 128 rows, 64-column
-  // tiles, A resident, the next tile's weights loaded before this tile's stores -- for routings
-  // with a full 128-row run per expert on average, and for 16-row blocks wherever the kernel
-  // above takes 256-row runs.  DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256), fp8,
-  // reduce mode (GEMM + reduction), graph-timed, bit-equal: 64-row blocks 2048 / 4096 / 8192
-  // tokens 146 / 246 / 438 us against 164 / 279 / 586, 32-row 163 / 259 against 186 / 382,
-  // 16-row 512 / 1024 / 2048 / 4096 tokens 70 / 115 / 162 / 258 against 199 / 217 / 286 / 372;
-  // below that the kernel above (1024 tokens, 64-row blocks: 89 against 96; 8 tokens: 20 against
-  // 27-47).
-  bool stream2 = false;
+  // of 1, 2 or 4 128-byte K steps: the stream kernel (moe_stream.h), 64-column tiles, A resident,
+  // the next tile's weights loaded before this tile's stores.  With 1 to 32 routes per expert on
+  // average it runs single routing blocks (32 rows for 16-row blocks), each workgroup walking
+  // about 64 KB of weights (four 64-column tiles of fp8 at inter_dim 256, two of bf16); with a
+  // full 128-row run per expert on average (and for 16-row blocks from 32 routes per expert,
+  // wherever the kernel above takes 256-row runs) runs of 128 rows.  Graph-timed, bit-equal,
+  // reduce mode (GEMM + reduction), fp8, inter_dim 256, model_dim 7168: DS-TP8 decode dims (256
+  // experts, 32-row blocks) 32 / 128 / 256 / 512 tokens 49.0 / 98.5 / 106.7 / 117.4 us against
+  // 59.0 / 117.3 / 123.6 / 124.5 (single-block kernel above), 8 tokens level (20 us); bf16 2
+  // tiles per workgroup, 9-16% faster from 32 tokens; DS-TP8 prefill dims (128 experts) 128 / 512
+  // tokens 42.3 / 60.1 against 46.7 / 80.5 (16-row blocks, the latter against 128-row runs),
+  // 43.1 / 59.4 against 51.3 / 61.6 (64-row blocks); at 64 routes per expert (1024 tokens) single
+  // blocks were 3-6% slower for 16- and 64-row blocks, and 128-row runs win from 128 (64-row
+  // blocks 2048 / 4096 / 8192 tokens 146 / 246 / 438 us against 164 / 279 / 586 for the kernel
+  // above).  Fewer routes than experts (8 tokens top-8 of 256): the kernel above.
+  bool stream2 = false, single2 = false;
   const long routes_all = (long)tokens * topk;
-  if (stage == 2 && rows && !bs && kb <= 512 &&
-      (routes_all >= 128L * experts || (tile_m == 16 && routes_all >= 32L * experts))) {
-    const MoeKernel k2 = moe_stage2_stream_kernel(kind, tile_m, (int)(kb / 128));
-    if (k2.fn) {
-      k = k2;
-      R = 128 / tile_m;
-      tile_n = 64;
-      stream2 = true;
+  if (stage == 2 && rows && !bs && kb <= 512 && routes_all >= experts) {
+    single2 = routes_all <= 32L * experts;
+    if (single2 || routes_all >= 128L * experts || (tile_m == 16 && routes_all >= 32L * experts)) {
+      const MoeKernel k2 = moe_stage2_stream_kernel(kind, tile_m, (int)(kb / 128), single2);
+      if (k2.fn) {
+        k = k2;
+        R = single2 ? (tile_m == 16 ? 2 : 1) : 128 / tile_m;
+        tile_n = 64;
+        stream2 = true;
+      }
     }
   }
   if (!k.fn) return fail(hipErrorInvalidValue, "%s: no kernel for tile %dx%d (runs of %d)", what, tile_m, tile_n, R);
@@ -244,6 +252,13 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
   // 470 / 438 / 468 / 444 us), more when the runs are few (about 1024 workgroups; 1024 tokens,
   // 32-row blocks: 16 ranges 111 us against 117 for 4)
   if (stream2) nsplit = std::min(ntn, std::max(4L, (1024 + runs - 1) / runs));
+  // single blocks: about 64 KB of weights per workgroup (DS-TP8 decode dims, 32 tokens: fp8 28
+  // ranges of four tiles 49.0 us, 4 ranges 52.6, 56 ranges 52.6; bf16 56 ranges of two 105.8
+  // against 107.9 for 28)
+  if (stream2 && single2) {
+    const long per = std::max(1L, 65536L / ((long)tile_n * kb));
+    nsplit = (ntn + per - 1) / per;
+  }
   MoeArgs args{out,      (const uint8_t*)a, (const uint8_t*)w, sa,  sw,      sorted_ids, expert_ids,
                sorted_w, num_valid,         tokens,            topk, N,      (int)kb,    experts,
                doweight ? 1 : 0, blocks, (int)nsplit, mout, (uint32_t)out_bytes, token_slot ? 1 : 0,

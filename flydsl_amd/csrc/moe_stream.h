@@ -297,15 +297,16 @@ namespace flygemm {
 // kernels/moe_gemm_2stage.py compile_moe_gemm2 :1267-2481 with accumulate = False, summed by
 // moe_reduce_kernel) for 1-byte and 16-bit weights and inter_dim of NK <= 4 128-byte K steps.
 //
-// One workgroup (4 waves) owns a run of up to R routing blocks of one expert (128 rows) and a
-// range of 64-column output tiles (nsplit ranges per run).  The run's gathered A rows -- all NK
+// One workgroup (4 waves) owns a run of up to R routing blocks of one expert (TM * R = 128 rows;
+// 32 or 64 for the single-block form of routings with few routes per expert) and a range of
+// 64-column output tiles (nsplit ranges per run).  The run's gathered A rows -- all NK
 // K steps -- go to LDS once and stay there.  Wave w owns output columns [16w, 16w + 16) of each
 // tile and loads their weight fragments (NK steps x two coalesced 1 KB loads) and column scales
 // straight into registers, one column tile ahead: the loads of tile j+1 are issued before tile
 // j's stores, so the compiler's wait for them (vector memory operations retire in issue order)
 // never covers a store, and each tile's 16 KB of row stores drain while the next tile computes.
-// The epilogue stages the tile through LDS in two rounds of 64 rows (16-byte chunk c of row r at
-// chunk c ^ (r % 8)) and stores whole 128-byte row segments.  40 KB of LDS and at most 128 VGPRs
+// The epilogue stages the tile through LDS in two rounds of 64 rows (one round for runs of 32
+// rows; 16-byte chunk c of row r at chunk c ^ (r % 8)) and stores whole 128-byte row segments.  40 KB of LDS and at most 128 VGPRs
 // let four workgroups share a CU.  DS-TP8 prefill (65536 routes, 7168 x 256, fp8), the GEMM and
 // the reduction: 438 us against 586 for the single-block kernel with A resident (bit-equal);
 // variants measured and not kept: three workgroups per CU with one staging round 453 us, the A
@@ -314,7 +315,7 @@ namespace flygemm {
 template <int KIND, int TM, int R, int NK>
 __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
   static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "1-byte or 16-bit weights");
-  constexpr int NW = 4, TN = 64, HALVES = 2;
+  constexpr int NW = 4, TN = 64, HALVES = TM * R >= 64 ? 2 : 1;   // staging rounds
   constexpr int TME = TM * R, MR = TME / 16;
   constexpr int A_STEP = TME * KT, AQ = A_STEP / 1024 / NW;
   constexpr int RB = TN * 2;                  // bytes of one output row of the tile

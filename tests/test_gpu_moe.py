@@ -418,6 +418,27 @@ def test_stage2_stream_rows_depths(gpu, kind, tile_m):
                    what=f"stream2 {kind} tm{tile_m} nk{nk} w{int(doweight)} {out_dtype}")
 
 
+@pytest.mark.parametrize("kind", ["fp8", "int8", "bf16", "fp16"])
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
+def test_stage2_stream_single_blocks(gpu, kind, tile_m):
+    """Routings with 1 to 32 routes per expert: reduce mode's GEMM runs the stage-2 stream kernel
+    on single routing blocks (two of 16 rows), each workgroup walking about 64 KB of weights
+    (model_dim 704 = 11 column tiles in 2, 3 or 6 ranges of 8, 4 or 2 tiles for 1, 2 or 4 K
+    steps, the last range shorter); 3 K steps keep the single-block kernel.  40 tokens top-4 of 16 experts (10 routes per expert) and 9
+    tokens top-2 of 16 (18 routes, one or two per expert), routing weights on and off."""
+    for tokens, topk in ((40, 4), (9, 2)):
+        for nk in (1, 2, 3, 4):
+            inter = nk * 128 // (2 if kind in ("bf16", "fp16") else 1)
+            w = W.moe_custom(tokens, 704, inter, 16, topk, tile_m, 64, 64, kind, seed=nk * 7 + tile_m + tokens)
+            p = W.moe_problem(w, gpu)
+            for doweight, out_dtype in ((True, "bf16"), (False, "f16")):
+                _say(f"stream stage2 single blocks {kind} tile_m={tile_m} tokens={tokens} K steps={nk} "
+                     f"doweight={doweight} out={out_dtype}")
+                out = _reduce(p, gpu, out_dtype, doweight)
+                _check(out, ref_stage2(p, doweight, route_round=out_dtype),
+                       what=f"stream2 single {kind} tm{tile_m} t{tokens} nk{nk} w{int(doweight)} {out_dtype}")
+
+
 @pytest.mark.parametrize("tile_m", [16, 32, 64])
 def test_stage2_stream_rows_tile_walks(gpu, tile_m):
     """A routing with many runs (4096 tokens top-8 of 16 experts): four column ranges per run over
