@@ -248,6 +248,16 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
   long nsplit = (1024 + runs - 1) / runs;
   nsplit = nsplit < 1 ? 1 : (nsplit > ntn ? ntn : nsplit);
   if (moe_stream_stage1(stage, kind, bs)) nsplit = ntn;
+  // stage 2 with atomics: at least half as many column ranges as tiles (two tiles of 128 columns
+  // or 256 per workgroup, at most; about 1024 workgroups leave few runs long walks whose atomic
+  // epilogues queue behind each other).  Graph-timed, fp8 (blockscale for DS-V3-M128), the
+  // former about-1024 rule against this: DS-TP8 prefill 64-row blocks 2048 / 4096 / 8192 tokens
+  // 269 / 437 / 861 us against 208 / 387 / 749, 32-row 2048 tokens 260 against 210, 16-row
+  // (256-row runs) 8192 tokens 899 against 859; DS-TP8 decode dims 32 / 128 tokens 64.7 / 112.6
+  // against 51.5 / 97.2; DS-V3-M128 blockscale 95.6 against 84.1.  Fewer routes than experts
+  // (decode, 8 tokens top-8 of 256: 19.0 against 19.5) and the per-route rows keep the rule
+  // above (level or faster there).
+  if (stage == 2 && !rows && routes_all >= experts && ntn / 2 > nsplit) nsplit = ntn / 2;
   // the stage-2 stream kernel: 4 column ranges per run (DS-TP8 prefill, 2 / 3 / 4 / 6 / 8: 574 /
   // 470 / 438 / 468 / 444 us), more when the runs are few (about 1024 workgroups; 1024 tokens,
   // 32-row blocks: 16 ranges 111 us against 117 for 4)
