@@ -28,8 +28,8 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
 #define T(M_, R_, N_, WM_, WN_)        \
   if (tm == M_ && r == R_ && tn == N_) \
     return MoeKernel{moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS>, WM_ * WN_ * 64};
-  T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(16, 1, 256, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4)
-  T(32, 1, 256, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4) T(64, 1, 256, 1, 4)
+  // (64 or 128 columns: the launcher never takes 256 for these single-block stage-1 tiles)
+  T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4)
 #undef T
   return MoeKernel{nullptr, 0};
 }
@@ -114,6 +114,14 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
     // 0-11% faster than 256 for fp8 and blockscale, never slower), so stage 2 never runs
     // single-block tiles of 256 columns
     else if (stage == 2 && tile_n == 256 && N % 128 == 0) tile_n = 128;
+    // stage 1 (W4A16, blockscale): 128 columns where that gives about three workgroups per CU,
+    // else 64, never 256.  Graph-timed against the caller's 256: W4A16 DS-TP8 prefill dims,
+    // 64-row blocks at 2048 tokens 220 us (128) against 387, 32-row blocks at 512 tokens 91.8
+    // (64) against 117.5 (128) and 161 (256); DS-V3 decode dims at 64 tokens 127.5 (64) / 124.4
+    // (128) against 162; blockscale DS-V3-M128 dims at 1024 tokens 244.5 (128) against 268 (64)
+    // and 324, at 128 tokens 157.9 (64) against 160.4 (128) and 162.
+    else if (stage == 1 && N % 128 == 0)
+      tile_n = runs1 * (N / 128) >= 768 ? 128 : 64;
   }
   if (tile_n != 64 && tile_n != 128 && tile_n != 256)
     return fail(hipErrorInvalidValue, "%s: tile_n=%d must be 64, 128 or 256", what, tile_n);

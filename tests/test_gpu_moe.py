@@ -759,14 +759,14 @@ WIDE_KINDS = [("fp8", -1), ("int8", -1), ("bf16", -1), ("fp16", -1), ("int4", -1
 
 @pytest.mark.parametrize("kind,group", WIDE_KINDS, ids=[k if g < 0 else f"{k}-g{g}" for k, g in WIDE_KINDS])
 def test_single_block_wide_tiles(gpu, kind, group):
-    """Routings with fewer than two blocks per expert but enough routes that the launcher keeps
-    wide single-block tiles: 160 tokens, top-4 of 64 experts, D = 512, I = 1024, tile_m 32,
-    tile_n 256 -> stage 1 of W4A16 runs the 256-column single-block kernel (the other kinds
+    """Routings with about one block per expert and enough routes that the launcher takes the
+    wide single-block tiles: 512 tokens, top-4 of 64 experts, D = 512, I = 1024, tile_m 32,
+    tile_n 256 -> stage 1 of W4A16 runs the 128-column single-block kernel (the other kinds
     the stream kernel), stage 2 the 128-column one (checked through flygemm_moe_select_tile
     first).  Stage 2 in atomic and reduce modes."""
-    w = W.moe_custom(160, 512, 1024, 64, 4, 32, 256, 256, kind, seed=11)
+    w = W.moe_custom(512, 512, 1024, 64, 4, 32, 256, 256, kind, seed=11)
     # (stage 1 of the other kinds: the stream kernel's 128-row runs of 64 columns)
-    assert _chosen_tile(1, w, kind) == ((1, 256) if kind == "int4_bf16" else (4, 64))
+    assert _chosen_tile(1, w, kind) == ((1, 128) if kind == "int4_bf16" else (4, 64))
     assert _chosen_tile(2, w, kind) == (1, 128)
     p = W.moe_problem(w, gpu, group_size=group)
     p["group_size"] = group
@@ -774,7 +774,7 @@ def test_single_block_wide_tiles(gpu, kind, group):
     o1 = run_stage1(p, gpu, "bf16", doweight=True)
     o2 = run_stage2(p, gpu, "f32", doweight=False)
     torch.cuda.synchronize()
-    check_stage1(p, o1, True, what=f"stage1 {kind} 1x256")
+    check_stage1(p, o1, True, what=f"stage1 {kind} 1x128")
     check_stage2(p, o2, False, what=f"stage2 {kind} 1x128 atomic")
     from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
     fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
@@ -790,14 +790,14 @@ def test_single_block_wide_tiles(gpu, kind, group):
 
 
 def test_single_block_wide_tiles_blockscale(gpu):
-    """The same routing through the blockscale MoE: stage 1 single-block 256-column tiles,
+    """The same routing through the blockscale MoE: stage 1 single-block 128-column tiles,
     stage 2 128-column ones."""
-    w = W.moe_custom(160, 512, 1024, 64, 4, 32, 256, 256, "fp8_block", seed=12)
-    assert _chosen_tile(1, w, "fp8", 1) == (1, 256) and _chosen_tile(2, w, "fp8", 1) == (1, 128)
+    w = W.moe_custom(512, 512, 1024, 64, 4, 32, 256, 256, "fp8_block", seed=12)
+    assert _chosen_tile(1, w, "fp8", 1) == (1, 128) and _chosen_tile(2, w, "fp8", 1) == (1, 128)
     p = W.moe_problem(w, gpu)
     _say("wide single-block tiles blockscale")
     o1 = run_bs_stage1(p, gpu, "f16", doweight=False)
     o2 = run_bs_stage2(p, gpu, "f32", doweight=True)
     torch.cuda.synchronize()
-    _check(o1, ref_bs1(p, False), what="blockscale stage1 1x256")
+    _check(o1, ref_bs1(p, False), what="blockscale stage1 1x128")
     _check(o2, ref_bs2(p, True), what="blockscale stage2 1x128")

@@ -441,11 +441,14 @@ def test_moe_tile_choice_pinned():
     # decode: 64-column single-block tiles whatever the caller asked
     assert sel(1, 8, 256, 256, 8, 32, 256, "int4_bf16") == (1, 64)
     assert sel(2, 8, 7168, 256, 8, 32, 256) == (1, 64)
-    # in between: the wide single-block tiles; stage 2 never keeps 256 single-block columns
-    assert sel(1, 160, 1024, 64, 4, 32, 256, "int4_bf16") == (1, 256)
+    # in between: stage 1 of W4A16 and blockscale 128 columns from about three workgroups per CU
+    # (runs x inter_dim / 128 >= 768), else 64; stage 2 never keeps 256 single-block columns
+    assert sel(1, 160, 1024, 64, 4, 32, 256, "int4_bf16") == (1, 64)      # 84 runs x 8 = 672
+    assert sel(1, 512, 1024, 64, 4, 32, 256, "int4_bf16") == (1, 128)     # 128 runs x 8
+    assert sel(1, 512, 1024, 64, 4, 32, 128, "fp8", 1) == (1, 128)
+    assert sel(1, 160, 1024, 64, 4, 32, 256, "fp8", 1) == (1, 64)
     for kind in ("fp8", "int8", "bf16", "fp16", "int4", "int8smooth", "int4_bf16"):
         assert sel(2, 160, 512, 64, 4, 32, 256, kind) == (1, 128), kind
-    assert sel(1, 160, 1024, 64, 4, 32, 256, "fp8", 1) == (1, 256)
     assert sel(2, 128, 7168, 256, 8, 32, 0) == (1, 128)
     # blockscale and W4A16 never take run tiles
     assert sel(2, 8192, 7168, 128, 8, 16, 256, "fp8", 1)[0] == 1
