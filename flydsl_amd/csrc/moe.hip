@@ -70,9 +70,10 @@ int pick_tile_n(int N, long runs) {
 }
 
 // Tile of a call: runs of R routing blocks per workgroup and tile_n output columns (the
-// caller's tile_n, already validated, is a hint).
+// caller's tile_n, already validated, is a hint).  atomics: a stage-2 call that accumulates
+// (per-route-row calls take the stream kernel's tiles where it applies).
 int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
-              const char* what, int* r_out, int* tn_out) {
+              bool atomics, const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
   // Stage 1 of 1-byte, 16-bit and W4A8 weights: the stream kernel, 128-row runs of 64 columns
   // (every N here is a multiple of 64: tile_n, checked by the callers, divides it).  The
@@ -114,6 +115,13 @@ int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, i
     // 0-11% faster than 256 for fp8 and blockscale, never slower), so stage 2 never runs
     // single-block tiles of 256 columns
     else if (stage == 2 && tile_n == 256 && N % 128 == 0) tile_n = 128;
+    // stage 2 with atomics on prefill routings (16+ routes per expert) of 32- and 64-row blocks:
+    // 64 columns (DS-TP8 dims, 64-row blocks: fp8 2048 / 8192 tokens 194.6 / 727.6 us against
+    // 206.3 / 749.4 for 128, W4A16 8192 tokens 806.9 against 861.9; 32-row int4 2048 tokens
+    // level); per-route rows and fewer routes keep 128 (fp8 rows at 1024 tokens: 88.2 against
+    // 114.9; DS-TP8 decode dims 128 tokens, W4A16 atomics: 80.5 against 87.5)
+    if (stage == 2 && atomics && tile_m >= 32 && routes >= 16L * experts && tile_n == 128 && N % 64 == 0)
+      tile_n = 64;
     // stage 1 (W4A16, blockscale): 128 columns where that gives about three workgroups per CU,
     // else 64, never 256.  Graph-timed against the caller's 256: W4A16 DS-TP8 prefill dims,
     // 64-row blocks at 2048 tokens 220 us (128) against 387, 32-row blocks at 512 tokens 91.8
@@ -185,7 +193,9 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
     return fail(hipErrorInvalidValue, "%s: group_size=%d: group scales are for int4_bf16 with group_size 32", what,
                 group_size);
   int R = 1;
-  if (int rc = moe_tiles(stage, tokens, N, experts, topk, tile_m, tile_n, kind, bs, what, &R, &tile_n)) return rc;
+  if (int rc = moe_tiles(stage, tokens, N, experts, topk, tile_m, tile_n, kind, bs, stage == 2 && accumulate != 0, what,
+                         &R, &tile_n))
+    return rc;
   const bool is16 = moe_a_16bit(kind);      // 2-byte activations (bf16, fp16, W4A16)
   const long kb = is16 ? 2L * K : (long)K;  // activation bytes per row
   if (kb % 128 != 0)
@@ -457,7 +467,7 @@ int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t ex
   const int kind = moe_kind(in_dtype, stage, &token_slot);
   if (kind < 0) return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
   int r = 1, tn = 0;
-  if (int rc = moe_tiles(stage, tokens, n, experts, topk, tile_m, tile_n, kind, blockscale != 0, what, &r, &tn))
+  if (int rc = moe_tiles(stage, tokens, n, experts, topk, tile_m, tile_n, kind, blockscale != 0, stage == 2, what, &r, &tn))
     return rc;
   *runs = r;
   *tile_n_out = tn;

@@ -432,10 +432,13 @@ def test_moe_tile_choice_pinned():
         for tokens, n, experts, topk in ((8192, 256, 128, 8), (8, 256, 256, 8), (160, 1024, 64, 4), (64, 256, 4, 2)):
             for tm in (16, 32, 64):
                 assert sel(1, tokens, n, experts, topk, tm, 256, kind) == (128 // tm, 64), (kind, tokens, tm)
-    # stage 2 on DS-TP8 prefill: 128-column single-block tiles for 32- and 64-row blocks, runs of
-    # 256 rows and 256 columns for 16-row blocks
-    assert sel(2, 8192, 7168, 128, 8, 64, 256) == (1, 128)
-    assert sel(2, 8192, 7168, 128, 8, 32, 256) == (1, 128)
+    # stage 2 (accumulating calls) on DS-TP8 prefill: 64-column single-block tiles for 32- and
+    # 64-row blocks (16+ routes per expert), runs of 256 rows and 256 columns for 16-row blocks
+    assert sel(2, 8192, 7168, 128, 8, 64, 256) == (1, 64)
+    assert sel(2, 8192, 7168, 128, 8, 32, 256) == (1, 64)
+    assert sel(2, 8192, 7168, 128, 8, 64, 128) == (1, 64)
+    assert sel(2, 1024, 7168, 128, 8, 64, 256) == (1, 64)     # 64 routes per expert
+    assert sel(2, 160, 7168, 128, 8, 64, 256) == (1, 128)     # 10 routes per expert
     assert sel(2, 8192, 7168, 128, 8, 16, 256) == (16, 256)
     assert sel(2, 8192, 7168, 128, 8, 16, 256, "int4") == (16, 256)
     # decode: 64-column single-block tiles whatever the caller asked
