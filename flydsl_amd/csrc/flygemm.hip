@@ -82,7 +82,9 @@ struct Shape {
   X(1, 2, 4, 4)          \
   X(1, 4, 4, 4)          \
   X(1, 5, 4, 3)          \
-  X(1, 7, 4, 2)
+  X(1, 7, 4, 2)          \
+  X(2, 2, 4, 4)          \
+  X(2, 4, 4, 2)
 
 // The streaming kernel over row blocks (plain B loads: the row blocks of a column group re-read
 // B from L2): for M too large for one row block but too small for the tiled kernel to give
@@ -198,15 +200,19 @@ int select_rows(int kind, int epi) {
 }
 
 int select_variant(int M, int N, int K, int kind, int epi) {
-  // The decode family wins up to 16 rows; above that its per-row A traffic grows and the
-  // 64x128 tile is faster above 32 rows -- and above 16 rows when N has at least 200 column
-  // tiles of 128, or at least 32 with the blockscale epilogue.  Measured on MI355X for every
-  // kind: fp8/int8/int4 (N x K = 28672x8192, 4096x4096, 7168x2048, 14336x4096, 8192x8192),
-  // bf16 and MXFP4 (28672x8192, 8192x8192), blockscale (7168x7168, 2112x7168); e.g.
-  // 64x28672x8192 fp8 43.8 us against 77.4, bf16 86 against 144, blockscale 64x7168x7168 18.1
-  // against 33.2.
+  // The decode family up to 32 rows; above that its per-row A traffic grows and the 64x128 tile
+  // is faster (and above 16 rows with the blockscale epilogue when N has at least 32 column tiles
+  // of 128).  Measured on MI355X for every kind: fp8/int8/int4 (N x K = 28672x8192, 4096x4096,
+  // 7168x2048, 14336x4096, 8192x8192), bf16 and MXFP4 (28672x8192, 8192x8192), blockscale
+  // (7168x7168, 2112x7168); e.g. 64x28672x8192 fp8 43.8 us against 77.4, bf16 86 against 144,
+  // blockscale 64x7168x7168 18.1 against 33.2.  With the 4-wave 32-row forms the decode family
+  // also takes 17-32 rows of wide N (graph-timed against the best of the 64x128 / 64x64 tiles:
+  // fp8 20x40960x5120 36.5 us against 63.1 for the 256x256 tile the main family gave it,
+  // 28x77824x5120 64.8 against 76.4, 32x28672x8192 42.6 against 41.1, 32x25600x4096 22.1 against
+  // 21.3; bf16 and int8 alike (bf16 32x25600x4096 41.0 against 38.3); int4 32x28672x8192 28.0
+  // against 44.1, 28x77824x5120 43.7 against 40.6).
   const int ncol = (N + 127) / 128;
-  const bool tile_small_m = M > 32 || (M > 16 && (ncol >= 200 || (epi == EPI_BLOCK && ncol >= 32)));
+  const bool tile_small_m = M > 32 || (M > 16 && epi == EPI_BLOCK && ncol >= 32);
   if (M <= 64 && !tile_small_m) {
     // decode family: fewest rows that cover M, then the column blocks per workgroup
     const int rows = M <= 16 ? 16 : (M <= 32 ? 32 : 64);
@@ -226,16 +232,19 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // 40960x5120 63.0 against 74.0 (the former rule for other kinds), 18432x7168 41.3 against
     // 58.1; MXFP4 24576x8192 18.9 against 23.4; blockscale 36864x7168 41.9 against 61.1,
     // 18432x7168 22.3 against 31.1; int4 40960x5120 19.3 with 10 blocks, its 4-wave forms level
-    // or up to 11% slower.  Without a choice that fills 75% (few columns), the rule below.
-    if (rows == 16) {
+    // or up to 11% slower.  32-row blocks follow the same rule with 1, 2 or 4 blocks (int4 too,
+    // in 4 waves: 32x28672x8192 28.0 us on 4 blocks against 39.1 on 2 in 8 waves; fp8
+    // 32x14336x4096 12.6 against 16.4, 32x12288x4096 11.7 against 15.9, 32x7168x2048 5.8 against
+    // 7.9).  Without a choice that fills 75% (few columns), the rule below.
+    if (rows <= 32) {
       int best = -1;
       for (int v = kFirstDecode; v < kFirstRows; ++v) {
-        if (kShapes[v].bm != 16) continue;
+        if (kShapes[v].bm != rows) continue;
         const int nbw = kShapes[v].bn / 16;
         const bool four = kShapes[v].threads == 256;
         const long wg = (nblk + nbw - 1) / nbw;
         bool ok;
-        if (kind == KIND_INT4)
+        if (kind == KIND_INT4 && rows == 16)
           ok = !four;
         else if (kind == KIND_FP4)
           ok = nbw <= 2 && four == (nbw == 2 && wg > kCUs);

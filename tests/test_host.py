@@ -43,10 +43,15 @@ def test_variant_table():
               (256, 14336, 4096, 2, 0): "main_64x128_w1x4", (8192, 8192, 8192, 0, 0): "main_256x256_w2x4"}
     for args, want in expect.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
-    # 17-64 rows: decode only up to 32 rows (16 for very wide N, or blockscale with 32+ column
-    # tiles); the 64x128 tile above, or the row-blocked kernel when that gives few tiles
+    # 17-64 rows: decode only up to 32 rows (16 for blockscale with 32+ column tiles); the
+    # 64x128 tile above, or the row-blocked kernel when that gives few tiles
     assert names[lib.flygemm_select_variant(64, 28672, 8192, 0, 0)] == "main_64x128_w1x4"
-    assert names[lib.flygemm_select_variant(32, 28672, 8192, 0, 0)] == "main_64x128_w1x4"
+    # 17-32 rows: the decode family's 4-wave 32-row forms, whatever N (not blockscale)
+    assert names[lib.flygemm_select_variant(32, 28672, 8192, 0, 0)] == "decode_m2_nb4_w4_u2"
+    assert names[lib.flygemm_select_variant(20, 40960, 5120, 0, 0)] == "decode_m2_nb4_w4_u2"
+    assert names[lib.flygemm_select_variant(32, 28672, 8192, 2, 0)] == "decode_m2_nb4_w4_u2"
+    assert names[lib.flygemm_select_variant(32, 18432, 7168, 3, 0)] == "decode_m2_nb2_w4_u4"
+    assert names[lib.flygemm_select_variant(32, 4096, 4096, 1, 0)] == "decode_m2_nb1_w8_u4"
     assert names[lib.flygemm_select_variant(32, 8192, 8192, 1, 0)].startswith("decode_m2")
     assert names[lib.flygemm_select_variant(48, 8192, 8192, 1, 0)] == "rows_m2_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(64, 7168, 2048, 2, 0)] == "rows_m2_nb4_w8_u3"  # 56 tiles
