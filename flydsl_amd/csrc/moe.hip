@@ -248,7 +248,11 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
   const long routes_all = (long)tokens * topk;
   if (stage == 2 && rows && !bs && kb <= 512 && routes_all >= experts) {
     single2 = routes_all <= 32L * experts;
-    if (single2 || routes_all >= 128L * experts || (tile_m == 16 && routes_all >= 32L * experts)) {
+    // (int4 weights, half the bytes per tile: 128-row runs from 256 routes per expert for 32- and
+    // 64-row blocks -- DS-TP8 prefill 4096 / 8192 tokens 232 / 443 us against 266 / 566 for the
+    // kernel above, at 2048 149 against 128)
+    const long runs_from = kind == KIND_INT4 ? 256L : 128L;
+    if (single2 || routes_all >= runs_from * experts || (tile_m == 16 && routes_all >= 32L * experts)) {
       const MoeKernel k2 = moe_stage2_stream_kernel(kind, tile_m, (int)(kb / 128), single2);
       if (k2.fn) {
         k = k2;

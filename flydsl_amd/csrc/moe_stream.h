@@ -295,7 +295,8 @@ namespace flygemm {
 
 // MoE stage 2 with per-route row outputs (the reduce mode's GEMM; reference
 // kernels/moe_gemm_2stage.py compile_moe_gemm2 :1267-2481 with accumulate = False, summed by
-// moe_reduce_kernel) for 1-byte and 16-bit weights and inter_dim of NK <= 4 128-byte K steps.
+// moe_reduce_kernel) for 1-byte, int4 (with int8 activations) and 16-bit weights and inter_dim of
+// NK <= 4 128-byte K steps.
 //
 // One workgroup (4 waves) owns a run of up to R routing blocks of one expert (TM * R = 128 rows;
 // 32 or 64 for the single-block form of routings with few routes per expert) and a range of
@@ -314,7 +315,9 @@ namespace flygemm {
 // column ranges per run 574 / 470 / 468 / 444.
 template <int KIND, int TM, int R, int NK>
 __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
-  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || kind_is_16bit(KIND), "1-byte or 16-bit weights");
+  static_assert(KIND == KIND_FP8 || KIND == KIND_INT8 || KIND == KIND_INT4 || kind_is_16bit(KIND),
+                "1-byte, int4 or 16-bit weights");
+  constexpr bool I4 = KIND == KIND_INT4;
   constexpr int NW = 4, TN = 64, HALVES = TM * R >= 64 ? 2 : 1;   // staging rounds
   constexpr int TME = TM * R, MR = TME / 16;
   constexpr int A_STEP = TME * KT, AQ = A_STEP / 1024 / NW;
@@ -391,13 +394,15 @@ __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
       const bool ok = r < rows_valid && t < p.tokens && s < p.topk;
       dst_c[h][i] = ok ? t * p.topk + s : -1;
     }
-  const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc(p.w + (size_t)e * (size_t)p.N * (size_t)K, p.N * K);
+  const uint32_t wrb = I4 ? (uint32_t)K / 2u : (uint32_t)K;   // weight bytes per row (int4: packed)
+  const __amdgpu_buffer_rsrc_t rsrc_w = make_rsrc(p.w + (size_t)e * (size_t)p.N * wrb, (int)((uint32_t)p.N * wrb));
   const __amdgpu_buffer_rsrc_t rsrc_s = make_rsrc(p.sw + (size_t)e * p.N, kScaled ? p.N * 4 : 0);
   const __amdgpu_buffer_rsrc_t rsrc_o = make_rsrc(p.out, (int)p.out_bytes);
   const bool obf16 = moe_out_bf16(p.out_mode);
 
   typedef typename std::conditional<kind_float_acc(KIND), f32x4, i32x4>::type AccT;
-  i32x4 bw[2][NK][2];   // weight fragments of two column tiles: [set][K step][K half]
+  typedef typename std::conditional<I4, i32x2, i32x4>::type BT;
+  BT bw[2][NK][2];      // weight fragments of two column tiles: [set][K step][K half]
   f32x4 sc[2];          // this lane's 4 column scales of each
   // column scales and weights of column tile j into set U; every tile issues the same loads (a
   // tile past the range reads zeros from past the buffers), so the compiler's counts hold
@@ -409,13 +414,21 @@ __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
     const uint32_t col = (uint32_t)(jj * TN + wave * 16 + lq * 4);
     sc[U] = kScaled ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_s, col * 4u + past, 0, 0))
                     : f32x4{1.f, 1.f, 1.f, 1.f};
-    const uint32_t so0 = (uint32_t)(jj * (TN / 16) + wave) * 16u * (uint32_t)K;
-    const uint32_t vo = (uint32_t)lane * 16u + past;
+    // 16-row weight block per K step: 2048 bytes (int4: 1024 packed, lane (l16, lq) holding 8
+    // bytes at 128*lq + 8*l16 and 512 past that, as the stage-1 stream kernel reads them)
+    const uint32_t so0 = (uint32_t)(jj * (TN / 16) + wave) * 16u * wrb;
+    const uint32_t vo = (I4 ? (uint32_t)(lq * 128 + l16 * 8) : (uint32_t)lane * 16u) + past;
 #pragma unroll
     for (int kt = 0; kt < NK; ++kt) {
-      const uint32_t so = so0 + (uint32_t)kt * 2048u;
-      bw[U][kt][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
-      bw[U][kt][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 1024u), 0);
+      if constexpr (I4) {
+        const uint32_t so = so0 + (uint32_t)kt * 1024u;
+        bw[U][kt][0] = __builtin_amdgcn_raw_buffer_load_b64(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
+        bw[U][kt][1] = __builtin_amdgcn_raw_buffer_load_b64(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 512u), 0);
+      } else {
+        const uint32_t so = so0 + (uint32_t)kt * 2048u;
+        bw[U][kt][0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so), 0);
+        bw[U][kt][1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_w, vo, __builtin_amdgcn_readfirstlane(so + 1024u), 0);
+      }
     }
   };
   auto tile = [&](auto u_tag, int j) __attribute__((always_inline)) {
@@ -427,7 +440,14 @@ __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
 #pragma unroll
     for (int kt = 0; kt < NK; ++kt) {
       const uint8_t* sA = sa_lds + kt * A_STEP;
-      const i32x4 bl = bw[U][kt][0], bh = bw[U][kt][1];
+      i32x4 bl, bh;
+      if constexpr (I4) {
+        bl = unpack_int4x16(bw[U][kt][0]);
+        bh = unpack_int4x16(bw[U][kt][1]);
+      } else {
+        bl = bw[U][kt][0];
+        bh = bw[U][kt][1];
+      }
 #pragma unroll
       for (int mi = 0; mi < MR; ++mi) {
         const int row = mi * 16 + l16;
@@ -438,8 +458,9 @@ __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
           acc[mi] = mfma_fp8(__builtin_shufflevector(bl, bh, 0, 1, 2, 3, 4, 5, 6, 7),
                              __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), acc[mi]);
         } else {
-          acc[mi] = mfma_k64<KIND>(bl, lo, acc[mi]);
-          acc[mi] = mfma_k64<KIND>(bh, hi, acc[mi]);
+          constexpr int MK = I4 ? KIND_INT8 : KIND;   // int4 weights: the int8 MFMA
+          acc[mi] = mfma_k64<MK>(bl, lo, acc[mi]);
+          acc[mi] = mfma_k64<MK>(bh, hi, acc[mi]);
         }
       }
     }
@@ -455,7 +476,7 @@ __global__ void __launch_bounds__(256, 4) moe_stream2_kernel(MoeArgs p) {
         const int c = wave * 16 + lq * 4;
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = ((float)acc[mi][q] * sc[U][q]) * fr_r[mi];
+        for (int q = 0; q < 4; ++q) v[q] = ((float)int4_acc<KIND>(acc[mi])[q] * sc[U][q]) * fr_r[mi];
         const i32x2 pk = obf16 ? pack_out4<true>(v) : pack_out4<false>(v);
         *(i32x2*)(stg + r * RB + (((c >> 3) ^ (r % CPR)) << 4) + (c & 7) * 2) = pk;
       }

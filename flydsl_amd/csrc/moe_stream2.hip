@@ -42,6 +42,7 @@ MoeKernel moe_stage2_stream_kernel(int kind, int tm, int nk, bool single) {
   switch (kind) {
     case KIND_FP8: return stream2_kind<KIND_FP8>(tm, nk, single);
     case KIND_INT8: return stream2_kind<KIND_INT8>(tm, nk, single);
+    case KIND_INT4: return stream2_kind<KIND_INT4>(tm, nk, single);
     case KIND_BF16: return stream2_kind<KIND_BF16>(tm, nk, single);
     case KIND_F16: return stream2_kind<KIND_F16>(tm, nk, single);
     default: return MoeKernel{nullptr, 0};

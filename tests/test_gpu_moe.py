@@ -401,10 +401,11 @@ def _reduce(p, gpu, out_dtype, doweight=True, rows=None):
     return out
 
 
-@pytest.mark.parametrize("kind", ["fp8", "int8", "bf16", "fp16"])
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "bf16", "fp16"])
 @pytest.mark.parametrize("tile_m", [16, 32, 64])
 def test_stage2_stream_rows_depths(gpu, kind, tile_m):
-    """Reduce mode's GEMM for these kinds runs the stage-2 stream kernel when inter_dim is 1, 2 or
+    """Reduce mode's GEMM for these kinds (int4: packed weights unpacked in registers) runs the
+    stage-2 stream kernel when inter_dim is 1, 2 or
     4 128-byte K steps (A resident for the run, the weights of the next 64-column tile loaded
     before this tile's row stores, rows staged in two rounds); 3 steps keep the single-block
     kernel.  300 tokens top-3 of 5 experts (runs cut at expert boundaries, partial runs), model_dim
@@ -421,7 +422,7 @@ def test_stage2_stream_rows_depths(gpu, kind, tile_m):
                    what=f"stream2 {kind} tm{tile_m} nk{nk} w{int(doweight)} {out_dtype}")
 
 
-@pytest.mark.parametrize("kind", ["fp8", "int8", "bf16", "fp16"])
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int4", "bf16", "fp16"])
 @pytest.mark.parametrize("tile_m", [16, 32, 64])
 def test_stage2_stream_single_blocks(gpu, kind, tile_m):
     """Routings with 1 to 32 routes per expert: reduce mode's GEMM runs the stage-2 stream kernel
