@@ -192,8 +192,17 @@ const KernelFn* kernel_row(int kind, int epi, int out_dtype) {
 // 14.2 against 26.8.  Blockscale and MXFP4 keep MR = 1: their per-tile scales make the 32-row
 // block spill registers (blockscale 256x2112x7168: 16x64 blocks 25.1 us, 32x64 37.1, 64x128
 // tiles 40.6; MXFP4 128x4096x4096: 9.1 against 10.9).
-int select_rows(int kind, int epi) {
-  const int mr = (epi == EPI_BLOCK || kind == KIND_FP4) ? 1 : 2;
+int select_rows(int M, int N, int kind, int epi) {
+  // 16-row blocks also where their workgroups fill the last round over the CUs better than
+  // 32-row blocks do (ties: 32 rows; graph-timed: 48x4096x4096 fp8 7.2 us against 9.0 -- 192
+  // workgroups against 128 --, int4 6.6 against 8.5, bf16 12.2 against 15.0; 48x7168x2048 fp8
+  // 6.8 with 32-row blocks -- 224 workgroups against 336 -- against 8.3; 128x4096x4096 256 or
+  // 512 workgroups: 32-row blocks, 8.8 us)
+  auto fill = [&](int rows) {
+    const long wg = (long)((M + rows - 1) / rows) * ((N + 63) / 64);
+    return (double)wg / (double)(((wg + kCUs - 1) / kCUs) * kCUs);
+  };
+  const int mr = (epi == EPI_BLOCK || kind == KIND_FP4 || fill(16) > fill(32)) ? 1 : 2;
   for (int v = kFirstRows; v < kNumShapes; ++v)
     if (kShapes[v].bm == 16 * mr && kShapes[v].bn == 64) return v;
   return -1;
@@ -333,6 +342,13 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     if (epi != EPI_BLOCK && kind != KIND_FP4 && list[i].bm == 128 && list[i].bn == 256 && K < 4096) continue;
     const long wg = (long)((M + list[i].bm - 1) / list[i].bm) * ((N + list[i].bn - 1) / list[i].bn);
     if (wg < list[i].min_wg || wg > list[i].max_wg) continue;
+    // int4 weights: 256x256 only from about 2.5 tiles per CU; below that 128x128 (graph-timed, int4:
+    // 4096x4096x4096, 256 tiles of 256x256, 60.5 us against 70.9; 1024x14336x4096 58.0 against
+    // 66.5; 2048x8192x8192 113.4 against 123.6; 4096x8192x8192 (512) 227.8 against 241.7;
+    // 2048x7168x2048 33.9 against 47.4; from 600 tiles 256x256 wins: 8192^3 445.9 against 453.5,
+    // 1536x28672x8192 (672) 300 against 327, 9728x8192x8320 508 against 547, 4096x28672x8192
+    // 726 against 816)
+    if (kind == KIND_INT4 && list[i].bm == 256 && list[i].bn == 256 && wg < 600) continue;
     // blockscale 256x256 tiles between one and two per CU: the second round runs half empty
     // behind the slow blockscale tile (1024x24576x1536, 384 tiles: 62.6 us against 50.4 for
     // 256x128; at 768 tiles, 2048x24576x1536, 94.6 against 99.1)
@@ -340,7 +356,7 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // the last resort (64x128) leaves CUs idle with few tiles: the row-blocked streaming kernel
     // or 64x64 tiles spread the output over more CUs instead
     const long rows_max = (epi == EPI_BLOCK || kind == KIND_FP4) ? kRowsMaxTiles16 : kRowsMaxTiles;
-    if (list[i].min_wg == 0 && wg <= rows_max) return select_rows(kind, epi);
+    if (list[i].min_wg == 0 && wg <= rows_max) return select_rows(M, N, kind, epi);
     if (list[i].min_wg == 0 && wg <= (epi == EPI_BLOCK ? kSmallMaxTilesBlock : kSmallMaxTiles) && kind != KIND_FP4)
       for (int v = 0; v < kFirstDecode; ++v)
         if (kShapes[v].bm == 64 && kShapes[v].bn == 64) return v;

@@ -53,7 +53,9 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(32, 18432, 7168, 3, 0)] == "decode_m2_nb2_w4_u4"
     assert names[lib.flygemm_select_variant(32, 4096, 4096, 1, 0)] == "decode_m2_nb1_w8_u4"
     assert names[lib.flygemm_select_variant(32, 8192, 8192, 1, 0)].startswith("decode_m2")
-    assert names[lib.flygemm_select_variant(48, 8192, 8192, 1, 0)] == "rows_m2_nb4_w8_u3"
+    assert names[lib.flygemm_select_variant(48, 8192, 8192, 1, 0)] == "rows_m2_nb4_w8_u3"   # 256 against 384
+    assert names[lib.flygemm_select_variant(48, 4096, 4096, 0, 0)] == "rows_m1_nb4_w8_u3"   # 192 against 128
+    assert names[lib.flygemm_select_variant(48, 7168, 2048, 0, 0)] == "rows_m2_nb4_w8_u3"   # 224 against 336
     assert names[lib.flygemm_select_variant(64, 7168, 2048, 2, 0)] == "rows_m2_nb4_w8_u3"  # 56 tiles
     assert names[lib.flygemm_select_variant(64, 8192, 8192, 3, 0)] == "rows_m2_nb4_w8_u3"
     assert names[lib.flygemm_select_variant(32, 7168, 7168, 0, 1)] == "rows_m1_nb4_w8_u3"
@@ -91,6 +93,11 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(1024, 7168, 1024, 3, 0)] == "main_128x128_w2x2"
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 5, 0)] == "main_128x256_w2x4"   # MXFP4
     assert names[lib.flygemm_select_variant(1024, 7168, 7168, 2, 0)] == "main_128x128_w2x2"  # int4: no 128x256
+    # int4: 256x256 only from 600 such tiles
+    assert names[lib.flygemm_select_variant(1536, 28672, 8192, 2, 0)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(4096, 4096, 4096, 2, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(8192, 8192, 8192, 2, 0)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(9728, 8192, 8320, 2, 0)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(1280, 7168, 7168, 0, 0)] == "main_128x128_w2x2"  # 280 tiles of 128x256
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
     # 145-256 tiles of 64x128 and at least 384 rows: 128x64 tiles (not int4, MXFP4, blockscale)
