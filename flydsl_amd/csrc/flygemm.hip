@@ -301,12 +301,21 @@ int select_variant(int M, int N, int K, int kind, int epi) {
   // 24576x1536): 256x256 from 160 tiles (4096x24576x1536: 196 us against 231 for 256x128;
   // 1536x7168x7168, 168 tiles: 107 against 110 for 128x128 and 121 for 128x256), then with
   // 160-256 tiles the three-stage 128x256 when N is a multiple of 256 (1024x7168x7168: 66.2 us
-  // against 70.2 for 256x128; 2048x3072x1536: 19.4 against 20.4), else 256x128, 128x128 from 240
+  // against 70.2 for 256x128; 2048x3072x1536: 19.4 against 20.4), 128x128 from 240.
+  // Re-measured against 128x128 as well (graph-timed, the tiles forced): with K of at least 4096
+  // 256x256 from 160 tiles also between one and two per CU (4096x7168x7168, 448 tiles: 220.8 us
+  // against 246.8 for 256x128), and 128x128 before 256x128 (4096x2112x7168: 102.8 against
+  // 120.1); with shorter K the three-stage 128x256 from 160 tiles whatever the count
+  // (1536x24576x1536: 72.0 against 102.9 for 256x256, 1024x24576x1536 45.8 against 49.1 for
+  // 256x128, 8192x7168x2048 132.9 against 156.4, 4096x3072x1536 29.9 against 41.6) -- and with
+  // few rows 64-row tiles rather than 256-row ones (48x24576x1536: 10.7 against 16.6).
   static const Pref kBlock[] = {{256, 256, 512, 160, 1 << 30, true},
                                 {128, 256, 512, 160, 256, true},
-                                {256, 128, 512, 160, 1 << 30, true},
                                 {128, 128, 256, 240, 1 << 30, true},
                                 {64, 128, 256, 0, 1 << 30, true}};
+  static const Pref kBlockShortK[] = {{128, 256, 512, 160, 1 << 30, true},
+                                      {128, 128, 256, 240, 1 << 30, true},
+                                      {64, 128, 256, 0, 1 << 30, true}};
   // int4 weights with few output tiles (at most 512 of 64x128): two K tiles per pipeline step.
   // A 4-wave tile's step moves little, so a step waits on DMA latency rather than bandwidth;
   // two K tiles per stage halve the waits (graph-timed on MI355X, int4 M x N x K with t 64x128
@@ -328,8 +337,9 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     if (t128 > kRowsMaxTiles && t128 <= 352) return find(64, 64, 2);
     if (t128 > 352 && t128 <= 512 && K >= 8192) return find(64, 128, 2);
   }
-  const Pref* list = epi == EPI_BLOCK ? kBlock : kRowcol;
-  const int n = epi == EPI_BLOCK ? 5 : 4;
+  const bool bs_short = epi == EPI_BLOCK && K < 4096;
+  const Pref* list = epi == EPI_BLOCK ? (bs_short ? kBlockShortK : kBlock) : kRowcol;
+  const int n = epi == EPI_BLOCK ? (bs_short ? 3 : 4) : 4;
   for (int i = 0; i < n; ++i) {
     if (kind == KIND_INT4 && !list[i].int4) continue;
     if (epi == EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && N % 256 != 0) continue;
@@ -349,10 +359,6 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // 1536x28672x8192 (672) 300 against 327, 9728x8192x8320 508 against 547, 4096x28672x8192
     // 726 against 816)
     if (kind == KIND_INT4 && list[i].bm == 256 && list[i].bn == 256 && wg < 600) continue;
-    // blockscale 256x256 tiles between one and two per CU: the second round runs half empty
-    // behind the slow blockscale tile (1024x24576x1536, 384 tiles: 62.6 us against 50.4 for
-    // 256x128; at 768 tiles, 2048x24576x1536, 94.6 against 99.1)
-    if (epi == EPI_BLOCK && list[i].bm == 256 && list[i].bn == 256 && wg > 256 && wg < 512) continue;
     // the last resort (64x128) leaves CUs idle with few tiles: the row-blocked streaming kernel
     // or 64x64 tiles spread the output over more CUs instead
     const long rows_max = (epi == EPI_BLOCK || kind == KIND_FP4) ? kRowsMaxTiles16 : kRowsMaxTiles;

@@ -77,8 +77,8 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(512, 4096, 7168, 0, 1)] == "main_64x64_w1x4"
     assert names[lib.flygemm_select_variant(512, 7168, 2304, 0, 1)] == "main_64x128_w1x4"   # 448 tiles
     # not 256x256 between one and two tiles per CU
-    assert names[lib.flygemm_select_variant(1024, 24576, 1536, 0, 1)] == "main_256x128_w2x4"  # 384 tiles
-    assert names[lib.flygemm_select_variant(2048, 24576, 1536, 0, 1)] == "main_256x256_w2x4"  # 768 tiles
+    assert names[lib.flygemm_select_variant(1024, 24576, 1536, 0, 1)] == "main_128x256_w2x4"  # K < 4096
+    assert names[lib.flygemm_select_variant(2048, 24576, 1536, 0, 1)] == "main_128x256_w2x4"  # K < 4096
     assert names[lib.flygemm_select_variant(1536, 7168, 7168, 0, 1)] == "main_256x256_w2x4"  # 168 tiles
     # 256x256 from about 160 tiles, then 128x128 from 272
     assert names[lib.flygemm_select_variant(1536, 8192, 8192, 0, 0)] == "main_256x256_w2x4"
