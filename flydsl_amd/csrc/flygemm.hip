@@ -208,6 +208,13 @@ int select_rows(int M, int N, int kind, int epi) {
   return -1;
 }
 
+// the main family's one-K-tile variant of a tile shape (-1: none)
+int main_shape(int bm, int bn) {
+  for (int v = 0; v < kFirstDecode; ++v)
+    if (kShapes[v].bm == bm && kShapes[v].bn == bn && kShapes[v].ksub == 1) return v;
+  return -1;
+}
+
 int select_variant(int M, int N, int K, int kind, int epi) {
   // The decode family up to 32 rows; above that its per-row A traffic grows and the 64x128 tile
   // is faster (and above 16 rows with the blockscale epilogue when N has at least 32 column tiles
@@ -373,8 +380,24 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // level or up to 2% slower; int4 10% slower), not for blockscale nor MXFP4
     if (list[i].min_wg == 0 && wg <= kMidMaxTiles && M >= 384 && epi != EPI_BLOCK && kind != KIND_INT4 &&
         kind != KIND_FP4 && (long)((M + 127) / 128) * ((N + 63) / 64) <= wg)
-      for (int v = 0; v < kFirstDecode; ++v)
-        if (kShapes[v].bm == 128 && kShapes[v].bn == 64) return v;
+      return main_shape(128, 64);
+    // 129-192 rows (two 128-row blocks against three of 64), or 65-128 rows with at least 96 MB
+    // of B (which 64-row tiles read twice, past what the 256 MB last-level cache keeps): 128x64
+    // tiles too (graph-timed against 64x128: fp8 144 / 160 / 192 x 14336 x 4096 24.4 / 24.1 /
+    // 25.9 us against 26.7 / 27.1 / 27.9, int8 alike, bf16 43.8 / 44.7 / 48.1 against 52.8 /
+    // 53.8 / 55.7, x 8192 x 8192 level to 4% faster; fp8 80 / 96 / 112 x 28672 x 8192 55.4 /
+    // 58.0 / 60.3 against 57.3 / 60.2 / 62.6, bf16 107.0 / 111.0 / 115.6 against 113.3 / 118.2 /
+    // 122.7; at 224-256 rows level or slower).  Not int4 nor MXFP4 (64x128 faster there at 160
+    // and 192 rows: 14.4 / 14.5 us against 15.8 / 16.1), nor blockscale.
+    if (list[i].min_wg == 0 && epi != EPI_BLOCK && kind != KIND_INT4 && kind != KIND_FP4 &&
+        ((M > 128 && M <= 192) || (M > 64 && M <= 128 && (long)N * K >= (96L << 20))))
+      return main_shape(128, 64);
+    // 129-256 rows: 256x128 rather than 128x256 -- as many tiles, but one row block, so B is
+    // read once instead of twice (graph-timed, x 28672 x 8192: fp8 M = 144 / 160 / 192 / 224 /
+    // 256 63.5 / 62.6 / 65.1 / 68.7 / 70.0 us against 74.6 / 74.6 / 74.6 / 72.4 / 73.1, int8
+    // alike, bf16 125.5 / 125.9 / 128.3 against 137.2 / 139.9 / 138.3 at 144-192 rows and level
+    // at 224-256; fp16 and MXFP4 at 160 rows 128.4 / 37.6 against 141.6 / 42.0)
+    if (epi != EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && M > 128 && M <= 256) return main_shape(256, 128);
     for (int v = 0; v < kFirstDecode; ++v)
       if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }

@@ -104,6 +104,20 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(512, 4096, 7168, 0, 0)] == "main_128x64_w2x2"
     assert names[lib.flygemm_select_variant(384, 5120, 7168, 1, 0)] == "main_128x64_w2x2"
     assert names[lib.flygemm_select_variant(512, 4096, 4096, 3, 0)] == "main_128x64_w2x2"
+    # 129-192 rows, or 65-128 rows with at least 96 MB of B: 128x64 rather than 64x128 (not int4,
+    # MXFP4, blockscale)
+    for args, want in {(144, 14336, 4096, 0, 0): "main_128x64_w2x2", (192, 14336, 4096, 1, 0): "main_128x64_w2x2",
+                       (160, 14336, 4096, 3, 0): "main_128x64_w2x2", (192, 8192, 8192, 4, 0): "main_128x64_w2x2",
+                       (96, 28672, 8192, 0, 0): "main_128x64_w2x2", (112, 14336, 4096, 3, 0): "main_128x64_w2x2",
+                       (96, 14336, 4096, 0, 0): "main_64x128_w1x4", (224, 14336, 4096, 0, 0): "main_64x128_w1x4",
+                       (192, 14336, 4096, 5, 0): "main_64x128_w1x4", (192, 14336, 4096, 2, 0): "main_64x64_w1x4_k2",
+                       (192, 14336, 7168, 0, 1): "main_64x128_w1x4"}.items():
+        assert names[lib.flygemm_select_variant(*args)] == want, args
+    # 129-256 rows: 256x128 where the list gives 128x256 (B read by one row block, not two)
+    for args in [(144, 28672, 8192, 0, 0), (256, 28672, 8192, 1, 0), (192, 28672, 8192, 3, 0),
+                 (160, 28672, 8192, 5, 0)]:
+        assert names[lib.flygemm_select_variant(*args)] == "main_256x128_w2x4", args
+    assert names[lib.flygemm_select_variant(384, 28672, 8192, 0, 0)] == "main_256x256_w2x4"
     # int4 with 65-512 tiles of 64x128: two K tiles per step -- 64x64 tiles up to 352, 64x128
     # tiles above with K of at least 8192 (the one-K-tile 64x128 below that)
     for args, want in {(256, 4096, 4096, 2, 0): "main_64x64_w1x4_k2", (512, 4096, 4096, 2, 0): "main_64x64_w1x4_k2",
