@@ -389,15 +389,21 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // 58.0 / 60.3 against 57.3 / 60.2 / 62.6, bf16 107.0 / 111.0 / 115.6 against 113.3 / 118.2 /
     // 122.7; at 224-256 rows level or slower).  Not int4 nor MXFP4 (64x128 faster there at 160
     // and 192 rows: 14.4 / 14.5 us against 15.8 / 16.1), nor blockscale.
+    // Above 192 rows the same holds for K of at least 8192 bytes (fp8 320 / 384 / 512 x 8192 x
+    // 8192 48.5 / 51.5 / 54.8 against 49.8 / 53.4 / 56.1, bf16 92.4 / 97.1 / 100.1 against 95.1
+    // / 102.5 / 106.5; bf16 x 4096 x 4096, 320-1024 rows, 3-7% faster), not for shorter K (fp8
+    // 640x4096x4096 24.3 against 21.6, x 7168 x 2048 6-18% slower).
     if (list[i].min_wg == 0 && epi != EPI_BLOCK && kind != KIND_INT4 && kind != KIND_FP4 &&
-        ((M > 128 && M <= 192) || (M > 64 && M <= 128 && (long)N * K >= (96L << 20))))
+        ((M > 128 && M <= 192) || (M > 64 && M <= 128 && (long)N * K >= (96L << 20)) || (M > 192 && K >= 8192)))
       return main_shape(128, 64);
-    // 129-256 rows: 256x128 rather than 128x256 -- as many tiles, but one row block, so B is
-    // read once instead of twice (graph-timed, x 28672 x 8192: fp8 M = 144 / 160 / 192 / 224 /
-    // 256 63.5 / 62.6 / 65.1 / 68.7 / 70.0 us against 74.6 / 74.6 / 74.6 / 72.4 / 73.1, int8
-    // alike, bf16 125.5 / 125.9 / 128.3 against 137.2 / 139.9 / 138.3 at 144-192 rows and level
-    // at 224-256; fp16 and MXFP4 at 160 rows 128.4 / 37.6 against 141.6 / 42.0)
-    if (epi != EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && M > 128 && M <= 256) return main_shape(256, 128);
+    // 129-256 and 385-512 rows: 256x128 rather than 128x256 -- as many tiles, half the row
+    // blocks, so B is read half as often (graph-timed, x 28672 x 8192: fp8 M = 144 / 160 / 192 /
+    // 224 / 256 63.5 / 62.6 / 65.1 / 68.7 / 70.0 us against 74.6 / 74.6 / 74.6 / 72.4 / 73.1,
+    // int8 alike, bf16 125.5 / 125.9 / 128.3 against 137.2 / 139.9 / 138.3 at 144-192 rows and
+    // level at 224-256; fp16 and MXFP4 at 160 rows 128.4 / 37.6 against 141.6 / 42.0;
+    // 512x14336x4096 fp8 34.7 against 36.0, bf16 64.9 against 68.9)
+    if (epi != EPI_BLOCK && list[i].bm == 128 && list[i].bn == 256 && M > 128 && M <= 512 && ((M + 127) / 128) % 2 == 0)
+      return main_shape(256, 128);
     for (int v = 0; v < kFirstDecode; ++v)
       if (kShapes[v].bm == list[i].bm && kShapes[v].bn == list[i].bn && kShapes[v].threads == list[i].threads) return v;
   }
