@@ -392,8 +392,10 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // Above 192 rows the same holds for K of at least 8192 bytes (fp8 320 / 384 / 512 x 8192 x
     // 8192 48.5 / 51.5 / 54.8 against 49.8 / 53.4 / 56.1, bf16 92.4 / 97.1 / 100.1 against 95.1
     // / 102.5 / 106.5; bf16 x 4096 x 4096, 320-1024 rows, 3-7% faster), not for shorter K (fp8
-    // 640x4096x4096 24.3 against 21.6, x 7168 x 2048 6-18% slower).
-    if (list[i].min_wg == 0 && epi != EPI_BLOCK && kind != KIND_INT4 && kind != KIND_FP4 &&
+    // 640x4096x4096 24.3 against 21.6, x 7168 x 2048 6-18% slower).  All of it where B
+    // dominates, N >= 4M: with N near M the 64x128 tile is faster (bf16 1536x2112x7168 68.8
+    // against 79.1).
+    if (list[i].min_wg == 0 && epi != EPI_BLOCK && kind != KIND_INT4 && kind != KIND_FP4 && N >= 4L * M &&
         ((M > 128 && M <= 192) || (M > 64 && M <= 128 && (long)N * K >= (96L << 20)) || (M > 192 && K >= 8192)))
       return main_shape(128, 64);
     // 129-256 and 385-512 rows: 256x128 rather than 128x256 -- as many tiles, half the row

@@ -124,7 +124,8 @@ def test_variant_table():
     # above 192 rows with K of at least 8192 bytes: 128x64 rather than 64x128
     for args, want in {(384, 8192, 8192, 0, 0): "main_128x64_w2x2", (640, 4096, 4096, 3, 0): "main_128x64_w2x2",
                        (640, 4096, 4096, 0, 0): "main_64x128_w1x4", (512, 7168, 2048, 3, 0): "main_64x128_w1x4",
-                       (256, 7168, 7168, 0, 0): "main_64x128_w1x4"}.items():
+                       (256, 7168, 7168, 0, 0): "main_64x128_w1x4", (1536, 2112, 7168, 3, 0): "main_64x128_w1x4",
+                       (1024, 4096, 4096, 3, 0): "main_128x64_w2x2"}.items():
         assert names[lib.flygemm_select_variant(*args)] == want, args
     # int4 with 65-512 tiles of 64x128: two K tiles per step -- 64x64 tiles up to 352, 64x128
     # tiles above with K of at least 8192 (the one-K-tile 64x128 below that)
