@@ -365,7 +365,16 @@ int select_variant(int M, int N, int K, int kind, int epi) {
     // 2048x7168x2048 33.9 against 47.4; from 600 tiles 256x256 wins: 8192^3 445.9 against 453.5,
     // 1536x28672x8192 (672) 300 against 327, 9728x8192x8320 508 against 547, 4096x28672x8192
     // 726 against 816)
-    if (kind == KIND_INT4 && list[i].bm == 256 && list[i].bn == 256 && wg < 600) continue;
+    // -- except with one round of them and B far larger than A (N >= 16M), where two row blocks
+    // read B half as often as 128x128's four (int4 x 28672 x 8192: 512 rows 109.6 us against 119.8,
+    // 384 rows 102.6 against 107.0; with 768 rows, 336 tiles, 197.9 against 169.8)
+    if (kind == KIND_INT4 && list[i].bm == 256 && list[i].bn == 256 && wg < 600 && !(wg <= kCUs && N >= 16L * M))
+      continue;
+    // int4 with 129-192 rows: 64x128 rather than 128x128 (three row blocks cover 192 rows, two of
+    // 128 leave a quarter or more idle; x 28672 x 8192: 160 / 192 rows 55.2 / 55.9 us against
+    // 58.5 / 59.3; 256 rows 69.3 against 64.2)
+    if (kind == KIND_INT4 && epi != EPI_BLOCK && list[i].bm == 128 && list[i].bn == 128 && M > 128 && M <= 192)
+      return main_shape(64, 128);
     // the last resort (64x128) leaves CUs idle with few tiles: the row-blocked streaming kernel
     // or 64x64 tiles spread the output over more CUs instead
     const long rows_max = (epi == EPI_BLOCK || kind == KIND_FP4) ? kRowsMaxTiles16 : kRowsMaxTiles;

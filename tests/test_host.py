@@ -98,6 +98,13 @@ def test_variant_table():
     assert names[lib.flygemm_select_variant(4096, 4096, 4096, 2, 0)] == "main_128x128_w2x2"
     assert names[lib.flygemm_select_variant(8192, 8192, 8192, 2, 0)] == "main_256x256_w2x4"
     assert names[lib.flygemm_select_variant(9728, 8192, 8320, 2, 0)] == "main_256x256_w2x4"
+    # ... and with one round of them where N >= 16M; 64x128 for 129-192 rows
+    assert names[lib.flygemm_select_variant(512, 28672, 8192, 2, 0)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(384, 28672, 8192, 2, 0)] == "main_256x256_w2x4"
+    assert names[lib.flygemm_select_variant(768, 28672, 8192, 2, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(1024, 14336, 4096, 2, 0)] == "main_128x128_w2x2"
+    assert names[lib.flygemm_select_variant(192, 28672, 8192, 2, 0)] == "main_64x128_w1x4"
+    assert names[lib.flygemm_select_variant(256, 28672, 8192, 2, 0)] == "main_128x128_w2x2"
     assert names[lib.flygemm_select_variant(1280, 7168, 7168, 0, 0)] == "main_128x128_w2x2"  # 280 tiles of 128x256
     assert names[lib.flygemm_select_variant(1024, 4096, 4096, 0, 0)] == "main_64x128_w1x4"
     # 145-256 tiles of 64x128 and at least 384 rows: 128x64 tiles (not int4, MXFP4, blockscale)
