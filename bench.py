@@ -187,7 +187,8 @@ class MoeStageWorkload:
 # bench name -> (MoE workload, stage)
 # (the R variants run stage 2 in reduce mode: per-route rows, then the top-k reduction)
 MOE_BENCH = {"MP1": ("DSP", 1), "MP2": ("DSP", 2), "MP2R": ("DSP", 2), "MD1": ("DSD", 1), "MD2": ("DSD", 2),
-             "MD2R": ("DSD", 2), "MB1": ("DSB", 1), "MB2": ("DSB", 2)}
+             "MD2R": ("DSD", 2), "MB1": ("DSB", 1), "MB2": ("DSB", 2),
+             "MG1": ("RBL", 1), "MG2": ("RBL", 2), "MH1": ("RBS", 1), "MH2": ("RBS", 2)}
 
 
 class MoeRunner:
@@ -569,7 +570,7 @@ def main():
         log(f"[bench] timing {name} variant={r2.variant}")
         n2 = max(50, args.secondary_launches)
         ms2, _ = r2.time(n2, max(2, args.warmup // 2), graph=True)
-        b2 = "hbm" if name in ("C1", "C2", "G1", "G2", "Q", "MD1", "MD2", "MD2R", "MB1", "MB2") else "mfma"
+        b2 = "hbm" if name in ("C1", "C2", "G1", "G2", "Q", "MD1", "MD2", "MD2R", "MB1", "MB2", "MH1", "MH2") else "mfma"
         sec[name] = {"ms": round(ms2, 5), "GB/s": round(w2.bytes / ms2 / 1e6, 1), "kernel": r2.variant,
                      "timing": f"HIP graph of {n2} launches, median of 3 timed replays after >= 0.1 s of untimed ones",
                      "roofline": roofline(w2, ms2, b2, traffic_from_profile(name))}

@@ -30,7 +30,7 @@ SIGNATURES = [
     ("flygemm_moe_gemm1", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 12 + [_P]),
     ("flygemm_moe_gemm2", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 13 + [_P]),
     ("flygemm_moe_reduce", ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _P]),
-    ("flygemm_moe_select_tile", ctypes.c_int, [_I] * 9 + [_P, _P]),
+    ("flygemm_moe_select_tile", ctypes.c_int, [_I] * 10 + [_P, _P]),
     ("flygemm_moe_gemm2_reduce_noalloc", ctypes.c_int,
      [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 12 + [_P, _I, _P]),
     ("flygemm_moe_blockscale_gemm1", ctypes.c_int, [_P, _P, _P, _F, _F, _P, _P, _F, _P] + [_I] * 11 + [_P]),

@@ -30,6 +30,11 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
     return MoeKernel{moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS>, WM_ * WN_ * 64};
   // (64 or 128 columns: the launcher never takes 256 for these single-block stage-1 tiles)
   T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4)
+  // runs of four 64-row blocks, 128 columns (128 gate + 128 up weight rows): fp8 routings with
+  // large experts (see moe_tiles)
+  if constexpr (!BS && KIND == KIND_FP8) {
+    T(64, 4, 128, 2, 4)
+  }
 #undef T
   return MoeKernel{nullptr, 0};
 }
@@ -49,6 +54,7 @@ bool moe_stream_stage1(int stage, int kind, bool bs) {
 
 MoeKernel moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
   if (bs) return kind == KIND_FP8 ? moe_stage1_tile<KIND_FP8, true>(tm, r, tn) : MoeKernel{nullptr, 0};
+  if (kind == KIND_FP8 && r * tm == 256) return moe_stage1_tile<KIND_FP8, false>(tm, r, tn);
   if (moe_stream_stage1(1, kind, bs))
     return r * tm == 128 && tn == 64 ? moe_stage1_stream_kernel(kind, tm) : MoeKernel{nullptr, 0};
   return kind == KIND_W4A16 ? moe_stage1_tile<KIND_W4A16, false>(tm, r, tn) : MoeKernel{nullptr, 0};
@@ -72,9 +78,34 @@ int pick_tile_n(int N, long runs) {
 // Tile of a call: runs of R routing blocks per workgroup and tile_n output columns (the
 // caller's tile_n, already validated, is a hint).  atomics: a stage-2 call that accumulates
 // (per-route-row calls take the stream kernel's tiles where it applies).
-int moe_tiles(int stage, int tokens, int N, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
+int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
               bool atomics, const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
+  // Large experts (fp8, 64-row blocks, inter_dim of at least 1024, at least 512 routes per
+  // expert on average; stage 1 with model_dim of at least 4096): runs of four blocks (256 rows)
+  // on 2 x 4 waves with both operands staged through LDS -- 128 output columns in stage 1 (128
+  // gate + 128 up weight rows), 256 in stage 2 -- the bytes per flop of the dense kernel's large
+  // tiles, where the stream kernel's 128 x 64 tiles (stage 1) and single-block tiles (stage 2)
+  // move two to four times as many.  Graph-timed on MI355X (µs, stage 1 / stage 2 with atomics,
+  // former choice against runs): the reference's benchmark shape 32768 tokens, 8192 x 8192, 16
+  // experts, top-4: 29190 -> 18376 / 25441 -> 8885; the same at 4096 tokens 3538 -> 2477 / 3119
+  // -> 1276; 8192 tokens, 4096 x 14336, 8 experts, top-2: 2931 -> 2015 / 2405 -> 1306, at 2048
+  // tokens 906 -> 709 / 582 -> 391; 8192 tokens, 4096 x 1536, 64 experts, top-8: 972 -> 851 / 910
+  // -> 747; 16384 tokens, 7168 x 2048, 256 experts, top-8: 5393 -> 4419 / 4562 -> 3060.  Not for
+  // DS-TP8 (inter_dim 256: 289 -> 336 / 731 -> 838) nor inter_dim 768 (270 -> 270 / 282 -> 324).
+  const int inter = stage == 1 ? N : K;
+  if (kind == KIND_FP8 && !bs && tile_m == 64 && inter >= 1024 && routes >= 512L * experts) {
+    if (stage == 1 && K >= 4096 && N % 128 == 0) {
+      *r_out = 4;
+      *tn_out = 128;
+      return 0;
+    }
+    if (stage == 2 && N % 256 == 0) {
+      *r_out = 4;
+      *tn_out = 256;
+      return 0;
+    }
+  }
   // Stage 1 of 1-byte, 16-bit and W4A8 weights: the stream kernel, 128-row runs of 64 columns
   // (every N here is a multiple of 64: tile_n, checked by the callers, divides it).  The
   // caller's tile_n is a hint throughout: tiling does not change results.
@@ -193,8 +224,8 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
     return fail(hipErrorInvalidValue, "%s: group_size=%d: group scales are for int4_bf16 with group_size 32", what,
                 group_size);
   int R = 1;
-  if (int rc = moe_tiles(stage, tokens, N, experts, topk, tile_m, tile_n, kind, bs, stage == 2 && accumulate != 0, what,
-                         &R, &tile_n))
+  if (int rc = moe_tiles(stage, tokens, N, K, experts, topk, tile_m, tile_n, kind, bs, stage == 2 && accumulate != 0,
+                         what, &R, &tile_n))
     return rc;
   const bool is16 = moe_a_16bit(kind);      // 2-byte activations (bf16, fp16, W4A16)
   const long kb = is16 ? 2L * K : (long)K;  // activation bytes per row
@@ -455,13 +486,14 @@ int flygemm_moe_reduce(void* y, const void* x, const void* valid_mask, int32_t t
   return 0;
 }
 
-int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t experts, int32_t topk, int32_t tile_m,
-                            int32_t tile_n, int32_t in_dtype, int32_t blockscale, int32_t* runs, int32_t* tile_n_out) {
+int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t k, int32_t experts, int32_t topk,
+                            int32_t tile_m, int32_t tile_n, int32_t in_dtype, int32_t blockscale, int32_t* runs,
+                            int32_t* tile_n_out) {
   const char* what = "moe_select_tile";
   if (stage != 1 && stage != 2) return fail(hipErrorInvalidValue, "%s: stage %d must be 1 or 2", what, stage);
-  if (tokens < 0 || n <= 0 || experts <= 0 || topk < 1 || topk > 255)
-    return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d n=%d experts=%d topk=%d", what, tokens, n, experts,
-                topk);
+  if (tokens < 0 || n <= 0 || k <= 0 || experts <= 0 || topk < 1 || topk > 255)
+    return fail(hipErrorInvalidValue, "%s: invalid sizes tokens=%d n=%d k=%d experts=%d topk=%d", what, tokens, n, k,
+                experts, topk);
   if (tile_m != 16 && tile_m != 32 && tile_m != 64)
     return fail(hipErrorInvalidValue, "%s: tile_m=%d must be 16, 32 or 64", what, tile_m);
   if (tile_n > 0 && ((tile_n != 64 && tile_n != 128 && tile_n != 256) || n % tile_n != 0))
@@ -471,7 +503,8 @@ int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t ex
   const int kind = moe_kind(in_dtype, stage, &token_slot);
   if (kind < 0) return fail(hipErrorInvalidValue, "%s: in_dtype %d not supported", what, in_dtype);
   int r = 1, tn = 0;
-  if (int rc = moe_tiles(stage, tokens, n, experts, topk, tile_m, tile_n, kind, blockscale != 0, stage == 2, what, &r, &tn))
+  if (int rc = moe_tiles(stage, tokens, n, k, experts, topk, tile_m, tile_n, kind, blockscale != 0, stage == 2, what, &r,
+                         &tn))
     return rc;
   *runs = r;
   *tile_n_out = tn;

@@ -164,6 +164,10 @@ MOE_WORKLOADS = {
     "DSD": MoeWorkload("DSD", 8, 7168, 256, 256, 8, 32, 256, 256, seed=2, note="DS-TP8-decode-bs8"),
     "DSB": MoeWorkload("DSB", 128, 7168, 256, 256, 8, 16, 256, 256, "fp8_block", seed=3,
                        note="DS-V3-M128 blockscale (test_moe_blockscale.py:201)"),
+    # the reference's MoE benchmark list (scripts/run_benchmark.sh:100-104): tokens, model_dim,
+    # inter_dim, experts, topk, tile_m, tile_n, tile_n2
+    "RBL": MoeWorkload("RBL", 32768, 8192, 8192, 16, 4, 64, 128, 256, seed=4, note="reference MoE benchmark, large"),
+    "RBS": MoeWorkload("RBS", 64, 6144, 1024, 128, 8, 16, 64, 64, seed=5, note="reference MoE benchmark, small"),
 }
 
 

@@ -202,17 +202,19 @@ int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const
 
 /* The MoE launchers' tile choice for a call with these sizes (they treat tile_n as a hint):
  * *runs = routing blocks per workgroup (1: single-block tiles; more: runs of 128 rows in stage
- * 1, 256 in stage 2) and *tile_n_out = output columns per tile.  Stage 2 values are those of
- * accumulating calls; per-route-row calls (accumulate = 0) of 1-byte, int4 (int8 activations)
- * and 16-bit weights with inter_dim of 1, 2 or 4 128-byte K steps run 64-column tiles instead:
- * single routing blocks (two for tile_m 16) with 1 to 32 routes per expert on average, 128-row
- * runs from 128 routes per expert (int4: 256; from 32 for tile_m 16).  n is inter_dim for stage 1 and
- * model_dim for stage 2; in_dtype as for flygemm_moe_gemm1/2; blockscale != 0 for the
- * blockscale MoE.  Validates like the launchers; touches no device.  Counterpart of the
- * reference's compile-time tile arguments (kernels/moe_gemm_2stage.py:93-121), for tests and
+ * 1, 256 in stage 2, and 256 in stage 1 of fp8 routings with large experts) and *tile_n_out =
+ * output columns per tile.  Stage 2 values are those of accumulating calls; per-route-row calls
+ * (accumulate = 0) of 1-byte, int4 (int8 activations) and 16-bit weights with inter_dim of 1, 2
+ * or 4 128-byte K steps run 64-column tiles instead: single routing blocks (two for tile_m 16)
+ * with 1 to 32 routes per expert on average, 128-row runs from 128 routes per expert (int4: 256;
+ * from 32 for tile_m 16).  n is the GEMM's output width and k its depth (stage 1: inter_dim and
+ * model_dim; stage 2: model_dim and inter_dim); in_dtype as for flygemm_moe_gemm1/2; blockscale
+ * != 0 for the blockscale MoE.  Validates like the launchers; touches no device.  Counterpart of
+ * the reference's compile-time tile arguments (kernels/moe_gemm_2stage.py:93-121), for tests and
  * tuning, like flygemm_select_variant. */
-int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t experts, int32_t topk, int32_t tile_m,
-                            int32_t tile_n, int32_t in_dtype, int32_t blockscale, int32_t* runs, int32_t* tile_n_out);
+int flygemm_moe_select_tile(int32_t stage, int32_t tokens, int32_t n, int32_t k, int32_t experts, int32_t topk,
+                            int32_t tile_m, int32_t tile_n, int32_t in_dtype, int32_t blockscale, int32_t* runs,
+                            int32_t* tile_n_out);
 
 /* Reduce mode, second step: y [tokens][model_dim] = sum over k < topk of x [tokens][topk]
  * [model_dim] (only slots with valid_mask[t*topk+k] != 0 when valid_mask, int8 [tokens*topk], is

@@ -462,10 +462,12 @@ def test_moe_tile_choice_pinned():
     import ctypes
     lib = _lib.load()
 
-    def sel(stage, tokens, n, experts, topk, tile_m, tile_n, kind="fp8", bs=0):
+    def sel(stage, tokens, n, experts, topk, tile_m, tile_n, kind="fp8", bs=0, k=None):
+        # k: the GEMM's depth, DS-TP8's by default (model_dim 7168 in stage 1, inter_dim 256 in 2)
+        k = (7168 if stage == 1 else 256) if k is None else k
         r, tn = ctypes.c_int32(), ctypes.c_int32()
-        rc = lib.flygemm_moe_select_tile(stage, tokens, n, experts, topk, tile_m, tile_n, _lib.FLYGEMM_IN[kind], bs,
-                                         ctypes.byref(r), ctypes.byref(tn))
+        rc = lib.flygemm_moe_select_tile(stage, tokens, n, k, experts, topk, tile_m, tile_n, _lib.FLYGEMM_IN[kind],
+                                         bs, ctypes.byref(r), ctypes.byref(tn))
         return (r.value, tn.value) if rc == 0 else rc
 
     # stage 1 stream kernel: 128 / tile_m blocks per run, 64 columns, whatever the routing and the
@@ -495,6 +497,19 @@ def test_moe_tile_choice_pinned():
     for kind in ("fp8", "int8", "bf16", "fp16", "int4", "int8smooth", "int4_bf16"):
         assert sel(2, 160, 512, 64, 4, 32, 256, kind) == (1, 128), kind
     assert sel(2, 128, 7168, 256, 8, 32, 0) == (1, 128)
+    # fp8 routings with large experts (64-row blocks, inter_dim >= 1024, >= 512 routes per expert;
+    # stage 1 with model_dim >= 4096): runs of 256 rows, 128 columns in stage 1, 256 in stage 2
+    assert sel(1, 32768, 8192, 16, 4, 64, 128, k=8192) == (4, 128)      # the reference's benchmark shape
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, k=8192) == (4, 256)
+    assert sel(1, 2048, 14336, 8, 2, 64, 128, k=4096) == (4, 128)       # 512 routes per expert
+    assert sel(2, 2048, 4096, 8, 2, 64, 256, k=14336) == (4, 256)
+    assert sel(1, 2048, 14336, 8, 2, 64, 128, k=2048) == (2, 64)        # model_dim below 4096
+    assert sel(2, 8192, 2048, 128, 8, 64, 256, k=768) == (1, 64)        # inter_dim below 1024
+    assert sel(2, 1000, 8192, 16, 4, 64, 256, k=8192)[0] == 1           # 250 routes per expert
+    assert sel(1, 32768, 8192, 16, 4, 32, 128, k=8192) == (4, 64)       # 32-row blocks: the stream kernel
+    assert sel(1, 32768, 8192, 16, 4, 64, 128, "int8", k=8192) == (2, 64)
+    assert lib.flygemm_moe_select_tile(1, 64, 256, 0, 4, 2, 64, 0, 0, 0, ctypes.byref(ctypes.c_int32()),
+                                       ctypes.byref(ctypes.c_int32())) != 0   # k = 0
     # blockscale and W4A16 never take run tiles
     assert sel(2, 8192, 7168, 128, 8, 16, 256, "fp8", 1)[0] == 1
     assert sel(2, 8192, 7168, 128, 8, 16, 256, "int4_bf16")[0] == 1
