@@ -110,6 +110,11 @@ __device__ __forceinline__ float silu_f(float x) {
 // more run, which streams the expert's weights once more (DS-TP8 prefill, 64-row blocks, R = 2:
 // 608 runs against 577).  Every lane reads one expert id behind b0 (and one ahead); the ballots
 // make the result uniform over the wave and, all waves reading the same ids, the workgroup.
+// Kinds with run tiles of four 64-row blocks for routings with large experts (moe_tiles)
+constexpr bool moe_big_kind(int kind) {
+  return kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_BF16 || kind == KIND_F16;
+}
+
 template <int R>
 __device__ __forceinline__ int moe_run_blocks(const int32_t* expert_ids, int b0, int e, int nbv, int lane) {
   if constexpr (R == 1) {

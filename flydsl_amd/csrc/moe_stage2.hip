@@ -22,8 +22,8 @@ MoeKernel stage2_tile(int tm, int r, int tn) {
   if constexpr (!BS && KIND != KIND_W4A16) {
     T(16, 16, 256, 2, 4)
   }
-  // runs of four 64-row blocks, 256 columns: fp8 routings with large experts (see moe_tiles)
-  if constexpr (!BS && KIND == KIND_FP8) {
+  // runs of four 64-row blocks, 256 columns: routings with large experts (see moe_tiles)
+  if constexpr (!BS && moe_big_kind(KIND)) {
     T(64, 4, 256, 2, 4)
   }
 #undef T

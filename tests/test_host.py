@@ -507,7 +507,13 @@ def test_moe_tile_choice_pinned():
     assert sel(2, 8192, 2048, 128, 8, 64, 256, k=768) == (1, 64)        # inter_dim below 1024
     assert sel(2, 1000, 8192, 16, 4, 64, 256, k=8192)[0] == 1           # 250 routes per expert
     assert sel(1, 32768, 8192, 16, 4, 32, 128, k=8192) == (4, 64)       # 32-row blocks: the stream kernel
-    assert sel(1, 32768, 8192, 16, 4, 64, 128, "int8", k=8192) == (2, 64)
+    for kind in ("int8", "int8smooth", "bf16", "fp16"):
+        assert sel(1, 32768, 8192, 16, 4, 64, 128, kind, k=8192) == (4, 128), kind
+        assert sel(2, 32768, 8192, 16, 4, 64, 256, kind, k=8192) == (4, 256), kind
+    for kind in ("int4", "int4_bf16"):
+        assert sel(2, 32768, 8192, 16, 4, 64, 256, kind, k=8192)[0] == 1, kind
+    assert sel(1, 32768, 8192, 16, 4, 64, 128, "int4", k=8192) == (2, 64)
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, "fp8", 1, k=8192)[0] == 1            # blockscale
     assert lib.flygemm_moe_select_tile(1, 64, 256, 0, 4, 2, 64, 0, 0, 0, ctypes.byref(ctypes.c_int32()),
                                        ctypes.byref(ctypes.c_int32())) != 0   # k = 0
     # blockscale and W4A16 never take run tiles
