@@ -30,10 +30,10 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
     return MoeKernel{moe_gemm_kernel<1, KIND, M_, R_, N_, WM_, WN_, false, BS>, WM_ * WN_ * 64};
   // (64 or 128 columns: the launcher never takes 256 for these single-block stage-1 tiles)
   T(16, 1, 64, 1, 4) T(16, 1, 128, 1, 4) T(32, 1, 64, 1, 4) T(32, 1, 128, 1, 4) T(64, 1, 64, 1, 4) T(64, 1, 128, 1, 4)
-  // runs of four 64-row blocks, 128 columns (128 gate + 128 up weight rows): routings with large
-  // experts (see moe_tiles)
+  // runs of 256 rows (four 64-row, eight 32-row or sixteen 16-row blocks), 128 columns (128 gate
+  // + 128 up weight rows): routings with large experts (see moe_tiles)
   if constexpr (!BS && moe_big_kind(KIND)) {
-    T(64, 4, 128, 2, 4)
+    T(64, 4, 128, 2, 4) T(32, 8, 128, 2, 4) T(16, 16, 128, 2, 4)
   }
 #undef T
   return MoeKernel{nullptr, 0};
@@ -89,8 +89,9 @@ int pick_tile_n(int N, long runs) {
 int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
               bool atomics, const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
-  // Large experts (fp8, int8, bf16, fp16; 64-row blocks, inter_dim of at least 1024, at least 512
-  // routes per expert on average; stage 1 with model_dim of at least 4096): runs of four blocks (256 rows)
+  // Large experts (fp8, int8, bf16, fp16; inter_dim of at least 1024, at least 512 routes per
+  // expert on average; stage 1 with model_dim of at least 4096): runs of 256 rows (four 64-row,
+  // eight 32-row or sixteen 16-row blocks)
   // on 2 x 4 waves with both operands staged through LDS -- 128 output columns in stage 1 (128
   // gate + 128 up weight rows), 256 in stage 2 -- the bytes per flop of the dense kernel's large
   // tiles, where the stream kernel's 128 x 64 tiles (stage 1) and single-block tiles (stage 2)
@@ -103,17 +104,20 @@ int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int ti
   // DS-TP8 (inter_dim 256: 289 -> 336 / 731 -> 838) nor inter_dim 768 (270 -> 270 / 282 -> 324).
   // int8, bf16 and fp16 alike (8192 tokens, 4096 x 14336, 8 experts, top-2: int8 3089 -> 2013 /
   // 2496 -> 1311, bf16 6574 -> 4106 / 5592 -> 2711; 4096 tokens, 8192 x 8192, 16 experts, top-4:
-  // bf16 7303 -> 4782 / 6984 -> 2494; stage-1 outputs bit-equal).  Not int4 nor W4A16, whose
+  // bf16 7303 -> 4782 / 6984 -> 2494; stage-1 outputs bit-equal), and 32- / 16-row blocks too
+  // (8192 tokens, 4096 x 14336, 8 experts, top-2, fp8: 32-row 3000 -> 2007 / 4920 -> 1199, 16-row
+  // stage 1 3117 -> 2195, its stage 2 already on runs; bf16 32-row 4096 tokens, 8192 x 8192, 16
+  // experts, top-4: 7313 -> 5109 / 12150 -> 2549).  Not int4 nor W4A16, whose
   // weights take other operand paths, nor blockscale.
   const int inter = stage == 1 ? N : K;
-  if (moe_big_kind(kind) && !bs && tile_m == 64 && inter >= 1024 && routes >= 512L * experts) {
+  if (moe_big_kind(kind) && !bs && inter >= 1024 && routes >= 512L * experts) {
     if (stage == 1 && K >= 4096 && N % 128 == 0) {
-      *r_out = 4;
+      *r_out = 256 / tile_m;
       *tn_out = 128;
       return 0;
     }
     if (stage == 2 && N % 256 == 0) {
-      *r_out = 4;
+      *r_out = 256 / tile_m;
       *tn_out = 256;
       return 0;
     }

@@ -22,9 +22,10 @@ MoeKernel stage2_tile(int tm, int r, int tn) {
   if constexpr (!BS && KIND != KIND_W4A16) {
     T(16, 16, 256, 2, 4)
   }
-  // runs of four 64-row blocks, 256 columns: routings with large experts (see moe_tiles)
+  // runs of 256 rows (four 64-row or eight 32-row blocks), 256 columns: routings with large
+  // experts (see moe_tiles)
   if constexpr (!BS && moe_big_kind(KIND)) {
-    T(64, 4, 256, 2, 4)
+    T(64, 4, 256, 2, 4) T(32, 8, 256, 2, 4)
   }
 #undef T
   return MoeKernel{nullptr, 0};

@@ -806,33 +806,35 @@ def test_single_block_wide_tiles_blockscale(gpu):
         _wide_blockscale(gpu, tokens, s1, s2)
 
 
+@pytest.mark.parametrize("tile_m", [64, 32, 16])
 @pytest.mark.parametrize("kind", ["fp8", "int8", "int8smooth", "bf16", "fp16"])
-def test_large_expert_run_tiles(gpu, kind):
-    """Routings with large experts (64-row blocks, inter_dim 1024, model_dim 4096, 550
-    routes per expert on average: 1100 tokens top-2 of 4 experts), checked through
+def test_large_expert_run_tiles(gpu, kind, tile_m):
+    """Routings with large experts (inter_dim 1024, model_dim 4096, 550 routes per expert on
+    average: 1100 tokens top-2 of 4 experts; routing blocks of 64, 32 and 16 rows), checked through
     flygemm_moe_select_tile first: stage 1 on runs of 256 rows x 128 columns, stage 2 on runs of
     256 rows x 256 columns, both with atomics (fp32 and bf16 outputs) and per-route rows (the
     reduce mode); the experts' uneven route counts leave partial last runs.  A sample of tokens
     against the oracle."""
     from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
-    w = W.moe_custom(1100, 4096, 1024, 4, 2, 64, 128, 256, kind, seed=31)
-    assert _chosen_tile(1, w, kind) == (4, 128) and _chosen_tile(2, w, kind) == (4, 256)
+    w = W.moe_custom(1100, 4096, 1024, 4, 2, tile_m, 128, 256, kind, seed=31)
+    R = 256 // tile_m
+    assert _chosen_tile(1, w, kind) == (R, 128) and _chosen_tile(2, w, kind) == (R, 256)
     p = W.moe_problem(w, gpu)
     counts = np.bincount(_np(p["topk_ids"]).ravel(), minlength=w.experts)
-    assert ((counts + 63) // 64 % 4 != 0).any(), counts     # some expert's last run is partial
+    assert ((counts + tile_m - 1) // tile_m % R != 0).any(), counts     # some expert's last run is partial
     rows = np.unique(np.r_[np.linspace(0, w.tokens - 1, 48).astype(int), w.tokens - 1])
-    _say(f"large-expert run tiles {kind}: stage 1")
+    _say(f"large-expert run tiles {kind} tm{tile_m}: stage 1")
     o1 = run_stage1(p, gpu, "bf16", doweight=True)
     torch.cuda.synchronize()
     assert torch.isfinite(o1.float()).all()
     _check(o1, ref_stage1(p, True, rows), rows, what=f"large experts {kind} stage1")
     for out_dtype in ("f32", "bf16"):
-        _say(f"large-expert run tiles {kind}: stage 2 atomics {out_dtype}")
+        _say(f"large-expert run tiles {kind} tm{tile_m}: stage 2 atomics {out_dtype}")
         o2 = run_stage2(p, gpu, out_dtype, doweight=True)
         torch.cuda.synchronize()
         _check(o2, ref_stage2(p, True, rows), rows, what=f"large experts {kind} stage2 {out_dtype}",
                atol_rms=BF16_ATOMIC_ATOL if out_dtype == "bf16" else 1e-2)
-    _say(f"large-expert run tiles {kind}: stage 2 reduce mode")
+    _say(f"large-expert run tiles {kind} tm{tile_m}: stage 2 reduce mode")
     fn = compile_moe_gemm2_ex(model_dim=w.model_dim, inter_dim=w.inter_dim, experts=w.experts, topk=w.topk,
                               tile_m=w.tile_m, tile_n=w.tile_n2, tile_k=_tile_k(kind), doweight_stage2=False,
                               in_dtype=kind, out_dtype="f16", mode=MoeGemm2Mode.REDUCE)

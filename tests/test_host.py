@@ -506,7 +506,10 @@ def test_moe_tile_choice_pinned():
     assert sel(1, 2048, 14336, 8, 2, 64, 128, k=2048) == (2, 64)        # model_dim below 4096
     assert sel(2, 8192, 2048, 128, 8, 64, 256, k=768) == (1, 64)        # inter_dim below 1024
     assert sel(2, 1000, 8192, 16, 4, 64, 256, k=8192)[0] == 1           # 250 routes per expert
-    assert sel(1, 32768, 8192, 16, 4, 32, 128, k=8192) == (4, 64)       # 32-row blocks: the stream kernel
+    assert sel(1, 32768, 8192, 16, 4, 32, 128, k=8192) == (8, 128)      # 32- and 16-row blocks alike
+    assert sel(2, 32768, 8192, 16, 4, 32, 256, k=8192) == (8, 256)
+    assert sel(1, 32768, 8192, 16, 4, 16, 128, k=8192) == (16, 128)
+    assert sel(1, 32768, 8192, 16, 4, 32, 128, k=2048) == (4, 64)       # model_dim below 4096: the stream kernel
     for kind in ("int8", "int8smooth", "bf16", "fp16"):
         assert sel(1, 32768, 8192, 16, 4, 64, 128, kind, k=8192) == (4, 128), kind
         assert sel(2, 32768, 8192, 16, 4, 64, 256, kind, k=8192) == (4, 256), kind
