@@ -112,7 +112,7 @@ __device__ __forceinline__ float silu_f(float x) {
 // make the result uniform over the wave and, all waves reading the same ids, the workgroup.
 // Kinds with run tiles of four 64-row blocks for routings with large experts (moe_tiles)
 constexpr bool moe_big_kind(int kind) {
-  return kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_BF16 || kind == KIND_F16;
+  return kind == KIND_FP8 || kind == KIND_INT8 || kind == KIND_BF16 || kind == KIND_F16 || kind == KIND_INT4;
 }
 
 template <int R>

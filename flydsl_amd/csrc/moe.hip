@@ -60,6 +60,7 @@ MoeKernel moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
       case KIND_INT8: return moe_stage1_tile<KIND_INT8, false>(tm, r, tn);
       case KIND_BF16: return moe_stage1_tile<KIND_BF16, false>(tm, r, tn);
       case KIND_F16: return moe_stage1_tile<KIND_F16, false>(tm, r, tn);
+      case KIND_INT4: return moe_stage1_tile<KIND_INT4, false>(tm, r, tn);
       default: return MoeKernel{nullptr, 0};
     }
   }
@@ -89,7 +90,7 @@ int pick_tile_n(int N, long runs) {
 int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
               bool atomics, const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
-  // Large experts (fp8, int8, bf16, fp16; inter_dim of at least 1024, at least 512 routes per
+  // Large experts (fp8, int8, bf16, fp16, int4; inter_dim of at least 1024, at least 512 routes per
   // expert on average; stage 1 with model_dim of at least 4096): runs of 256 rows (four 64-row,
   // eight 32-row or sixteen 16-row blocks)
   // on 2 x 4 waves with both operands staged through LDS -- 128 output columns in stage 1 (128
@@ -107,10 +108,13 @@ int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int ti
   // bf16 7303 -> 4782 / 6984 -> 2494; stage-1 outputs bit-equal), and 32- / 16-row blocks too
   // (8192 tokens, 4096 x 14336, 8 experts, top-2, fp8: 32-row 3000 -> 2007 / 4920 -> 1199, 16-row
   // stage 1 3117 -> 2195, its stage 2 already on runs; bf16 32-row 4096 tokens, 8192 x 8192, 16
-  // experts, top-4: 7313 -> 5109 / 12150 -> 2549).  Not int4 nor W4A16, whose
-  // weights take other operand paths, nor blockscale.
+  // experts, top-4: 7313 -> 5109 / 12150 -> 2549).  int4 (W4A8), whose weights move half the
+  // bytes, from inter_dim 4096 (4096 tokens, 8192 x 8192, 16 experts, top-4: 2353 -> 1935 / 1769
+  // -> 1085; 8192 tokens, 4096 x 14336: 2062 -> 1787 / 1371 -> 1168; at 4096 x 1536, 64 experts:
+  // 765 -> 744 / 671 -> 731).  Not W4A16 (its group scales ride the two-slot pipeline) nor
+  // blockscale.
   const int inter = stage == 1 ? N : K;
-  if (moe_big_kind(kind) && !bs && inter >= 1024 && routes >= 512L * experts) {
+  if (moe_big_kind(kind) && !bs && inter >= (kind == KIND_INT4 ? 4096 : 1024) && routes >= 512L * experts) {
     if (stage == 1 && K >= 4096 && N % 128 == 0) {
       *r_out = 256 / tile_m;
       *tn_out = 128;

@@ -807,7 +807,7 @@ def test_single_block_wide_tiles_blockscale(gpu):
 
 
 @pytest.mark.parametrize("tile_m", [64, 32, 16])
-@pytest.mark.parametrize("kind", ["fp8", "int8", "int8smooth", "bf16", "fp16"])
+@pytest.mark.parametrize("kind", ["fp8", "int8", "int8smooth", "bf16", "fp16", "int4"])
 def test_large_expert_run_tiles(gpu, kind, tile_m):
     """Routings with large experts (inter_dim 1024, model_dim 4096, 550 routes per expert on
     average: 1100 tokens top-2 of 4 experts; routing blocks of 64, 32 and 16 rows), checked through
@@ -816,7 +816,8 @@ def test_large_expert_run_tiles(gpu, kind, tile_m):
     reduce mode); the experts' uneven route counts leave partial last runs.  A sample of tokens
     against the oracle."""
     from flydsl_amd.kernels.moe_gemm_2stage import MoeGemm2Mode, compile_moe_gemm2_ex
-    w = W.moe_custom(1100, 4096, 1024, 4, 2, tile_m, 128, 256, kind, seed=31)
+    # (int4 weights from inter_dim 4096)
+    w = W.moe_custom(1100, 4096, 4096 if kind == "int4" else 1024, 4, 2, tile_m, 128, 256, kind, seed=31)
     R = 256 // tile_m
     assert _chosen_tile(1, w, kind) == (R, 128) and _chosen_tile(2, w, kind) == (R, 256)
     p = W.moe_problem(w, gpu)

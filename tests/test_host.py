@@ -513,9 +513,11 @@ def test_moe_tile_choice_pinned():
     for kind in ("int8", "int8smooth", "bf16", "fp16"):
         assert sel(1, 32768, 8192, 16, 4, 64, 128, kind, k=8192) == (4, 128), kind
         assert sel(2, 32768, 8192, 16, 4, 64, 256, kind, k=8192) == (4, 256), kind
-    for kind in ("int4", "int4_bf16"):
-        assert sel(2, 32768, 8192, 16, 4, 64, 256, kind, k=8192)[0] == 1, kind
-    assert sel(1, 32768, 8192, 16, 4, 64, 128, "int4", k=8192) == (2, 64)
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4_bf16", k=8192)[0] == 1
+    assert sel(1, 32768, 8192, 16, 4, 64, 128, "int4", k=8192) == (4, 128)    # int4 from inter_dim 4096
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4", k=8192) == (4, 256)
+    assert sel(1, 32768, 2048, 16, 4, 64, 128, "int4", k=8192) == (2, 64)
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4", k=2048)[0] == 1
     assert sel(2, 32768, 8192, 16, 4, 64, 256, "fp8", 1, k=8192)[0] == 1            # blockscale
     assert lib.flygemm_moe_select_tile(1, 64, 256, 0, 4, 2, 64, 0, 0, 0, ctypes.byref(ctypes.c_int32()),
                                        ctypes.byref(ctypes.c_int32())) != 0   # k = 0
