@@ -113,8 +113,15 @@ int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int ti
   // -> 1085; 8192 tokens, 4096 x 14336: 2062 -> 1787 / 1371 -> 1168; at 4096 x 1536, 64 experts:
   // 765 -> 744 / 671 -> 731).  Not W4A16 (its group scales ride the two-slot pipeline) nor
   // blockscale.
+  // With inter_dim of at least 4096 (not int4) from 256 routes per expert already (1024 tokens,
+  // 4096 x 14336, 8 experts, top-2: 485 -> 361 / 358 -> 199; 1024 tokens, 8192 x 8192, 16
+  // experts, top-4: 1148 -> 906 / 816 -> 478), not at 1536 (2048 tokens, 64 experts, top-8, stage
+  // 2 256 -> 265) nor with fewer routes (128 per expert, 4096 x 1536: 198 -> 216 / 155 -> 210).
   const int inter = stage == 1 ? N : K;
-  if (moe_big_kind(kind) && !bs && inter >= (kind == KIND_INT4 ? 4096 : 1024) && routes >= 512L * experts) {
+  const bool big = kind == KIND_INT4 ? inter >= 4096 && routes >= 512L * experts
+                                     : (inter >= 1024 && routes >= 512L * experts) ||
+                                           (inter >= 4096 && routes >= 256L * experts);
+  if (moe_big_kind(kind) && !bs && big) {
     if (stage == 1 && K >= 4096 && N % 128 == 0) {
       *r_out = 256 / tile_m;
       *tn_out = 128;

@@ -848,6 +848,22 @@ def test_large_expert_run_tiles(gpu, kind, tile_m):
     _check(o3, ref_stage2(p, False, rows, route_round="f16"), rows, what=f"large experts {kind} stage2 reduce")
 
 
+@pytest.mark.parametrize("kind", ["fp8", "bf16"])
+def test_large_expert_run_tiles_few_routes(gpu, kind):
+    """About 256 routes per expert with inter_dim 4096 (520 tokens top-2 of 4 experts, model_dim
+    4096): the run tiles too, each expert about one run of 256 rows, some partial."""
+    w = W.moe_custom(520, 4096, 4096, 4, 2, 64, 128, 256, kind, seed=37)
+    assert _chosen_tile(1, w, kind) == (4, 128) and _chosen_tile(2, w, kind) == (4, 256)
+    p = W.moe_problem(w, gpu)
+    rows = np.unique(np.r_[np.linspace(0, w.tokens - 1, 40).astype(int), w.tokens - 1])
+    _say(f"large-expert run tiles, few routes {kind}")
+    o1 = run_stage1(p, gpu, "f16", doweight=False)
+    o2 = run_stage2(p, gpu, "f32", doweight=True)
+    torch.cuda.synchronize()
+    _check(o1, ref_stage1(p, False, rows), rows, what=f"few routes {kind} stage1")
+    _check(o2, ref_stage2(p, True, rows), rows, what=f"few routes {kind} stage2")
+
+
 def _wide_blockscale(gpu, tokens, s1, s2):
     w = W.moe_custom(tokens, 512, 1024, 64, 4, 32, 256, 256, "fp8_block", seed=12 + tokens)
     assert _chosen_tile(1, w, "fp8", 1) == s1 and _chosen_tile(2, w, "fp8", 1) == s2

@@ -505,7 +505,11 @@ def test_moe_tile_choice_pinned():
     assert sel(2, 2048, 4096, 8, 2, 64, 256, k=14336) == (4, 256)
     assert sel(1, 2048, 14336, 8, 2, 64, 128, k=2048) == (2, 64)        # model_dim below 4096
     assert sel(2, 8192, 2048, 128, 8, 64, 256, k=768) == (1, 64)        # inter_dim below 1024
-    assert sel(2, 1000, 8192, 16, 4, 64, 256, k=8192)[0] == 1           # 250 routes per expert
+    assert sel(1, 1024, 14336, 8, 2, 64, 128, k=4096) == (4, 128)       # 256 routes per expert, inter_dim
+    assert sel(2, 1024, 4096, 8, 2, 64, 256, k=14336) == (4, 256)       # of 4096 or more
+    assert sel(2, 2048, 4096, 64, 8, 64, 256, k=1536)[0] == 1           # 256 per expert, inter_dim 1536
+    assert sel(2, 1024, 4096, 8, 2, 64, 256, "int4", k=14336)[0] == 1   # int4: 512 per expert
+    assert sel(2, 960, 8192, 16, 4, 64, 256, k=8192)[0] == 1            # 240 routes per expert
     assert sel(1, 32768, 8192, 16, 4, 32, 128, k=8192) == (8, 128)      # 32- and 16-row blocks alike
     assert sel(2, 32768, 8192, 16, 4, 32, 256, k=8192) == (8, 256)
     assert sel(1, 32768, 8192, 16, 4, 16, 128, k=8192) == (16, 128)
