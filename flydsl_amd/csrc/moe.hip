@@ -35,6 +35,10 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
   if constexpr (!BS && moe_big_kind(KIND)) {
     T(64, 4, 128, 2, 4) T(32, 8, 128, 2, 4) T(16, 16, 128, 2, 4)
   }
+  // blockscale with 16-row blocks: runs of 256 rows, 64 columns (see moe_tiles)
+  if constexpr (BS) {
+    T(16, 16, 64, 2, 4)
+  }
 #undef T
   return MoeKernel{nullptr, 0};
 }
@@ -90,6 +94,27 @@ int pick_tile_n(int N, long runs) {
 int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
               bool atomics, const char* what, int* r_out, int* tn_out) {
   const long routes = (long)tokens * topk;
+  const int inter = stage == 1 ? N : K;
+  // Blockscale on large experts (inter_dim of at least 1024): runs of 256 rows, 128 columns in
+  // stage 2 (16-row blocks from 128 routes per expert, 64-row blocks from 512) and 64 in stage 1
+  // (16-row blocks only).  Graph-timed, DS-V3 prefill dims (7168 x 2048, 256 experts, top-8),
+  // single-block tiles against runs (µs): 16-row blocks, 16384 tokens stage 1 15736 -> 13737,
+  // stage 2 17192 -> 6105; 4096 tokens 4868 -> 4067 / 4495 -> 2036; 64-row blocks stage 2 7054 ->
+  // 5748 at 16384 tokens, level at 4096 (2032 / 2012); 64-row stage 1 slower on runs (9239 ->
+  // 12862), as is inter_dim 256 (8192 tokens, 16-row blocks, stage 2 909 -> 1196).
+  if (bs && inter >= 1024) {
+    if (stage == 2 && N % 128 == 0 &&
+        (tile_m == 16 ? routes >= 128L * experts : tile_m == 64 && routes >= 512L * experts)) {
+      *r_out = 256 / tile_m;
+      *tn_out = 128;
+      return 0;
+    }
+    if (stage == 1 && tile_m == 16 && routes >= 128L * experts && N % 64 == 0) {
+      *r_out = 16;
+      *tn_out = 64;
+      return 0;
+    }
+  }
   // Large experts (fp8, int8, bf16, fp16, int4; inter_dim of at least 1024, at least 512 routes per
   // expert on average; stage 1 with model_dim of at least 4096): runs of 256 rows (four 64-row,
   // eight 32-row or sixteen 16-row blocks)
@@ -117,7 +142,6 @@ int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int ti
   // 4096 x 14336, 8 experts, top-2: 485 -> 361 / 358 -> 199; 1024 tokens, 8192 x 8192, 16
   // experts, top-4: 1148 -> 906 / 816 -> 478), not at 1536 (2048 tokens, 64 experts, top-8, stage
   // 2 256 -> 265) nor with fewer routes (128 per expert, 4096 x 1536: 198 -> 216 / 155 -> 210).
-  const int inter = stage == 1 ? N : K;
   const bool big = kind == KIND_INT4 ? inter >= 4096 && routes >= 512L * experts
                                      : (inter >= 1024 && routes >= 512L * experts) ||
                                            (inter >= 4096 && routes >= 256L * experts);

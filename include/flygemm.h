@@ -202,7 +202,7 @@ int flygemm_moe_blockscale_gemm2(void* out, const void* a2, const void* w, const
 
 /* The MoE launchers' tile choice for a call with these sizes (they treat tile_n as a hint):
  * *runs = routing blocks per workgroup (1: single-block tiles; more: runs of 128 rows in stage
- * 1, 256 in stage 2, and 256 in stage 1 of routings with large experts) and *tile_n_out =
+ * 1, 256 in stage 2, and 256 in stage 1 of routings with large experts, blockscale included) and *tile_n_out =
  * output columns per tile.  Stage 2 values are those of accumulating calls; per-route-row calls
  * (accumulate = 0) of 1-byte, int4 (int8 activations) and 16-bit weights with inter_dim of 1, 2
  * or 4 128-byte K steps run 64-column tiles instead: single routing blocks (two for tile_m 16)

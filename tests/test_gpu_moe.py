@@ -584,6 +584,29 @@ def run_bs_stage2(p, dev, out_dtype="f16", doweight=True, mode="atomic"):
     return out
 
 
+@pytest.mark.parametrize("tile_m", [16, 64])
+def test_blockscale_run_tiles(gpu, tile_m):
+    """Blockscale MoE with large experts (1100 tokens top-2 of 4 experts, model_dim 1024,
+    inter_dim 1024: 550 routes per expert), checked through flygemm_moe_select_tile first: stage
+    2 on runs of 256 rows x 128 columns (atomics and per-route rows), stage 1 on runs of 256 rows
+    x 64 columns for 16-row blocks (single-block tiles for 64-row ones); some runs partial."""
+    w = W.moe_custom(1100, 1024, 1024, 4, 2, tile_m, 128, 256, "fp8_block", seed=41)
+    R = 256 // tile_m
+    assert _chosen_tile(2, w, "fp8", 1) == (R, 128)
+    assert _chosen_tile(1, w, "fp8", 1)[0] == (R if tile_m == 16 else 1)
+    p = W.moe_problem(w, gpu)
+    counts = np.bincount(_np(p["topk_ids"]).ravel(), minlength=w.experts)
+    assert ((counts + tile_m - 1) // tile_m % R != 0).any(), counts
+    _say(f"blockscale run tiles tm{tile_m}")
+    o1 = run_bs_stage1(p, gpu, "f16", doweight=True)
+    o2 = run_bs_stage2(p, gpu, "f32", doweight=True)
+    o3 = run_bs_stage2(p, gpu, "f16", doweight=False, mode="reduce")
+    torch.cuda.synchronize()
+    _check(o1, ref_bs1(p, True), what=f"blockscale runs tm{tile_m} stage1")
+    _check(o2, ref_bs2(p, True), what=f"blockscale runs tm{tile_m} stage2 atomics")
+    _check(o3, ref_bs2(p, False), what=f"blockscale runs tm{tile_m} stage2 reduce")
+
+
 def ref_bs1(p, doweight, subset=None):
     w = p["workload"]
     return omoe.gemm1_blockscale(_host(p["x"]), _host(p["w1"]), _np(p["sx_blocks"]), _np(p["sw1_blocks"]),

@@ -455,8 +455,9 @@ def test_moe_blockscale_validation():
 
 def test_moe_tile_choice_pinned():
     """flygemm_moe_select_tile gives the launchers' tile choice without a device: stage 1 of
-    1-byte, 16-bit and W4A8 weights always runs the stream kernel (runs of 128 rows, 64
-    columns); W4A16 and blockscale stage 1 keep single-block tiles; stage 2 takes runs for
+    1-byte, 16-bit and W4A8 weights runs the stream kernel (runs of 128 rows, 64 columns) but
+    for large experts; W4A16 and blockscale stage 1 keep single-block tiles but blockscale's
+    large experts of 16-row blocks; stage 2 takes runs for
     16-row blocks of prefill routings, 64 columns for decode-sized ones, wide single-block tiles
     in between (the reachable kernel set the GPU tests cover), and the launchers' validation."""
     import ctypes
@@ -522,10 +523,19 @@ def test_moe_tile_choice_pinned():
     assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4", k=8192) == (4, 256)
     assert sel(1, 32768, 2048, 16, 4, 64, 128, "int4", k=8192) == (2, 64)
     assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4", k=2048)[0] == 1
-    assert sel(2, 32768, 8192, 16, 4, 64, 256, "fp8", 1, k=8192)[0] == 1            # blockscale
+    # blockscale on large experts (inter_dim >= 1024): stage 2 runs of 256 rows x 128 columns for
+    # 16-row blocks from 128 routes per expert and 64-row blocks from 512; stage 1 runs of 256 rows
+    # x 64 columns for 16-row blocks only
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, "fp8", 1, k=8192) == (4, 128)
+    assert sel(2, 16384, 7168, 256, 8, 16, 256, "fp8", 1, k=2048) == (16, 128)
+    assert sel(2, 4096, 7168, 256, 8, 16, 256, "fp8", 1, k=2048) == (16, 128)      # 128 routes per expert
+    assert sel(2, 4096, 7168, 256, 8, 64, 256, "fp8", 1, k=2048)[0] == 1           # 64-row blocks: 512
+    assert sel(1, 16384, 2048, 256, 8, 16, 256, "fp8", 1, k=7168) == (16, 64)
+    assert sel(1, 16384, 2048, 256, 8, 64, 256, "fp8", 1, k=7168)[0] == 1
+    assert sel(2, 8192, 7168, 256, 8, 16, 256, "fp8", 1, k=256)[0] == 1            # inter_dim 256
     assert lib.flygemm_moe_select_tile(1, 64, 256, 0, 4, 2, 64, 0, 0, 0, ctypes.byref(ctypes.c_int32()),
                                        ctypes.byref(ctypes.c_int32())) != 0   # k = 0
-    # blockscale and W4A16 never take run tiles
+    # blockscale (inter_dim 256) and W4A16 take no run tiles
     assert sel(2, 8192, 7168, 128, 8, 16, 256, "fp8", 1)[0] == 1
     assert sel(2, 8192, 7168, 128, 8, 16, 256, "int4_bf16")[0] == 1
     assert sel(1, 8192, 256, 128, 8, 16, 256, "fp8", 1)[0] == 1
