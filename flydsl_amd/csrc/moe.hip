@@ -96,15 +96,17 @@ int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int ti
   const long routes = (long)tokens * topk;
   const int inter = stage == 1 ? N : K;
   // Blockscale on large experts (inter_dim of at least 1024): runs of 256 rows, 128 columns in
-  // stage 2 (16-row blocks from 128 routes per expert, 64-row blocks from 512) and 64 in stage 1
-  // (16-row blocks only).  Graph-timed, DS-V3 prefill dims (7168 x 2048, 256 experts, top-8),
-  // single-block tiles against runs (µs): 16-row blocks, 16384 tokens stage 1 15736 -> 13737,
-  // stage 2 17192 -> 6105; 4096 tokens 4868 -> 4067 / 4495 -> 2036; 64-row blocks stage 2 7054 ->
-  // 5748 at 16384 tokens, level at 4096 (2032 / 2012); 64-row stage 1 slower on runs (9239 ->
-  // 12862), as is inter_dim 256 (8192 tokens, 16-row blocks, stage 2 909 -> 1196).
+  // stage 2 (16- and 32-row blocks from 128 routes per expert, 64-row blocks from 512) and 64 in
+  // stage 1 (16-row blocks only).  Graph-timed, DS-V3 prefill dims (7168 x 2048, 256 experts,
+  // top-8), single-block tiles against runs (µs): 16-row blocks, 16384 tokens stage 1 15736 ->
+  // 13737, stage 2 17192 -> 6105; 4096 tokens 4868 -> 4067 / 4495 -> 2036; 32-row blocks stage 2
+  // 8812 -> 5908 at 16384 tokens, 2453 -> 2032 at 4096, slower at 2048 (1386 -> 1713); 64-row
+  // blocks stage 2 7054 -> 5748 at 16384 tokens, level at 4096 (2032 / 2012); stage 1 slower on
+  // runs for 32- and 64-row blocks (9239 -> 12862), as is inter_dim 256 (8192 tokens, 16-row
+  // blocks, stage 2 909 -> 1196).
   if (bs && inter >= 1024) {
     if (stage == 2 && N % 128 == 0 &&
-        (tile_m == 16 ? routes >= 128L * experts : tile_m == 64 && routes >= 512L * experts)) {
+        (tile_m == 64 ? routes >= 512L * experts : routes >= 128L * experts)) {
       *r_out = 256 / tile_m;
       *tn_out = 128;
       return 0;

@@ -30,7 +30,7 @@ MoeKernel stage2_tile(int tm, int r, int tn) {
   // blockscale: runs of 256 rows, 128 columns (the per-K-block partials and factors fit next to
   // 128-column accumulators), for large experts (see moe_tiles)
   if constexpr (BS) {
-    T(64, 4, 128, 2, 4) T(16, 16, 128, 2, 4)
+    T(64, 4, 128, 2, 4) T(32, 8, 128, 2, 4) T(16, 16, 128, 2, 4)
   }
 #undef T
   return MoeKernel{nullptr, 0};

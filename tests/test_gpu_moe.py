@@ -584,12 +584,12 @@ def run_bs_stage2(p, dev, out_dtype="f16", doweight=True, mode="atomic"):
     return out
 
 
-@pytest.mark.parametrize("tile_m", [16, 64])
+@pytest.mark.parametrize("tile_m", [16, 32, 64])
 def test_blockscale_run_tiles(gpu, tile_m):
     """Blockscale MoE with large experts (1100 tokens top-2 of 4 experts, model_dim 1024,
     inter_dim 1024: 550 routes per expert), checked through flygemm_moe_select_tile first: stage
     2 on runs of 256 rows x 128 columns (atomics and per-route rows), stage 1 on runs of 256 rows
-    x 64 columns for 16-row blocks (single-block tiles for 64-row ones); some runs partial."""
+    x 64 columns for 16-row blocks (single-block tiles for 32- and 64-row ones); some runs partial."""
     w = W.moe_custom(1100, 1024, 1024, 4, 2, tile_m, 128, 256, "fp8_block", seed=41)
     R = 256 // tile_m
     assert _chosen_tile(2, w, "fp8", 1) == (R, 128)

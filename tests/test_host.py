@@ -530,6 +530,9 @@ def test_moe_tile_choice_pinned():
     assert sel(2, 16384, 7168, 256, 8, 16, 256, "fp8", 1, k=2048) == (16, 128)
     assert sel(2, 4096, 7168, 256, 8, 16, 256, "fp8", 1, k=2048) == (16, 128)      # 128 routes per expert
     assert sel(2, 4096, 7168, 256, 8, 64, 256, "fp8", 1, k=2048)[0] == 1           # 64-row blocks: 512
+    assert sel(2, 4096, 7168, 256, 8, 32, 256, "fp8", 1, k=2048) == (8, 128)       # 32-row blocks: 128
+    assert sel(2, 2048, 7168, 256, 8, 32, 256, "fp8", 1, k=2048)[0] == 1
+    assert sel(1, 16384, 2048, 256, 8, 32, 256, "fp8", 1, k=7168)[0] == 1
     assert sel(1, 16384, 2048, 256, 8, 16, 256, "fp8", 1, k=7168) == (16, 64)
     assert sel(1, 16384, 2048, 256, 8, 64, 256, "fp8", 1, k=7168)[0] == 1
     assert sel(2, 8192, 7168, 256, 8, 16, 256, "fp8", 1, k=256)[0] == 1            # inter_dim 256
