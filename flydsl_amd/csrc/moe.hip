@@ -35,6 +35,9 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
   if constexpr (!BS && moe_big_kind(KIND)) {
     T(64, 4, 128, 2, 4) T(32, 8, 128, 2, 4) T(16, 16, 128, 2, 4)
   }
+  if constexpr (KIND == KIND_W4A16) {
+    T(64, 4, 128, 2, 4) T(32, 8, 128, 2, 4)
+  }
   // blockscale with 16-row blocks: runs of 256 rows, 64 columns (see moe_tiles)
   if constexpr (BS) {
     T(16, 16, 64, 2, 4)
@@ -65,6 +68,7 @@ MoeKernel moe_stage1_kernel(int kind, int tm, int r, int tn, bool bs) {
       case KIND_BF16: return moe_stage1_tile<KIND_BF16, false>(tm, r, tn);
       case KIND_F16: return moe_stage1_tile<KIND_F16, false>(tm, r, tn);
       case KIND_INT4: return moe_stage1_tile<KIND_INT4, false>(tm, r, tn);
+      case KIND_W4A16: return moe_stage1_tile<KIND_W4A16, false>(tm, r, tn);
       default: return MoeKernel{nullptr, 0};
     }
   }
@@ -92,7 +96,7 @@ int pick_tile_n(int N, long runs) {
 // caller's tile_n, already validated, is a hint).  atomics: a stage-2 call that accumulates
 // (per-route-row calls take the stream kernel's tiles where it applies).
 int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int tile_m, int tile_n, int kind, bool bs,
-              bool atomics, const char* what, int* r_out, int* tn_out) {
+              bool atomics, const char* what, int* r_out, int* tn_out, bool wgroup = false) {
   const long routes = (long)tokens * topk;
   const int inter = stage == 1 ? N : K;
   // Blockscale on large experts (inter_dim of at least 1024): runs of 256 rows, 128 columns in
@@ -147,7 +151,13 @@ int moe_tiles(int stage, int tokens, int N, int K, int experts, int topk, int ti
   const bool big = kind == KIND_INT4 ? inter >= 4096 && routes >= 512L * experts
                                      : (inter >= 1024 && routes >= 512L * experts) ||
                                            (inter >= 4096 && routes >= 256L * experts);
-  if (moe_big_kind(kind) && !bs && big) {
+  // W4A16 with per-row weight scales (no group scales, which ride the two-slot pipeline) takes
+  // them as bf16 does, for 32- and 64-row blocks (4096 tokens, 8192 x 8192, 16 experts, top-4:
+  // 6994 -> 5431 / 3271 -> 2392; 8192 tokens, 4096 x 14336, 8 experts, top-2: 6213 -> 4603 / 2780
+  // -> 2815).
+  const bool w4a16_runs = kind == KIND_W4A16 && !wgroup && tile_m >= 32 &&
+                          ((inter >= 1024 && routes >= 512L * experts) || (inter >= 4096 && routes >= 256L * experts));
+  if ((moe_big_kind(kind) && !bs && big) || w4a16_runs) {
     if (stage == 1 && K >= 4096 && N % 128 == 0) {
       *r_out = 256 / tile_m;
       *tn_out = 128;
@@ -278,7 +288,7 @@ int moe_plan(int stage, void* out, const void* a, const void* w, const float* sa
                 group_size);
   int R = 1;
   if (int rc = moe_tiles(stage, tokens, N, K, experts, topk, tile_m, tile_n, kind, bs, stage == 2 && accumulate != 0,
-                         what, &R, &tile_n))
+                         what, &R, &tile_n, group_size > 0))
     return rc;
   const bool is16 = moe_a_16bit(kind);      // 2-byte activations (bf16, fp16, W4A16)
   const long kb = is16 ? 2L * K : (long)K;  // activation bytes per row

@@ -24,7 +24,7 @@ MoeKernel stage2_tile(int tm, int r, int tn) {
   }
   // runs of 256 rows (four 64-row or eight 32-row blocks), 256 columns: routings with large
   // experts (see moe_tiles)
-  if constexpr (!BS && moe_big_kind(KIND)) {
+  if constexpr (!BS && (moe_big_kind(KIND) || KIND == KIND_W4A16)) {
     T(64, 4, 256, 2, 4) T(32, 8, 256, 2, 4)
   }
   // blockscale: runs of 256 rows, 128 columns (the per-K-block partials and factors fit next to

@@ -871,6 +871,24 @@ def test_large_expert_run_tiles(gpu, kind, tile_m):
     _check(o3, ref_stage2(p, False, rows, route_round="f16"), rows, what=f"large experts {kind} stage2 reduce")
 
 
+@pytest.mark.parametrize("tile_m", [64, 32])
+def test_large_expert_run_tiles_w4a16(gpu, tile_m):
+    """W4A16 with per-row weight scales on large experts (1100 tokens top-2 of 4 experts,
+    model_dim 4096, inter_dim 1024): runs of 256 rows in both stages; with group scales the
+    single-block tiles stay.  A sample of tokens against the oracle."""
+    w = W.moe_custom(1100, 4096, 1024, 4, 2, tile_m, 128, 256, "int4_bf16", seed=43)
+    R = 256 // tile_m
+    assert _chosen_tile(1, w, "int4_bf16") == (R, 128) and _chosen_tile(2, w, "int4_bf16") == (R, 256)
+    p = W.moe_problem(w, gpu)
+    rows = np.unique(np.r_[np.linspace(0, w.tokens - 1, 40).astype(int), w.tokens - 1])
+    _say(f"large-expert run tiles W4A16 tm{tile_m}")
+    o1 = run_stage1(p, gpu, "bf16", doweight=True)
+    o2 = run_stage2(p, gpu, "f32", doweight=True)
+    torch.cuda.synchronize()
+    check_stage1(p, o1, True, rows, rows, what=f"W4A16 runs tm{tile_m} stage1")
+    check_stage2(p, o2, True, rows, rows, what=f"W4A16 runs tm{tile_m} stage2")
+
+
 @pytest.mark.parametrize("kind", ["fp8", "bf16"])
 def test_large_expert_run_tiles_few_routes(gpu, kind):
     """About 256 routes per expert with inter_dim 4096 (520 tokens top-2 of 4 experts, model_dim

@@ -518,7 +518,9 @@ def test_moe_tile_choice_pinned():
     for kind in ("int8", "int8smooth", "bf16", "fp16"):
         assert sel(1, 32768, 8192, 16, 4, 64, 128, kind, k=8192) == (4, 128), kind
         assert sel(2, 32768, 8192, 16, 4, 64, 256, kind, k=8192) == (4, 256), kind
-    assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4_bf16", k=8192)[0] == 1
+    assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4_bf16", k=8192) == (4, 256)    # W4A16, per-row scales
+    assert sel(1, 32768, 8192, 16, 4, 32, 128, "int4_bf16", k=8192) == (8, 128)
+    assert sel(1, 32768, 8192, 16, 4, 16, 128, "int4_bf16", k=8192)[0] == 1     # not for 16-row blocks
     assert sel(1, 32768, 8192, 16, 4, 64, 128, "int4", k=8192) == (4, 128)    # int4 from inter_dim 4096
     assert sel(2, 32768, 8192, 16, 4, 64, 256, "int4", k=8192) == (4, 256)
     assert sel(1, 32768, 2048, 16, 4, 64, 128, "int4", k=8192) == (2, 64)
