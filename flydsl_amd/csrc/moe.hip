@@ -47,7 +47,7 @@ MoeKernel moe_stage1_tile(int tm, int r, int tn) {
 }
 
 // Stage 1 of fp8, int8 (int8smooth included), int4 weights with int8 activations (W4A8), bf16
-// and fp16 runs the stream kernel (moe_stream.h) for every routing: DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256),
+// and fp16 runs the stream kernel (moe_stream.h) for every routing but large experts (moe_tiles): DS-TP8 dims (128 experts, model_dim 7168, inter_dim 256),
 // fp8, graph-timed against the kernels it replaced (64-column single-block tiles for 64-row
 // blocks, 128-row run tiles with weights in LDS for 16- and 32-row blocks), bit-equal outputs:
 // 64-row blocks 2048 / 4096 / 8192 / 16384 tokens 134 / 181 / 298 / 527 us against 160 / 216 /
